@@ -1,0 +1,215 @@
+/*
+ * joyomni_hip.h — C ABI of the MI355X (gfx950) joyomni_ops kernel library.
+ *
+ * libjoyomni_hip.so exports these entry points. Every argument is a plain
+ * pointer, an integer or a float; no torch or HIP type appears, so the header
+ * can be bound from ctypes, cgo, JNI or N-API as easily as from C++.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor pointers are DEVICE pointers on the device that owns
+ *     `stream`; that device must be current on the calling thread.
+ *   - `stream` is a hipStream_t passed as void*; NULL selects the null stream.
+ *     Work is enqueued asynchronously on it. No entry point synchronizes,
+ *     allocates device memory or queries device properties after its first
+ *     call on a device, so all of them are safe inside HIP graph capture.
+ *   - Strides are in ELEMENTS of the tensor they describe. The innermost
+ *     dimension is always contiguous. A row stride of 0 broadcasts one row.
+ *   - Element types are selected with JO_DTYPE_*; fp8 outputs are OCP
+ *     float8 e4m3fn bytes (the format of torch.float8_e4m3fn).
+ *   - The return value is a status: JO_OK (0) or a JO_ERR_* code. On error
+ *     nothing is enqueued (validation errors) or the launch failed
+ *     (JO_ERR_HIP); jo_last_error() returns a message for the calling thread.
+ *
+ * Which reference function each entry point replaces is given in its comment
+ * as path:line into jd-opensource/JoyAI-Video-Edit.
+ */
+#ifndef JOYOMNI_HIP_H
+#define JOYOMNI_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JO_ABI_VERSION 1
+
+/* Status codes. */
+#define JO_OK 0
+#define JO_ERR_INVALID 1     /* bad pointer, shape, stride, alignment or enum   */
+#define JO_ERR_UNSUPPORTED 2 /* valid request this build has no kernel for      */
+#define JO_ERR_HIP 3         /* the HIP runtime reported an error at launch     */
+
+/* Element types of bf16/fp16/fp32 tensors. */
+#define JO_DTYPE_F32 0
+#define JO_DTYPE_F16 1
+#define JO_DTYPE_BF16 2
+
+/* norm_type values; the integers are the reference's own
+ * (deploy/joyomni_ops/csrc/fused_norm_scale_shift.cu:25,
+ *  deploy/joyomni_ops/joyomni_ops/__init__.py:38-41). */
+#define JO_NORM_LAYER 0
+#define JO_NORM_RMS 1
+
+/* Message describing the last error on the calling thread ("" if none). */
+const char* jo_last_error(void);
+
+/* JO_ABI_VERSION of the loaded library. */
+int jo_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Per-token FP8 e4m3 quantization.
+ * Replaces joyomni_ops::sgl_per_token_quant_fp8
+ *   (deploy/joyomni_ops/csrc/per_token_quant_fp8.cu:148-176; kernel :43-83).
+ * For each row r:  s[r] = max_j |x[r,j]| / 448  (IEEE fp32 division),
+ *   inv = (s[r] == 0) ? 0 : 1 / s[r],
+ *   q[r,j] = e4m3fn_rne(min(max(x[r,j] * inv, -448), 448)).
+ * NaN inputs are ignored by the max and quantize to +448, as in the reference.
+ * input: [num_tokens, hidden_dim] bf16 or fp16 (dtype), row stride in_stride.
+ * output_q: fp8 bytes, row stride q_stride. output_s: fp32 [num_tokens].
+ * hidden_dim % 4 == 0 (the reference's requirement).
+ * ------------------------------------------------------------------------ */
+int jo_sgl_per_token_quant_fp8(const void* input, int dtype, int64_t num_tokens,
+                               int64_t hidden_dim, int64_t in_stride, void* output_q,
+                               int64_t q_stride, float* output_s, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused per-head QK RMSNorm + interleaved-pair RoPE from bf16 cos/sin tables,
+ * in place on q and k.
+ * Replaces joyomni_ops::fused_qk_norm_rope_3d_paired
+ *   (deploy/joyomni_ops/csrc/fused_qknorm_rope_3d_kernel.cu:179-208;
+ *    kernel :56-143, launch :145-175).
+ * For every head vector x (head_dim elements) of q (weight q_weight) and of
+ * k (weight k_weight) at sequence position n:
+ *   r = 1/sqrt(sum(x^2)/head_dim + eps);  e_d = x_d * (r * w_d)
+ *   (e_2i, e_2i+1) <- (e_2i c - e_2i+1 s, e_2i s + e_2i+1 c),
+ *   c = cos[n, i], s = sin[n, i]; one bf16 rounding at the end.
+ * q, k: bf16 [batch, seq_len, num_heads, head_dim] with the given batch and
+ * token strides; heads of a token are contiguous (head stride head_dim).
+ * q_weight, k_weight: bf16 [head_dim]. cos, sin: bf16 [seq_len, head_dim/2]
+ * contiguous. head_dim in {64, 128, 256}.
+ * ------------------------------------------------------------------------ */
+int jo_fused_qk_norm_rope_3d_paired(void* q, void* k, int64_t batch, int64_t seq_len,
+                                    int64_t num_heads, int64_t head_dim,
+                                    int64_t q_batch_stride, int64_t q_token_stride,
+                                    int64_t k_batch_stride, int64_t k_token_stride, float eps,
+                                    const void* q_weight, const void* k_weight,
+                                    const void* cos, const void* sin, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Same normalization and rotation as jo_fused_qk_norm_rope_3d_paired, with
+ * the rotation angles computed in registers from the token's 3D grid
+ * position instead of read from [seq_len, head_dim/2] tables.
+ * No reference counterpart with this signature: it computes what the
+ * reference's table builders feed the paired kernel
+ *   (deploy/xvideo/models/dit/rope.py:31-52, dit.py:745-783 for the 3D
+ *    angles, dit.py:785-809,918-933 for the source-id rotation).
+ * Token n of the sequence sits in frame f = n / (grid_h*grid_w) at
+ *   t = t0 + f,  h = (n % (grid_h*grid_w)) / grid_w,  w = n % grid_w.
+ * Pair i (0 <= i < head_dim/2) uses axis t for i < pairs_t, h for
+ * i < pairs_t + pairs_h, w otherwise; its angle is pos_axis * freqs[i]
+ * (fp32 product). If source_id != 0 the pair is further rotated by
+ * source_id * freqs[head_dim/2 + i] by angle addition.
+ * freqs: device fp32 [2, head_dim/2] (axis frequencies, source-id
+ * frequencies); the second row is read only when source_id != 0.
+ * ------------------------------------------------------------------------ */
+int jo_fused_qk_norm_rope_3d_grid(void* q, void* k, int64_t batch, int64_t seq_len,
+                                  int64_t num_heads, int64_t head_dim,
+                                  int64_t q_batch_stride, int64_t q_token_stride,
+                                  int64_t k_batch_stride, int64_t k_token_stride, float eps,
+                                  const void* q_weight, const void* k_weight,
+                                  const float* freqs, int32_t pairs_t, int32_t pairs_h,
+                                  int32_t grid_h, int32_t grid_w, int32_t t0,
+                                  float source_id, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Grid-mode QK norm + RoPE that writes the rotated K straight into a frame
+ * ring buffer: q is updated in place, k is only read, and the rotated head
+ * vectors of k for frame f go to cache frame slot (slot_start + f) % cache_slots,
+ * i.e. cache token ((slot_start + f) % cache_slots) * grid_h*grid_w + (n % (grid_h*grid_w)).
+ * No reference counterpart: it fuses the reference's pre-RoPE K staging and
+ * RoPE-at-commit pool write
+ *   (deploy/xvideo/serving/graph_runner.py:49-60,137-142; dit.py:360-363).
+ * k_cache: bf16 [batch, cache_slots*grid_h*grid_w, num_heads, head_dim] with
+ * the given batch and token strides.
+ * ------------------------------------------------------------------------ */
+int jo_fused_qk_norm_rope_3d_kvcache(void* q, const void* k, void* k_cache, int64_t batch,
+                                     int64_t seq_len, int64_t num_heads, int64_t head_dim,
+                                     int64_t q_batch_stride, int64_t q_token_stride,
+                                     int64_t k_batch_stride, int64_t k_token_stride,
+                                     int64_t cache_batch_stride, int64_t cache_token_stride,
+                                     int64_t cache_slots, int64_t slot_start, float eps,
+                                     const void* q_weight, const void* k_weight,
+                                     const float* freqs, int32_t pairs_t, int32_t pairs_h,
+                                     int32_t grid_h, int32_t grid_w, int32_t t0,
+                                     float source_id, void* stream);
+
+/* ------------------------------------------------------------------------
+ * (Layer|RMS)Norm + AdaLN modulation.
+ * Replaces joyomni_ops::fused_norm_scale_shift
+ *   (deploy/joyomni_ops/csrc/fused_norm_scale_shift.cu:172-209; kernel :70-143).
+ *   LN:  y = ((x - mu) * r * g + b) * (1 + scale) + shift,  r = 1/sqrt(var + eps)
+ *   RMS: y = (x * r * g) * (1 + scale) + shift,            r = 1/sqrt(mean(x^2) + eps)
+ * with fp32 arithmetic and one rounding to dtype. g = gamma (1 if NULL);
+ * b = beta, used only by LN and only when gamma is given (0 otherwise), as in
+ * the reference. x, y: [M, N] with row strides; scale, shift: [M, N] with row
+ * strides (0 broadcasts a single [N] row to every row). N % 4 == 0.
+ * ------------------------------------------------------------------------ */
+int jo_fused_norm_scale_shift(const void* x, int64_t x_stride, const void* gamma,
+                              const void* beta, const void* scale, int64_t scale_stride,
+                              const void* shift, int64_t shift_stride, void* y,
+                              int64_t y_stride, int64_t M, int64_t N, int dtype,
+                              int norm_type, float eps, void* stream);
+
+/* ------------------------------------------------------------------------
+ * RMSNorm: out = (x * r) * w, r = 1/sqrt(mean(x^2) + eps), fp32 arithmetic.
+ * Replaces joyomni_ops::rmsnorm (deploy/joyomni_ops/csrc/rmsnorm.cu:76-95;
+ * kernel :37-61). x, out: [M, N] with row strides; weight: [N]. Any N >= 1.
+ * ------------------------------------------------------------------------ */
+int jo_rmsnorm(const void* x, int64_t x_stride, const void* weight, void* out,
+               int64_t out_stride, int64_t M, int64_t N, int dtype, float eps,
+               void* stream);
+
+/* ------------------------------------------------------------------------
+ * Residual add (optionally gated) + LayerNorm + AdaLN modulation, one pass:
+ *   residual <- round(residual + x * gate)        (gate = 1 if NULL)
+ *   y = LN(residual)(g, b) * (1 + scale) + shift  on the ROUNDED residual.
+ * No reference counterpart: it fuses fused_add_gate / torch.addcmul
+ *   (deploy/xvideo/models/dit/sgl_fused_ops.py:114-117) with the
+ * fused_norm_scale_shift LayerNorm path (fused_norm_scale_shift.cu:88-142) as
+ * the DiT block uses them back to back (dit.py:447-476).
+ * x: [M, N]; residual: [M, N], updated in place; y: [M, N];
+ * gate, scale, shift: [M, N] row-strided, stride 0 = one [N] row for all.
+ * gamma/beta as in jo_fused_norm_scale_shift. N % 4 == 0.
+ * ------------------------------------------------------------------------ */
+int jo_fused_add_layernorm_scale_shift(const void* x, int64_t x_stride, void* residual,
+                                       int64_t res_stride, const void* gate,
+                                       int64_t gate_stride, const void* gamma,
+                                       const void* beta, const void* scale,
+                                       int64_t scale_stride, const void* shift,
+                                       int64_t shift_stride, void* y, int64_t y_stride,
+                                       int64_t M, int64_t N, int dtype, float eps,
+                                       void* stream);
+
+/* ------------------------------------------------------------------------
+ * RMSNorm with an FP8 e4m3 quantization epilogue.
+ *   v = (x * r) * w  in fp32 (never rounded to dtype), r as in jo_rmsnorm;
+ *   group_size == 0:   one scale per row,       s: fp32 [M]
+ *   group_size == 128: one scale per 1x128 block, s: fp32 [M, N/128] row-major
+ *   s = amax(|v| over the group) / 448; q = e4m3fn_rne(clamp(v * inv, +-448)),
+ *   inv = (s == 0) ? 0 : 1/s  — the per_token_quant_fp8 rule applied to v.
+ * No reference counterpart: it fuses rmsnorm (rmsnorm.cu:41-60) with the
+ * quantization of per_token_quant_fp8.cu:56-82 that Fp8Linear runs next
+ * (deploy/xvideo/models/dit/fp8_linear.py:138-169).
+ * x: [M, N] row-strided; out_q: fp8 [M, N] row stride q_stride.
+ * N % 8 == 0, and N % 128 == 0 for group_size 128.
+ * ------------------------------------------------------------------------ */
+int jo_rmsnorm_quant_fp8(const void* x, int64_t x_stride, const void* weight, void* out_q,
+                         int64_t q_stride, float* out_s, int64_t M, int64_t N, int dtype,
+                         float eps, int64_t group_size, void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif /* JOYOMNI_HIP_H */

@@ -1,0 +1,250 @@
+// Device-side building blocks shared by the joyomni gfx950 kernels.
+//
+// Everything here is written for CDNA4 wave64: 16-byte global accesses,
+// cross-lane reductions with DPP row operations (within 16-lane rows),
+// ds_swizzle (across the two rows of a 32-lane half) and readlane (across
+// the two halves), and the gfx950 conversion instructions for bf16
+// (v_cvt_pk_bf16_f32, round-to-nearest-even) and OCP fp8 e4m3fn
+// (v_cvt_pk_fp8_f32, round-to-nearest-even).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace jo {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;  // threads per workgroup for every row kernel
+constexpr float kFp8Max = 448.0f;
+
+// ---------------------------------------------------------------------------
+// Element types. kVec = elements carried by one 16-byte chunk.
+// ---------------------------------------------------------------------------
+struct BF16 {
+  static constexpr int kVec = 8;
+  static constexpr int kBytes = 2;
+};
+struct F16 {
+  static constexpr int kVec = 8;
+  static constexpr int kBytes = 2;
+};
+struct F32 {
+  static constexpr int kVec = 4;
+  static constexpr int kBytes = 4;
+};
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) {
+  return __builtin_bit_cast(float, w & 0xffff0000u);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+__device__ __forceinline__ f32x2 unpack_f16x2(uint32_t w) {
+  return __builtin_convertvector(__builtin_bit_cast(f16x2, w), f32x2);
+}
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
+// One element of a 16-byte chunk as fp32.
+template <class Tag>
+__device__ __forceinline__ float elem(const u32x4& c, int j);
+
+template <>
+__device__ __forceinline__ float elem<BF16>(const u32x4& c, int j) {
+  const uint32_t w = c[j >> 1];
+  return (j & 1) ? bf16_hi(w) : bf16_lo(w);
+}
+template <>
+__device__ __forceinline__ float elem<F16>(const u32x4& c, int j) {
+  const f32x2 v = unpack_f16x2(c[j >> 1]);
+  return (j & 1) ? v.y : v.x;
+}
+template <>
+__device__ __forceinline__ float elem<F32>(const u32x4& c, int j) {
+  return __builtin_bit_cast(float, c[j]);
+}
+
+// All kVec elements of a chunk as fp32.
+template <class Tag>
+__device__ __forceinline__ void unpack(const u32x4& c, float (&f)[Tag::kVec]) {
+#pragma unroll
+  for (int j = 0; j < Tag::kVec; ++j) f[j] = elem<Tag>(c, j);
+}
+
+// kVec fp32 values rounded (nearest-even) into one 16-byte chunk.
+template <class Tag>
+__device__ __forceinline__ u32x4 pack(const float (&f)[Tag::kVec]);
+
+template <>
+__device__ __forceinline__ u32x4 pack<BF16>(const float (&f)[8]) {
+  return u32x4{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+               pack_bf16x2(f[6], f[7])};
+}
+template <>
+__device__ __forceinline__ u32x4 pack<F16>(const float (&f)[8]) {
+  return u32x4{pack_f16x2(f[0], f[1]), pack_f16x2(f[2], f[3]), pack_f16x2(f[4], f[5]),
+               pack_f16x2(f[6], f[7])};
+}
+template <>
+__device__ __forceinline__ u32x4 pack<F32>(const float (&f)[4]) {
+  return u32x4{__builtin_bit_cast(uint32_t, f[0]), __builtin_bit_cast(uint32_t, f[1]),
+               __builtin_bit_cast(uint32_t, f[2]), __builtin_bit_cast(uint32_t, f[3])};
+}
+
+// Scalar element load / store (generic fallback kernels).
+template <class Tag>
+__device__ __forceinline__ float load_elem(const void* p, int64_t i);
+template <>
+__device__ __forceinline__ float load_elem<BF16>(const void* p, int64_t i) {
+  return __builtin_bit_cast(float, uint32_t(static_cast<const uint16_t*>(p)[i]) << 16);
+}
+template <>
+__device__ __forceinline__ float load_elem<F16>(const void* p, int64_t i) {
+  return float(static_cast<const _Float16*>(p)[i]);
+}
+template <>
+__device__ __forceinline__ float load_elem<F32>(const void* p, int64_t i) {
+  return static_cast<const float*>(p)[i];
+}
+template <class Tag>
+__device__ __forceinline__ void store_elem(void* p, int64_t i, float v);
+template <>
+__device__ __forceinline__ void store_elem<BF16>(void* p, int64_t i, float v) {
+  static_cast<__bf16*>(p)[i] = __bf16(v);
+}
+template <>
+__device__ __forceinline__ void store_elem<F16>(void* p, int64_t i, float v) {
+  static_cast<_Float16*>(p)[i] = _Float16(v);
+}
+template <>
+__device__ __forceinline__ void store_elem<F32>(void* p, int64_t i, float v) {
+  static_cast<float*>(p)[i] = v;
+}
+
+// ---------------------------------------------------------------------------
+// 16-byte global accesses.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *static_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, const u32x4& v) { *static_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ void st8(void* p, const u32x2& v) { *static_cast<u32x2*>(p) = v; }
+
+__device__ __forceinline__ const void* byte_off(const void* p, int64_t bytes) {
+  return static_cast<const char*>(p) + bytes;
+}
+__device__ __forceinline__ void* byte_off(void* p, int64_t bytes) {
+  return static_cast<char*>(p) + bytes;
+}
+
+// ---------------------------------------------------------------------------
+// FP8 e4m3fn.
+// The clamp reproduces fmaxf(fminf(v, 448), -448): a NaN becomes +448.
+// v_cvt_pk_fp8_f32 rounds to nearest-even; the clamp keeps every input in the
+// finite range, so the result equals a saturating conversion.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float fp8_clamp(float v) { return fmaxf(fminf(v, kFp8Max), -kFp8Max); }
+
+// Four clamped values -> four e4m3fn bytes (element 0 in the lowest byte).
+__device__ __forceinline__ uint32_t fp8x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(a), fp8_clamp(b), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(c), fp8_clamp(d), w, true);
+  return static_cast<uint32_t>(w);
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane reductions.
+// allreduce<W>(v) combines v over aligned groups of W consecutive lanes
+// (W in {8, 16, 32, 64}) and returns the result in every lane of the group.
+// Every lane of a group ends with bit-identical values: each step combines a
+// lane with a partner holding the mirror partial, and + / max commute.
+// ---------------------------------------------------------------------------
+struct OpSum {
+  __device__ __forceinline__ static float apply(float a, float b) { return a + b; }
+};
+struct OpMax {
+  __device__ __forceinline__ static float apply(float a, float b) { return fmaxf(a, b); }
+};
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               kCtrl, 0xf, 0xf, false));
+}
+// DPP controls (gfx9 encoding).
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppRor4 = 0x124;       // row_ror:4
+constexpr int kDppRor8 = 0x128;       // row_ror:8
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror
+
+__device__ __forceinline__ float swizzle_xor16(float v) {
+  // ds_swizzle bit mode: and_mask 0x1f, or_mask 0, xor_mask 0x10.
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401f));
+}
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+template <int W, class Op>
+__device__ __forceinline__ float allreduce(float v) {
+  static_assert(W == 8 || W == 16 || W == 32 || W == 64, "group width");
+  if constexpr (W == 8) {
+    v = Op::apply(v, dpp<kDppHalfMirror>(v));
+  } else {
+    v = Op::apply(v, dpp<kDppRor8>(v));
+    v = Op::apply(v, dpp<kDppRor4>(v));
+  }
+  v = Op::apply(v, dpp<kDppXor2>(v));
+  v = Op::apply(v, dpp<kDppXor1>(v));
+  if constexpr (W >= 32) v = Op::apply(v, swizzle_xor16(v));
+  if constexpr (W == 64) v = Op::apply(readlane(v, 0), readlane(v, 32));
+  return v;
+}
+
+// Reduction over LPR lanes of a 256-thread block (LPR in {8..256}). Groups
+// wider than a wave exchange per-wave partials through LDS; `slot` is a
+// __shared__ float[4] scratch owned by the caller (one per reduction in
+// flight). All threads of the block must call it (it may hit a barrier).
+template <int LPR, class Op>
+__device__ __forceinline__ float row_reduce(float v, float* slot) {
+  if constexpr (LPR <= kWave) {
+    return allreduce<LPR, Op>(v);
+  } else {
+    static_assert(LPR == 128 || LPR == 256, "lanes per row");
+    v = allreduce<kWave, Op>(v);
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) slot[wave] = v;
+    __syncthreads();
+    constexpr int kWavesPerRow = LPR / kWave;
+    const int first = (wave / kWavesPerRow) * kWavesPerRow;
+    float r = slot[first];
+#pragma unroll
+    for (int i = 1; i < kWavesPerRow; ++i) r = Op::apply(r, slot[first + i]);
+    return r;
+  }
+}
+
+// Block-wide reduction for the generic (one row per block) kernels.
+template <class Op>
+__device__ __forceinline__ float block_reduce(float v, float* slot) {
+  v = allreduce<kWave, Op>(v);
+  const int wave = threadIdx.x / kWave;
+  __syncthreads();  // slot may still be read by a previous reduction
+  if ((threadIdx.x & (kWave - 1)) == 0) slot[wave] = v;
+  __syncthreads();
+  float r = slot[0];
+#pragma unroll
+  for (int i = 1; i < kBlock / kWave; ++i) r = Op::apply(r, slot[i]);
+  return r;
+}
+
+}  // namespace jo

@@ -1,0 +1,72 @@
+// Host-side helpers for the C ABI: per-thread error messages, argument
+// validation and the row-shape dispatch shared by every row kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "joyomni_hip.h"
+
+namespace jo {
+
+// Records a printf-style message as the calling thread's last error.
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+// Converts the launch status of the kernel just enqueued into a JO_ status.
+int launch_status(const char* op);
+
+#define JO_REQUIRE(cond, ...)      \
+  do {                             \
+    if (!(cond)) {                 \
+      ::jo::set_error(__VA_ARGS__); \
+      return JO_ERR_INVALID;       \
+    }                              \
+  } while (0)
+
+inline bool aligned(const void* p, int64_t bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes)) == 0;
+}
+
+// Number of row-kernel workgroups needed for M rows at LPR lanes per row.
+inline int64_t row_blocks(int64_t M, int lpr) {
+  const int64_t rows_per_block = 256 / lpr;
+  return (M + rows_per_block - 1) / rows_per_block;
+}
+
+// Row shapes. A row of N elements is split into 16-byte chunks of kVec
+// elements; LPR lanes share a row and each lane holds CH chunks. The
+// dispatcher picks the smallest shape that covers N and calls
+// fn(std::integral_constant<int, LPR>, std::integral_constant<int, CH>).
+// Returns false when N exceeds the largest shape (the caller then uses its
+// generic kernel).
+template <int V, class Fn>
+bool dispatch_row_shape(int64_t N, Fn&& fn) {
+  using std::integral_constant;
+  const int64_t chunks = (N + V - 1) / V;
+  if (chunks <= 8) { fn(integral_constant<int, 8>{}, integral_constant<int, 1>{}); return true; }
+  if (chunks <= 16) { fn(integral_constant<int, 16>{}, integral_constant<int, 1>{}); return true; }
+  if (chunks <= 32) { fn(integral_constant<int, 32>{}, integral_constant<int, 1>{}); return true; }
+  if (chunks <= 64 * 1) { fn(integral_constant<int, 64>{}, integral_constant<int, 1>{}); return true; }
+  if (chunks <= 64 * 2) { fn(integral_constant<int, 64>{}, integral_constant<int, 2>{}); return true; }
+  if (chunks <= 64 * 3) { fn(integral_constant<int, 64>{}, integral_constant<int, 3>{}); return true; }
+  if (chunks <= 64 * 4) { fn(integral_constant<int, 64>{}, integral_constant<int, 4>{}); return true; }
+  if (chunks <= 64 * 6) { fn(integral_constant<int, 64>{}, integral_constant<int, 6>{}); return true; }
+  if (chunks <= 64 * 8) { fn(integral_constant<int, 64>{}, integral_constant<int, 8>{}); return true; }
+  if (chunks <= 64 * 12) { fn(integral_constant<int, 64>{}, integral_constant<int, 12>{}); return true; }
+  if (chunks <= 64 * 16) { fn(integral_constant<int, 64>{}, integral_constant<int, 16>{}); return true; }
+  if (chunks <= 256 * 8) { fn(integral_constant<int, 256>{}, integral_constant<int, 8>{}); return true; }
+  if (chunks <= 256 * 12) { fn(integral_constant<int, 256>{}, integral_constant<int, 12>{}); return true; }
+  if (chunks <= 256 * 16) { fn(integral_constant<int, 256>{}, integral_constant<int, 16>{}); return true; }
+  return false;
+}
+
+inline int dtype_bytes(int dtype) { return dtype == JO_DTYPE_F32 ? 4 : 2; }
+
+inline bool valid_dtype(int dtype) {
+  return dtype == JO_DTYPE_F32 || dtype == JO_DTYPE_F16 || dtype == JO_DTYPE_BF16;
+}
+
+}  // namespace jo

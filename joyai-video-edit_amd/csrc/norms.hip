@@ -1,0 +1,388 @@
+// LayerNorm / RMSNorm with AdaLN modulation, standalone RMSNorm, and the
+// fused (gated) residual add + LayerNorm + AdaLN.
+//
+// Row kernels: LPR lanes per row, CH 16-byte chunks per lane held in
+// registers, so x (and the residual) are read from HBM once and y (and the
+// residual) written once. LayerNorm statistics are two-pass from registers
+// (mean, then the sum of squared deviations), like the reference. Row sums
+// reduce with DPP / swizzle / readlane, through LDS only across waves.
+#include "jo_device.hpp"
+#include "jo_host.hpp"
+
+namespace jo {
+namespace {
+
+struct NormArgs {
+  const void* x;
+  int64_t xs;
+  void* res;  // residual (add kernel only), updated in place
+  int64_t rs;
+  const void* gate;  // optional gate of the residual update
+  int64_t gs;
+  const void* gamma;  // optional, [N]
+  const void* beta;   // optional, [N]; applied only with gamma
+  const void* scale;
+  int64_t scs;  // 0 = one row for all rows
+  const void* shift;
+  int64_t shs;
+  void* y;
+  int64_t ys;
+  int64_t M;
+  int N;
+  float eps;
+};
+
+constexpr int kLayer = JO_NORM_LAYER;
+constexpr int kRms = JO_NORM_RMS;
+
+// residual + x * gate as torch.addcmul evaluates it: the product and the sum
+// are two separately rounded fp32 operations (no fused multiply-add).
+__device__ __forceinline__ float residual_update(float res, float x, float gate, bool gated) {
+#pragma clang fp contract(off)
+  return gated ? res + x * gate : res + x;
+}
+
+template <class Tag>
+__device__ __forceinline__ u32x4 ld_chunk(const void* base, int64_t row_elems, int e) {
+  return ld16(byte_off(base, (row_elems + e) * Tag::kBytes));
+}
+
+// ---------------------------------------------------------------------------
+// y = Norm(v)(gamma, beta) * (1 + scale) + shift, follows
+// fused_norm_scale_shift.cu:88-142. With ADD, v is first formed as
+// round(res + x * gate) and written back to res (sgl_fused_ops.py:114-117).
+// ---------------------------------------------------------------------------
+template <class Tag, int LPR, int CH, int NT, bool ADD>
+__global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
+  constexpr int V = Tag::kVec;
+  constexpr int RPB = kBlock / LPR;
+  __shared__ float red_a[kBlock / kWave];
+  __shared__ float red_b[kBlock / kWave];
+  const int lane = threadIdx.x % LPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
+  const bool row_ok = row < a.M;
+  const int N = a.N;
+
+  u32x4 c[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * V;
+    c[i] = (row_ok && e < N) ? ld_chunk<Tag>(a.x, row * a.xs, e) : u32x4{0u, 0u, 0u, 0u};
+  }
+  if constexpr (ADD) {
+    u32x4 rc[CH];
+    u32x4 gc[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int e = (i * LPR + lane) * V;
+      const bool ok = row_ok && e < N;
+      rc[i] = ok ? ld_chunk<Tag>(a.res, row * a.rs, e) : u32x4{0u, 0u, 0u, 0u};
+      gc[i] = (ok && a.gate) ? ld_chunk<Tag>(a.gate, row * a.gs, e) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int e = (i * LPR + lane) * V;
+      float u[V];
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        u[j] = residual_update(elem<Tag>(rc[i], j), elem<Tag>(c[i], j), elem<Tag>(gc[i], j),
+                               a.gate != nullptr);
+      c[i] = pack<Tag>(u);  // the rounded residual is what gets normalized
+      if (row_ok && e < N) st16(byte_off(a.res, (row * a.rs + e) * Tag::kBytes), c[i]);
+    }
+  }
+
+  // Statistics.
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const float v = elem<Tag>(c[i], j);
+      if constexpr (NT == kLayer)
+        sum += v;
+      else
+        sum += v * v;
+    }
+  }
+  sum = row_reduce<LPR, OpSum>(sum, red_a);
+  const float nf = static_cast<float>(N);
+  float mean = 0.f;
+  float r;
+  if constexpr (NT == kLayer) {
+    mean = sum / nf;
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int e = (i * LPR + lane) * V;
+      if (e < N) {
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const float t = elem<Tag>(c[i], j) - mean;
+          ss += t * t;
+        }
+      }
+    }
+    ss = row_reduce<LPR, OpSum>(ss, red_b);
+    r = 1.0f / sqrtf(ss / nf + a.eps);
+  } else {
+    r = 1.0f / sqrtf(sum / nf + a.eps);
+  }
+
+  // Output.
+  const bool affine = a.gamma != nullptr;
+  const bool has_beta = affine && a.beta != nullptr && NT == kLayer;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * V;
+    if (!(row_ok && e < N)) continue;
+    const u32x4 sc = ld_chunk<Tag>(a.scale, row * a.scs, e);
+    const u32x4 sh = ld_chunk<Tag>(a.shift, row * a.shs, e);
+    u32x4 gm = u32x4{0u, 0u, 0u, 0u}, bt = u32x4{0u, 0u, 0u, 0u};
+    if (affine) gm = ld_chunk<Tag>(a.gamma, 0, e);
+    if (has_beta) bt = ld_chunk<Tag>(a.beta, 0, e);
+    float o[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      float t = (NT == kLayer) ? (elem<Tag>(c[i], j) - mean) * r : elem<Tag>(c[i], j) * r;
+      if (affine) t = t * elem<Tag>(gm, j);
+      if (has_beta) t = t + elem<Tag>(bt, j);
+      o[j] = t * (1.f + elem<Tag>(sc, j)) + elem<Tag>(sh, j);
+    }
+    st16(byte_off(a.y, (row * a.ys + e) * Tag::kBytes), pack<Tag>(o));
+  }
+}
+
+// One row per workgroup with element-wise accesses (any N, any alignment).
+template <class Tag, int NT, bool ADD>
+__global__ __launch_bounds__(kBlock) void norm_mod_generic_kernel(const NormArgs a) {
+  __shared__ float red[kBlock / kWave];
+  const int64_t row = blockIdx.x;
+  const int N = a.N;
+  const int64_t xo = row * a.xs, ro = row * a.rs, go = row * a.gs;
+  const int64_t so = row * a.scs, ho = row * a.shs, yo = row * a.ys;
+  if constexpr (ADD) {
+    // Each thread later reads back exactly the elements it writes here.
+    for (int i = threadIdx.x; i < N; i += kBlock) {
+      const float xv = load_elem<Tag>(a.x, xo + i);
+      store_elem<Tag>(a.res, ro + i, residual_update(load_elem<Tag>(a.res, ro + i), xv,
+                                                     a.gate ? load_elem<Tag>(a.gate, go + i) : 1.f,
+                                                     a.gate != nullptr));
+    }
+  }
+  const void* src = ADD ? a.res : a.x;
+  const int64_t so_src = ADD ? ro : xo;
+  float sum = 0.f;
+  for (int i = threadIdx.x; i < N; i += kBlock) {
+    const float v = load_elem<Tag>(src, so_src + i);
+    sum += (NT == kLayer) ? v : v * v;
+  }
+  sum = block_reduce<OpSum>(sum, red);
+  const float nf = static_cast<float>(N);
+  float mean = 0.f, r;
+  if constexpr (NT == kLayer) {
+    mean = sum / nf;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < N; i += kBlock) {
+      const float t = load_elem<Tag>(src, so_src + i) - mean;
+      ss += t * t;
+    }
+    ss = block_reduce<OpSum>(ss, red);
+    r = 1.0f / sqrtf(ss / nf + a.eps);
+  } else {
+    r = 1.0f / sqrtf(sum / nf + a.eps);
+  }
+  const bool affine = a.gamma != nullptr;
+  const bool has_beta = affine && a.beta != nullptr && NT == kLayer;
+  for (int i = threadIdx.x; i < N; i += kBlock) {
+    const float v = load_elem<Tag>(src, so_src + i);
+    float t = (NT == kLayer) ? (v - mean) * r : v * r;
+    if (affine) t = t * load_elem<Tag>(a.gamma, i);
+    if (has_beta) t = t + load_elem<Tag>(a.beta, i);
+    store_elem<Tag>(a.y, yo + i,
+                    t * (1.f + load_elem<Tag>(a.scale, so + i)) + load_elem<Tag>(a.shift, ho + i));
+  }
+}
+
+template <class Tag, int NT, bool ADD>
+int launch_norm_mod(const NormArgs& a, hipStream_t stream, const char* op) {
+  const int b = Tag::kBytes;
+  bool vec_ok = (a.N % Tag::kVec == 0) && aligned(a.x, 16) && (a.xs * b) % 16 == 0 &&
+                aligned(a.y, 16) && (a.ys * b) % 16 == 0 && aligned(a.scale, 16) &&
+                (a.scs * b) % 16 == 0 && aligned(a.shift, 16) && (a.shs * b) % 16 == 0 &&
+                aligned(a.gamma, 16) && aligned(a.beta, 16);
+  if (ADD)
+    vec_ok = vec_ok && aligned(a.res, 16) && (a.rs * b) % 16 == 0 && aligned(a.gate, 16) &&
+             (a.gs * b) % 16 == 0;
+  bool launched = false;
+  if (vec_ok) {
+    launched = dispatch_row_shape<Tag::kVec>(a.N, [&](auto lpr, auto ch) {
+      constexpr int LPR = decltype(lpr)::value;
+      constexpr int CH = decltype(ch)::value;
+      hipLaunchKernelGGL((norm_mod_kernel<Tag, LPR, CH, NT, ADD>), dim3(row_blocks(a.M, LPR)),
+                         dim3(kBlock), 0, stream, a);
+    });
+  }
+  if (!launched)
+    hipLaunchKernelGGL((norm_mod_generic_kernel<Tag, NT, ADD>), dim3(a.M), dim3(kBlock), 0,
+                       stream, a);
+  return launch_status(op);
+}
+
+template <int NT, bool ADD>
+int launch_norm_mod_dt(int dtype, const NormArgs& a, hipStream_t stream, const char* op) {
+  switch (dtype) {
+    case JO_DTYPE_BF16: return launch_norm_mod<BF16, NT, ADD>(a, stream, op);
+    case JO_DTYPE_F16: return launch_norm_mod<F16, NT, ADD>(a, stream, op);
+    default: return launch_norm_mod<F32, NT, ADD>(a, stream, op);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm: out = (x * r) * w, follows rmsnorm.cu:41-60.
+// ---------------------------------------------------------------------------
+template <class Tag, int LPR, int CH>
+__global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const void* __restrict__ x, int64_t xs,
+                                                         const void* __restrict__ w,
+                                                         void* __restrict__ out, int64_t os,
+                                                         int64_t M, int N, float eps) {
+  constexpr int V = Tag::kVec;
+  constexpr int RPB = kBlock / LPR;
+  __shared__ float red[kBlock / kWave];
+  const int lane = threadIdx.x % LPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
+  const bool row_ok = row < M;
+  u32x4 c[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * V;
+    c[i] = (row_ok && e < N) ? ld_chunk<Tag>(x, row * xs, e) : u32x4{0u, 0u, 0u, 0u};
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const float v = elem<Tag>(c[i], j);
+      ss += v * v;
+    }
+  }
+  ss = row_reduce<LPR, OpSum>(ss, red);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(N) + eps);
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * V;
+    if (!(row_ok && e < N)) continue;
+    const u32x4 wc = ld_chunk<Tag>(w, 0, e);
+    float o[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) o[j] = (elem<Tag>(c[i], j) * r) * elem<Tag>(wc, j);
+    st16(byte_off(out, (row * os + e) * Tag::kBytes), pack<Tag>(o));
+  }
+}
+
+template <class Tag>
+__global__ __launch_bounds__(kBlock) void rmsnorm_generic_kernel(const void* __restrict__ x,
+                                                                 int64_t xs,
+                                                                 const void* __restrict__ w,
+                                                                 void* __restrict__ out,
+                                                                 int64_t os, int N, float eps) {
+  __shared__ float red[kBlock / kWave];
+  const int64_t row = blockIdx.x;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < N; i += kBlock) {
+    const float v = load_elem<Tag>(x, row * xs + i);
+    ss += v * v;
+  }
+  ss = block_reduce<OpSum>(ss, red);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(N) + eps);
+  for (int i = threadIdx.x; i < N; i += kBlock)
+    store_elem<Tag>(out, row * os + i, (load_elem<Tag>(x, row * xs + i) * r) * load_elem<Tag>(w, i));
+}
+
+template <class Tag>
+int launch_rmsnorm(const void* x, int64_t xs, const void* w, void* out, int64_t os, int64_t M,
+                   int64_t N, float eps, hipStream_t stream) {
+  const int b = Tag::kBytes;
+  const bool vec_ok = (N % Tag::kVec == 0) && aligned(x, 16) && (xs * b) % 16 == 0 &&
+                      aligned(w, 16) && aligned(out, 16) && (os * b) % 16 == 0;
+  bool launched = false;
+  if (vec_ok) {
+    launched = dispatch_row_shape<Tag::kVec>(N, [&](auto lpr, auto ch) {
+      constexpr int LPR = decltype(lpr)::value;
+      constexpr int CH = decltype(ch)::value;
+      hipLaunchKernelGGL((rmsnorm_kernel<Tag, LPR, CH>), dim3(row_blocks(M, LPR)), dim3(kBlock),
+                         0, stream, x, xs, w, out, os, M, static_cast<int>(N), eps);
+    });
+  }
+  if (!launched)
+    hipLaunchKernelGGL((rmsnorm_generic_kernel<Tag>), dim3(M), dim3(kBlock), 0, stream, x, xs, w,
+                       out, os, static_cast<int>(N), eps);
+  return launch_status("rmsnorm");
+}
+
+}  // namespace
+}  // namespace jo
+
+using namespace jo;
+
+extern "C" int jo_fused_norm_scale_shift(const void* x, int64_t x_stride, const void* gamma,
+                                         const void* beta, const void* scale,
+                                         int64_t scale_stride, const void* shift,
+                                         int64_t shift_stride, void* y, int64_t y_stride,
+                                         int64_t M, int64_t N, int dtype, int norm_type,
+                                         float eps, void* stream) {
+  // Checks of fused_norm_scale_shift.cu:176-196.
+  JO_REQUIRE(valid_dtype(dtype), "Unsupported dtype; use float32/float16/bfloat16");
+  JO_REQUIRE(norm_type == JO_NORM_LAYER || norm_type == JO_NORM_RMS,
+             "norm_type must be 0 (layer) or 1 (rms)");
+  JO_REQUIRE(M >= 0 && N >= 0 && N <= INT32_MAX, "fused_norm_scale_shift: bad shape");
+  JO_REQUIRE(N % 4 == 0, "N must be divisible by 4");
+  JO_REQUIRE(x_stride >= N && y_stride >= N && scale_stride >= 0 && shift_stride >= 0,
+             "fused_norm_scale_shift: bad row stride");
+  if (M == 0 || N == 0) return JO_OK;
+  JO_REQUIRE(x && y && scale && shift, "fused_norm_scale_shift: null pointer");
+  NormArgs a{x, x_stride, nullptr, 0, nullptr, 0, gamma, beta, scale, scale_stride, shift,
+             shift_stride, y, y_stride, M, static_cast<int>(N), eps};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (norm_type == JO_NORM_LAYER)
+    return launch_norm_mod_dt<kLayer, false>(dtype, a, st, "fused_norm_scale_shift");
+  return launch_norm_mod_dt<kRms, false>(dtype, a, st, "fused_norm_scale_shift");
+}
+
+extern "C" int jo_rmsnorm(const void* x, int64_t x_stride, const void* weight, void* out,
+                          int64_t out_stride, int64_t M, int64_t N, int dtype, float eps,
+                          void* stream) {
+  // Checks of rmsnorm.cu:77-81.
+  JO_REQUIRE(valid_dtype(dtype), "Unsupported dtype; use float32/float16/bfloat16");
+  JO_REQUIRE(M >= 0 && N >= 0 && N <= INT32_MAX, "rmsnorm: bad shape");
+  JO_REQUIRE(x_stride >= N && out_stride >= N, "rmsnorm: bad row stride");
+  if (M == 0 || N == 0) return JO_OK;
+  JO_REQUIRE(x && weight && out, "rmsnorm: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case JO_DTYPE_BF16: return launch_rmsnorm<BF16>(x, x_stride, weight, out, out_stride, M, N, eps, st);
+    case JO_DTYPE_F16: return launch_rmsnorm<F16>(x, x_stride, weight, out, out_stride, M, N, eps, st);
+    default: return launch_rmsnorm<F32>(x, x_stride, weight, out, out_stride, M, N, eps, st);
+  }
+}
+
+extern "C" int jo_fused_add_layernorm_scale_shift(
+    const void* x, int64_t x_stride, void* residual, int64_t res_stride, const void* gate,
+    int64_t gate_stride, const void* gamma, const void* beta, const void* scale,
+    int64_t scale_stride, const void* shift, int64_t shift_stride, void* y, int64_t y_stride,
+    int64_t M, int64_t N, int dtype, float eps, void* stream) {
+  JO_REQUIRE(valid_dtype(dtype), "Unsupported dtype; use float32/float16/bfloat16");
+  JO_REQUIRE(M >= 0 && N >= 0 && N <= INT32_MAX, "fused_add_layernorm_scale_shift: bad shape");
+  JO_REQUIRE(N % 4 == 0, "N must be divisible by 4");
+  JO_REQUIRE(x_stride >= N && res_stride >= N && y_stride >= N && scale_stride >= 0 &&
+                 shift_stride >= 0 && gate_stride >= 0,
+             "fused_add_layernorm_scale_shift: bad row stride");
+  if (M == 0 || N == 0) return JO_OK;
+  JO_REQUIRE(x && residual && y && scale && shift,
+             "fused_add_layernorm_scale_shift: null pointer");
+  NormArgs a{x, x_stride, residual, res_stride, gate, gate_stride, gamma, beta, scale,
+             scale_stride, shift, shift_stride, y, y_stride, M, static_cast<int>(N), eps};
+  return launch_norm_mod_dt<kLayer, true>(dtype, a, static_cast<hipStream_t>(stream),
+                                          "fused_add_layernorm_scale_shift");
+}

@@ -1,0 +1,277 @@
+// Per-token FP8 e4m3 quantization (drop-in for the reference's
+// sgl_per_token_quant_fp8) and the fused RMSNorm -> FP8 epilogue.
+//
+// Kernel shape: a row is split into 16-byte chunks; LPR lanes share a row and
+// each lane keeps its CH chunks in registers, so HBM is read exactly once and
+// written exactly once. The row maximum is reduced with DPP / swizzle /
+// readlane (and LDS only when a row spans several waves).
+#include "jo_device.hpp"
+#include "jo_host.hpp"
+
+namespace jo {
+namespace {
+
+// Quantizes 8 fp32 values with the reference's rule and returns 8 bytes.
+__device__ __forceinline__ u32x2 quant8(const float (&v)[8], float inv) {
+  return u32x2{fp8x4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv),
+               fp8x4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv)};
+}
+
+// ---------------------------------------------------------------------------
+// Per-token quantization: follows per_token_quant_fp8.cu:56-82.
+//   amax = max |x| (NaN ignored: fmaxf), scale = amax / 448 (IEEE division),
+//   inv = (scale == 0) ? 0 : 1 / scale, q = e4m3fn(clamp(x * inv, +-448)).
+// ---------------------------------------------------------------------------
+template <class Tag, int LPR, int CH>
+__global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restrict__ x, int64_t xs,
+                                                            uint8_t* __restrict__ q, int64_t qs,
+                                                            float* __restrict__ s, int64_t M, int N) {
+  static_assert(Tag::kVec == 8, "fp8 rows are built from 8-element chunks");
+  constexpr int RPB = kBlock / LPR;
+  __shared__ float red[kBlock / kWave];
+  const int lane = threadIdx.x % LPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
+  const bool row_ok = row < M;
+  const void* xr = byte_off(x, row * xs * Tag::kBytes);
+
+  u32x4 c[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * 8;
+    c[i] = (row_ok && e < N) ? ld16(byte_off(xr, static_cast<int64_t>(e) * Tag::kBytes))
+                             : u32x4{0u, 0u, 0u, 0u};
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(elem<Tag>(c[i], j)));
+  }
+  amax = row_reduce<LPR, OpMax>(amax, red);
+  const float scale = amax / kFp8Max;
+  if (row_ok && lane == 0) s[row] = scale;
+  const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;
+
+  uint8_t* qr = q + row * qs;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * 8;
+    if (row_ok && e < N) {
+      float v[8];
+      unpack<Tag>(c[i], v);
+      st8(qr + e, quant8(v, inv));
+    }
+  }
+}
+
+// One row per workgroup, element-wise accesses: any hidden size and any
+// alignment (rows whose size is not a multiple of 8, or unaligned views).
+template <class Tag>
+__global__ __launch_bounds__(kBlock) void quant_generic_kernel(const void* __restrict__ x,
+                                                               int64_t xs, uint8_t* __restrict__ q,
+                                                               int64_t qs, float* __restrict__ s,
+                                                               int N) {
+  __shared__ float red[kBlock / kWave];
+  const int64_t row = blockIdx.x;
+  const int64_t xo = row * xs;
+  float amax = 0.f;
+  for (int i = threadIdx.x; i < N; i += kBlock) amax = fmaxf(amax, fabsf(load_elem<Tag>(x, xo + i)));
+  amax = block_reduce<OpMax>(amax, red);
+  const float scale = amax / kFp8Max;
+  if (threadIdx.x == 0) s[row] = scale;
+  const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;
+  uint8_t* qr = q + row * qs;
+  for (int i = threadIdx.x; i < N; i += kBlock) {
+    const float v = fp8_clamp(load_elem<Tag>(x, xo + i) * inv);
+    qr[i] = static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.f, 0, false) & 0xff);
+  }
+}
+
+template <class Tag>
+int launch_quant(const void* x, int64_t M, int64_t N, int64_t xs, void* q, int64_t qs, float* s,
+                 hipStream_t stream) {
+  const bool vec_ok = (N % 8 == 0) && aligned(x, 16) && ((xs * Tag::kBytes) % 16 == 0) &&
+                      aligned(q, 8) && (qs % 8 == 0);
+  bool launched = false;
+  if (vec_ok) {
+    launched = dispatch_row_shape<8>(N, [&](auto lpr, auto ch) {
+      constexpr int LPR = decltype(lpr)::value;
+      constexpr int CH = decltype(ch)::value;
+      hipLaunchKernelGGL((quant_rows_kernel<Tag, LPR, CH>), dim3(row_blocks(M, LPR)), dim3(kBlock),
+                         0, stream, x, xs, static_cast<uint8_t*>(q), qs, s, M,
+                         static_cast<int>(N));
+    });
+  }
+  if (!launched) {
+    hipLaunchKernelGGL((quant_generic_kernel<Tag>), dim3(M), dim3(kBlock), 0, stream, x, xs,
+                       static_cast<uint8_t*>(q), qs, s, static_cast<int>(N));
+  }
+  return launch_status("sgl_per_token_quant_fp8");
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm -> FP8. v = (x * r) * w in fp32 (rmsnorm.cu:41-60 without the
+// rounding to the input type), r = 1/sqrt(sum(x^2)/N + eps) with IEEE sqrt
+// and division; then the per_token_quant_fp8.cu:56-82 rule over the row
+// (GROUP == 0) or over each 1x128 block (GROUP == 128, 16 lanes x 8 values).
+// ---------------------------------------------------------------------------
+template <class Tag, int LPR, int CH, int GROUP>
+__global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
+    const void* __restrict__ x, int64_t xs, const void* __restrict__ w, uint8_t* __restrict__ q,
+    int64_t qs, float* __restrict__ s, int64_t M, int N, float eps) {
+  static_assert(Tag::kVec == 8, "fp8 rows are built from 8-element chunks");
+  static_assert(GROUP == 0 || (GROUP == 128 && LPR >= 16), "group layout");
+  constexpr int RPB = kBlock / LPR;
+  __shared__ float red_ss[kBlock / kWave];
+  __shared__ float red_max[kBlock / kWave];
+  const int lane = threadIdx.x % LPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
+  const bool row_ok = row < M;
+  const void* xr = byte_off(x, row * xs * Tag::kBytes);
+
+  u32x4 c[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * 8;
+    c[i] = (row_ok && e < N) ? ld16(byte_off(xr, static_cast<int64_t>(e) * Tag::kBytes))
+                             : u32x4{0u, 0u, 0u, 0u};
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = elem<Tag>(c[i], j);
+      ss += v * v;
+    }
+  }
+  ss = row_reduce<LPR, OpSum>(ss, red_ss);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(N) + eps);
+
+  // v = (x * r) * w, kept in registers for the quantization pass.
+  float v[CH][8];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * 8;
+    u32x4 wc = u32x4{0u, 0u, 0u, 0u};
+    if (e < N) wc = ld16(byte_off(w, static_cast<int64_t>(e) * Tag::kBytes));
+    float gmax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[i][j] = (elem<Tag>(c[i], j) * r) * elem<Tag>(wc, j);
+      gmax = fmaxf(gmax, fabsf(v[i][j]));
+    }
+    if constexpr (GROUP == 128) {
+      // The 16 lanes of this DPP row hold one 128-element block.
+      gmax = allreduce<16, OpMax>(gmax);
+      const float gs = gmax / kFp8Max;
+      const float ginv = (gs == 0.f) ? 0.f : 1.0f / gs;
+      if (row_ok && e < N) {
+        if ((lane & 15) == 0) s[row * (N / 128) + e / 128] = gs;
+        st8(q + row * qs + e, quant8(v[i], ginv));
+      }
+    } else {
+      amax = fmaxf(amax, gmax);
+    }
+  }
+  if constexpr (GROUP == 0) {
+    amax = row_reduce<LPR, OpMax>(amax, red_max);
+    const float scale = amax / kFp8Max;
+    if (row_ok && lane == 0) s[row] = scale;
+    const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int e = (i * LPR + lane) * 8;
+      if (row_ok && e < N) st8(q + row * qs + e, quant8(v[i], inv));
+    }
+  }
+}
+
+template <class Tag>
+int launch_rmsnorm_quant(const void* x, int64_t xs, const void* w, void* q, int64_t qs, float* s,
+                         int64_t M, int64_t N, float eps, int64_t group, hipStream_t stream) {
+  bool launched = false;
+  if (group == 0) {
+    launched = dispatch_row_shape<8>(N, [&](auto lpr, auto ch) {
+      constexpr int LPR = decltype(lpr)::value;
+      constexpr int CH = decltype(ch)::value;
+      hipLaunchKernelGGL((rmsnorm_quant_kernel<Tag, LPR, CH, 0>), dim3(row_blocks(M, LPR)),
+                         dim3(kBlock), 0, stream, x, xs, w, static_cast<uint8_t*>(q), qs, s, M,
+                         static_cast<int>(N), eps);
+    });
+  } else {
+    launched = dispatch_row_shape<8>(N, [&](auto lpr, auto ch) {
+      constexpr int LPR = decltype(lpr)::value < 16 ? 16 : decltype(lpr)::value;
+      constexpr int CH = decltype(ch)::value;
+      hipLaunchKernelGGL((rmsnorm_quant_kernel<Tag, LPR, CH, 128>), dim3(row_blocks(M, LPR)),
+                         dim3(kBlock), 0, stream, x, xs, w, static_cast<uint8_t*>(q), qs, s, M,
+                         static_cast<int>(N), eps);
+    });
+  }
+  if (!launched) {
+    set_error("rmsnorm_quant_fp8: hidden size %lld exceeds the largest row shape (32768)",
+              static_cast<long long>(N));
+    return JO_ERR_UNSUPPORTED;
+  }
+  return launch_status("rmsnorm_quant_fp8");
+}
+
+}  // namespace
+}  // namespace jo
+
+using namespace jo;
+
+extern "C" int jo_sgl_per_token_quant_fp8(const void* input, int dtype, int64_t num_tokens,
+                                          int64_t hidden_dim, int64_t in_stride, void* output_q,
+                                          int64_t q_stride, float* output_s, void* stream) {
+  // Checks of per_token_quant_fp8.cu:149-156 and :168-175, plus the output
+  // checks the reference leaves out.
+  JO_REQUIRE(dtype == JO_DTYPE_BF16 || dtype == JO_DTYPE_F16,
+             "per_token_quant_fp8: input must be bf16 or fp16");
+  JO_REQUIRE(num_tokens >= 0 && hidden_dim >= 0, "per_token_quant_fp8: negative size");
+  JO_REQUIRE(hidden_dim % 4 == 0, "hidden_dim must be divisible by 4, got %lld",
+             static_cast<long long>(hidden_dim));
+  JO_REQUIRE(hidden_dim <= INT32_MAX, "per_token_quant_fp8: hidden_dim too large");
+  JO_REQUIRE(in_stride >= hidden_dim && q_stride >= hidden_dim,
+             "per_token_quant_fp8: row stride smaller than hidden_dim");
+  if (num_tokens == 0) return JO_OK;
+  JO_REQUIRE(input && output_q && output_s, "per_token_quant_fp8: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == JO_DTYPE_BF16)
+    return launch_quant<BF16>(input, num_tokens, hidden_dim, in_stride, output_q, q_stride,
+                              output_s, st);
+  return launch_quant<F16>(input, num_tokens, hidden_dim, in_stride, output_q, q_stride, output_s,
+                           st);
+}
+
+extern "C" int jo_rmsnorm_quant_fp8(const void* x, int64_t x_stride, const void* weight,
+                                    void* out_q, int64_t q_stride, float* out_s, int64_t M,
+                                    int64_t N, int dtype, float eps, int64_t group_size,
+                                    void* stream) {
+  JO_REQUIRE(dtype == JO_DTYPE_BF16 || dtype == JO_DTYPE_F16,
+             "rmsnorm_quant_fp8: x must be bf16 or fp16");
+  JO_REQUIRE(group_size == 0 || group_size == 128,
+             "rmsnorm_quant_fp8: group_size must be 0 (per token) or 128, got %lld",
+             static_cast<long long>(group_size));
+  JO_REQUIRE(M >= 0 && N > 0, "rmsnorm_quant_fp8: bad shape [%lld, %lld]",
+             static_cast<long long>(M), static_cast<long long>(N));
+  JO_REQUIRE(N % 8 == 0, "rmsnorm_quant_fp8: N must be divisible by 8, got %lld",
+             static_cast<long long>(N));
+  JO_REQUIRE(group_size == 0 || N % 128 == 0,
+             "rmsnorm_quant_fp8: N must be divisible by 128 for 1x128 blocks, got %lld",
+             static_cast<long long>(N));
+  JO_REQUIRE(x_stride >= N && q_stride >= N, "rmsnorm_quant_fp8: row stride smaller than N");
+  if (M == 0) return JO_OK;
+  JO_REQUIRE(x && weight && out_q && out_s, "rmsnorm_quant_fp8: null pointer");
+  JO_REQUIRE(aligned(x, 16) && (x_stride * 2) % 16 == 0 && aligned(weight, 16),
+             "rmsnorm_quant_fp8: x rows and weight must be 16-byte aligned");
+  JO_REQUIRE(aligned(out_q, 8) && q_stride % 8 == 0,
+             "rmsnorm_quant_fp8: output rows must be 8-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == JO_DTYPE_BF16)
+    return launch_rmsnorm_quant<BF16>(x, x_stride, weight, out_q, q_stride, out_s, M, N, eps,
+                                      group_size, st);
+  return launch_rmsnorm_quant<F16>(x, x_stride, weight, out_q, q_stride, out_s, M, N, eps,
+                                   group_size, st);
+}

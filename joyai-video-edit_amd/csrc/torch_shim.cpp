@@ -1,0 +1,406 @@
+// TORCH_LIBRARY(joyomni_ops) registration over the C ABI of libjoyomni_hip.so.
+//
+// The four reference ops keep their schema strings byte-for-byte
+// (deploy/joyomni_ops/csrc/pybind.cpp:35-43) and their TORCH_CHECKs
+// (fused_qknorm_rope_3d_kernel.cu:183-200, fused_norm_scale_shift.cu:176-196,
+// rmsnorm.cu:77-81, per_token_quant_fp8.cu:149-156), so
+// torch.ops.joyomni_ops.* behaves as the reference does for callers. The new
+// ops (grid RoPE, K ring-cache write, add+LayerNorm, RMSNorm->FP8) have their
+// own names. Tensors on ROCm carry the CUDA device type, so the impls are
+// registered on the CUDA dispatch key like the reference's. Every op runs
+// on the current stream of the tensor's device and never synchronizes.
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <torch/all.h>
+#include <torch/library.h>
+
+#include <vector>
+
+#include "joyomni_hip.h"
+
+namespace joyomni_ops {
+namespace {
+
+#define JO_CHECK_CUDA(x) TORCH_CHECK((x).is_cuda(), #x " must be a CUDA tensor")
+#define JO_CHECK_CONTIGUOUS(x) TORCH_CHECK((x).is_contiguous(), #x " must be contiguous")
+#define JO_CHECK_DTYPE(x, dt) \
+  TORCH_CHECK((x).scalar_type() == (dt), #x " dtype is ", (x).scalar_type(), ", expected ", (dt))
+#define JO_CHECK_INPUT(x, dt) \
+  JO_CHECK_CUDA(x);           \
+  JO_CHECK_CONTIGUOUS(x);     \
+  JO_CHECK_DTYPE(x, dt)
+
+void check_status(int status, const char* op) {
+  TORCH_CHECK(status == JO_OK, op, ": ", jo_last_error());
+}
+
+void* current_stream(const torch::Tensor& t) {
+  return static_cast<void*>(
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.get_device()).stream());
+}
+
+int dtype_code(const torch::Tensor& t) {
+  switch (t.scalar_type()) {
+    case torch::kFloat32: return JO_DTYPE_F32;
+    case torch::kFloat16: return JO_DTYPE_F16;
+    case torch::kBFloat16: return JO_DTYPE_BF16;
+    default: TORCH_CHECK(false, "Unsupported dtype; use float32/float16/bfloat16");
+  }
+  return -1;
+}
+
+// Row stride of a 2-D tensor whose last dim is contiguous; a size-1 leading
+// dim has no meaningful stride, report the row length instead.
+int64_t row_stride(const torch::Tensor& t) { return t.size(0) <= 1 ? t.size(1) : t.stride(0); }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Reference ops.
+// ---------------------------------------------------------------------------
+void fused_qk_norm_rope_3d_paired(torch::Tensor& q, torch::Tensor& k, int64_t seq_len,
+                                  int64_t num_heads, double eps, torch::Tensor& q_weight,
+                                  torch::Tensor& k_weight, torch::Tensor& cos,
+                                  torch::Tensor& sin) {
+  TORCH_CHECK(q.dim() == 3, "q must be 3D [batch, seq_len*num_heads, head_dim]");
+  TORCH_CHECK(k.dim() == 3, "k must be 3D [batch, seq_len*num_heads, head_dim]");
+  TORCH_CHECK(q.sizes() == k.sizes(), "q and k must have the same shape");
+  TORCH_CHECK(q_weight.dim() == 1 && k_weight.dim() == 1, "weights must be 1D [head_dim]");
+  TORCH_CHECK(cos.dim() == 2 && sin.dim() == 2, "cos/sin must be 2D [seq_len, head_dim/2]");
+  JO_CHECK_INPUT(q, torch::kBFloat16);
+  JO_CHECK_INPUT(k, torch::kBFloat16);
+  JO_CHECK_INPUT(q_weight, torch::kBFloat16);
+  JO_CHECK_INPUT(k_weight, torch::kBFloat16);
+  JO_CHECK_INPUT(cos, torch::kBFloat16);
+  JO_CHECK_INPUT(sin, torch::kBFloat16);
+  const int64_t batch = q.size(0);
+  const int64_t head_dim = q.size(2);
+  TORCH_CHECK(q.size(1) == seq_len * num_heads, "q.size(1) must equal seq_len*num_heads");
+  TORCH_CHECK(q_weight.size(0) == head_dim && k_weight.size(0) == head_dim,
+              "weight size must match head_dim");
+  TORCH_CHECK(cos.size(0) == seq_len && cos.size(1) == head_dim / 2,
+              "cos shape must be [seq_len, head_dim/2]");
+  TORCH_CHECK(sin.size(0) == seq_len && sin.size(1) == head_dim / 2,
+              "sin shape must be [seq_len, head_dim/2]");
+  TORCH_CHECK(head_dim == 64 || head_dim == 128 || head_dim == 256,
+              "Unsupported head_dim for fused_qk_norm_rope_3d_paired: ", head_dim);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(q.device());
+  const int64_t tok = num_heads * head_dim;
+  check_status(jo_fused_qk_norm_rope_3d_paired(
+                   q.data_ptr(), k.data_ptr(), batch, seq_len, num_heads, head_dim,
+                   seq_len * tok, tok, seq_len * tok, tok, static_cast<float>(eps),
+                   q_weight.data_ptr(), k_weight.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                   current_stream(q)),
+               "fused_qk_norm_rope_3d_paired");
+}
+
+torch::Tensor fused_norm_scale_shift(const torch::Tensor& x,
+                                     const c10::optional<torch::Tensor>& gamma_opt,
+                                     const c10::optional<torch::Tensor>& beta_opt,
+                                     const torch::Tensor& scale, const torch::Tensor& shift,
+                                     int64_t norm_type, double eps) {
+  JO_CHECK_CUDA(x);
+  JO_CHECK_CUDA(scale);
+  JO_CHECK_CUDA(shift);
+  TORCH_CHECK(x.dim() == 2, "x must be 2D [M, N]");
+  TORCH_CHECK(x.stride(-1) == 1, "x last dim must be contiguous");
+  const int64_t M = x.size(0), N = x.size(1);
+  TORCH_CHECK((N % 4) == 0, "N must be divisible by 4");
+  TORCH_CHECK(scale.dim() == 2 && shift.dim() == 2, "scale/shift must be 2D [M, N]");
+  TORCH_CHECK(scale.size(0) == M && shift.size(0) == M,
+              "scale/shift rows must equal M (per-row modulation)");
+  TORCH_CHECK(scale.size(1) == N && shift.size(1) == N, "scale/shift last dim must be N");
+  TORCH_CHECK(scale.stride(-1) == 1 && shift.stride(-1) == 1,
+              "scale/shift last dim must be contiguous");
+  TORCH_CHECK(x.dtype() == scale.dtype() && x.dtype() == shift.dtype(),
+              "x/scale/shift dtype must match");
+  TORCH_CHECK(norm_type == 0 || norm_type == 1, "norm_type must be 0 (layer) or 1 (rms)");
+  const bool has_gamma = gamma_opt.has_value() && gamma_opt->defined();
+  const bool has_beta = beta_opt.has_value() && beta_opt->defined();
+  if (has_gamma) {
+    TORCH_CHECK(gamma_opt->numel() == N, "gamma must be length N");
+    TORCH_CHECK(gamma_opt->is_cuda() && gamma_opt->is_contiguous() &&
+                    gamma_opt->dtype() == x.dtype(),
+                "gamma must be a contiguous CUDA tensor of x's dtype");
+  }
+  if (has_beta) {
+    TORCH_CHECK(beta_opt->numel() == N, "beta must be length N");
+    TORCH_CHECK(beta_opt->is_cuda() && beta_opt->is_contiguous() &&
+                    beta_opt->dtype() == x.dtype(),
+                "beta must be a contiguous CUDA tensor of x's dtype");
+  }
+  const int dt = dtype_code(x);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  auto y = torch::empty({M, N}, x.options());
+  if (M == 0) return y;
+  check_status(jo_fused_norm_scale_shift(
+                   x.data_ptr(), row_stride(x), has_gamma ? gamma_opt->data_ptr() : nullptr,
+                   has_beta ? beta_opt->data_ptr() : nullptr, scale.data_ptr(),
+                   row_stride(scale), shift.data_ptr(), row_stride(shift), y.data_ptr(), N, M,
+                   N, dt, static_cast<int>(norm_type), static_cast<float>(eps),
+                   current_stream(x)),
+               "fused_norm_scale_shift");
+  return y;
+}
+
+torch::Tensor rmsnorm(const torch::Tensor& x, const torch::Tensor& weight, double eps) {
+  JO_CHECK_CUDA(x);
+  JO_CHECK_CUDA(weight);
+  TORCH_CHECK(x.dim() == 2, "x must be 2D [M, N]");
+  TORCH_CHECK(x.stride(-1) == 1, "x last dim must be contiguous");
+  TORCH_CHECK(weight.dim() == 1 && weight.numel() == x.size(1), "weight must be 1D [N]");
+  TORCH_CHECK(x.dtype() == weight.dtype(), "x and weight dtype must match");
+  TORCH_CHECK(weight.stride(0) == 1 || weight.numel() <= 1, "weight must be contiguous");
+  const int dt = dtype_code(x);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int64_t M = x.size(0), N = x.size(1);
+  auto out = torch::empty({M, N}, x.options());
+  if (M == 0 || N == 0) return out;
+  check_status(jo_rmsnorm(x.data_ptr(), row_stride(x), weight.data_ptr(), out.data_ptr(), N, M,
+                          N, dt, static_cast<float>(eps), current_stream(x)),
+               "rmsnorm");
+  return out;
+}
+
+void sgl_per_token_quant_fp8(torch::Tensor input, torch::Tensor output_q,
+                             torch::Tensor output_s) {
+  JO_CHECK_CUDA(input);
+  JO_CHECK_CONTIGUOUS(input);
+  JO_CHECK_CUDA(output_q);
+  JO_CHECK_CUDA(output_s);
+  TORCH_CHECK(input.dim() == 2, "input must be 2D [num_tokens, hidden_dim]");
+  const int64_t num_tokens = input.size(0);
+  const int64_t hidden_dim = input.size(1);
+  TORCH_CHECK(hidden_dim % 4 == 0, "hidden_dim must be divisible by 4, got ", hidden_dim);
+  TORCH_CHECK(input.scalar_type() == torch::kBFloat16 || input.scalar_type() == torch::kFloat16,
+              "per_token_quant_fp8: input must be bf16 or fp16");
+  // Output checks the reference leaves implicit: the kernel writes
+  // output_q as a contiguous [num_tokens, hidden_dim] fp8 array and output_s
+  // as num_tokens consecutive fp32 values ([M] or [M, 1]).
+  TORCH_CHECK(output_q.scalar_type() == at::kFloat8_e4m3fn, "output_q must be float8_e4m3fn");
+  TORCH_CHECK(output_q.is_contiguous() && output_q.numel() == input.numel(),
+              "output_q must be a contiguous tensor with input's number of elements");
+  TORCH_CHECK(output_s.scalar_type() == torch::kFloat32, "output_s must be float32");
+  TORCH_CHECK(output_s.is_contiguous() && output_s.numel() == num_tokens,
+              "output_s must be a contiguous tensor of num_tokens floats");
+  if (num_tokens == 0) return;
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(input.device());
+  check_status(jo_sgl_per_token_quant_fp8(input.data_ptr(), dtype_code(input), num_tokens,
+                                          hidden_dim, hidden_dim, output_q.data_ptr(),
+                                          hidden_dim, output_s.data_ptr<float>(),
+                                          current_stream(input)),
+               "sgl_per_token_quant_fp8");
+}
+
+// ---------------------------------------------------------------------------
+// New ops.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct QKGeom {
+  int64_t batch, seq_len, num_heads, head_dim;
+};
+
+QKGeom check_qk_common(const torch::Tensor& q, const torch::Tensor& k, int64_t seq_len,
+                       int64_t num_heads, const torch::Tensor& q_weight,
+                       const torch::Tensor& k_weight, const torch::Tensor& freqs) {
+  TORCH_CHECK(q.dim() == 3, "q must be 3D [batch, seq_len*num_heads, head_dim]");
+  TORCH_CHECK(k.dim() == 3, "k must be 3D [batch, seq_len*num_heads, head_dim]");
+  TORCH_CHECK(q.sizes() == k.sizes(), "q and k must have the same shape");
+  JO_CHECK_INPUT(q, torch::kBFloat16);
+  JO_CHECK_INPUT(k, torch::kBFloat16);
+  JO_CHECK_INPUT(q_weight, torch::kBFloat16);
+  JO_CHECK_INPUT(k_weight, torch::kBFloat16);
+  JO_CHECK_INPUT(freqs, torch::kFloat32);
+  const int64_t head_dim = q.size(2);
+  TORCH_CHECK(q.size(1) == seq_len * num_heads, "q.size(1) must equal seq_len*num_heads");
+  TORCH_CHECK(q_weight.numel() == head_dim && k_weight.numel() == head_dim,
+              "weight size must match head_dim");
+  TORCH_CHECK(freqs.dim() == 2 && freqs.size(0) == 2 && freqs.size(1) == head_dim / 2,
+              "freqs must be [2, head_dim/2] float32");
+  TORCH_CHECK(head_dim == 64 || head_dim == 128 || head_dim == 256,
+              "Unsupported head_dim: ", head_dim);
+  return {q.size(0), seq_len, num_heads, head_dim};
+}
+
+}  // namespace
+
+void fused_qk_norm_rope_3d_grid(torch::Tensor& q, torch::Tensor& k, int64_t seq_len,
+                                int64_t num_heads, double eps, torch::Tensor& q_weight,
+                                torch::Tensor& k_weight, torch::Tensor& freqs, int64_t pairs_t,
+                                int64_t pairs_h, int64_t grid_h, int64_t grid_w, int64_t t0,
+                                double source_id) {
+  const QKGeom g = check_qk_common(q, k, seq_len, num_heads, q_weight, k_weight, freqs);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(q.device());
+  const int64_t tok = g.num_heads * g.head_dim;
+  check_status(jo_fused_qk_norm_rope_3d_grid(
+                   q.data_ptr(), k.data_ptr(), g.batch, g.seq_len, g.num_heads, g.head_dim,
+                   g.seq_len * tok, tok, g.seq_len * tok, tok, static_cast<float>(eps),
+                   q_weight.data_ptr(), k_weight.data_ptr(), freqs.data_ptr<float>(),
+                   static_cast<int32_t>(pairs_t), static_cast<int32_t>(pairs_h),
+                   static_cast<int32_t>(grid_h), static_cast<int32_t>(grid_w),
+                   static_cast<int32_t>(t0), static_cast<float>(source_id), current_stream(q)),
+               "fused_qk_norm_rope_3d_grid");
+}
+
+void fused_qk_norm_rope_3d_kvcache(torch::Tensor& q, const torch::Tensor& k,
+                                   torch::Tensor& k_cache, int64_t seq_len, int64_t num_heads,
+                                   double eps, const torch::Tensor& q_weight,
+                                   const torch::Tensor& k_weight, const torch::Tensor& freqs,
+                                   int64_t pairs_t, int64_t pairs_h, int64_t grid_h,
+                                   int64_t grid_w, int64_t t0, double source_id,
+                                   int64_t slot_start) {
+  const QKGeom g = check_qk_common(q, k, seq_len, num_heads, q_weight, k_weight, freqs);
+  JO_CHECK_INPUT(k_cache, torch::kBFloat16);
+  TORCH_CHECK(k_cache.dim() == 3 && k_cache.size(0) == g.batch && k_cache.size(2) == g.head_dim,
+              "k_cache must be [batch, cache_tokens*num_heads, head_dim]");
+  TORCH_CHECK(grid_h > 0 && grid_w > 0, "grid_h and grid_w must be positive");
+  const int64_t frame_tokens = grid_h * grid_w;
+  TORCH_CHECK(k_cache.size(1) % (frame_tokens * num_heads) == 0,
+              "k_cache token count must be a whole number of frames");
+  const int64_t cache_slots = k_cache.size(1) / (frame_tokens * num_heads);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(q.device());
+  const int64_t tok = g.num_heads * g.head_dim;
+  check_status(jo_fused_qk_norm_rope_3d_kvcache(
+                   q.data_ptr(), k.data_ptr(), k_cache.data_ptr(), g.batch, g.seq_len,
+                   g.num_heads, g.head_dim, g.seq_len * tok, tok, g.seq_len * tok, tok,
+                   k_cache.size(1) * g.head_dim, tok, cache_slots, slot_start,
+                   static_cast<float>(eps), q_weight.data_ptr(), k_weight.data_ptr(),
+                   freqs.data_ptr<float>(), static_cast<int32_t>(pairs_t),
+                   static_cast<int32_t>(pairs_h), static_cast<int32_t>(grid_h),
+                   static_cast<int32_t>(grid_w), static_cast<int32_t>(t0),
+                   static_cast<float>(source_id), current_stream(q)),
+               "fused_qk_norm_rope_3d_kvcache");
+}
+
+namespace {
+// Row stride of an [N] vector or an [M, N] per-row tensor: 0 broadcasts.
+int64_t mod_stride(const torch::Tensor& t, int64_t M, int64_t N, const char* name) {
+  JO_CHECK_CUDA(t);
+  if (t.dim() == 1) {
+    TORCH_CHECK(t.size(0) == N && t.stride(0) == 1, name, " must be [N] contiguous");
+    return 0;
+  }
+  TORCH_CHECK(t.dim() == 2 && t.size(0) == M && t.size(1) == N && t.stride(1) == 1, name,
+              " must be [N] or [M, N] with a contiguous last dim");
+  return row_stride(t);
+}
+}  // namespace
+
+torch::Tensor fused_add_layernorm_scale_shift(const torch::Tensor& x, torch::Tensor& residual,
+                                              const c10::optional<torch::Tensor>& gate_opt,
+                                              const c10::optional<torch::Tensor>& gamma_opt,
+                                              const c10::optional<torch::Tensor>& beta_opt,
+                                              const torch::Tensor& scale,
+                                              const torch::Tensor& shift, double eps) {
+  JO_CHECK_CUDA(x);
+  JO_CHECK_CUDA(residual);
+  TORCH_CHECK(x.dim() == 2 && x.stride(-1) == 1, "x must be 2D [M, N] with contiguous rows");
+  TORCH_CHECK(residual.sizes() == x.sizes() && residual.stride(-1) == 1,
+              "residual must match x");
+  const int64_t M = x.size(0), N = x.size(1);
+  TORCH_CHECK(N % 4 == 0, "N must be divisible by 4");
+  TORCH_CHECK(residual.dtype() == x.dtype() && scale.dtype() == x.dtype() &&
+                  shift.dtype() == x.dtype(),
+              "x/residual/scale/shift dtype must match");
+  const int64_t sc_stride = mod_stride(scale, M, N, "scale");
+  const int64_t sh_stride = mod_stride(shift, M, N, "shift");
+  const bool has_gate = gate_opt.has_value() && gate_opt->defined();
+  int64_t g_stride = 0;
+  if (has_gate) {
+    TORCH_CHECK(gate_opt->dtype() == x.dtype(), "gate dtype must match x");
+    g_stride = mod_stride(*gate_opt, M, N, "gate");
+  }
+  const bool has_gamma = gamma_opt.has_value() && gamma_opt->defined();
+  const bool has_beta = beta_opt.has_value() && beta_opt->defined();
+  if (has_gamma)
+    TORCH_CHECK(gamma_opt->numel() == N && gamma_opt->is_contiguous() &&
+                    gamma_opt->dtype() == x.dtype(),
+                "gamma must be [N] contiguous of x's dtype");
+  if (has_beta)
+    TORCH_CHECK(beta_opt->numel() == N && beta_opt->is_contiguous() &&
+                    beta_opt->dtype() == x.dtype(),
+                "beta must be [N] contiguous of x's dtype");
+  const int dt = dtype_code(x);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  auto y = torch::empty({M, N}, x.options());
+  if (M == 0) return y;
+  check_status(jo_fused_add_layernorm_scale_shift(
+                   x.data_ptr(), row_stride(x), residual.data_ptr(), row_stride(residual),
+                   has_gate ? gate_opt->data_ptr() : nullptr, g_stride,
+                   has_gamma ? gamma_opt->data_ptr() : nullptr,
+                   has_beta ? beta_opt->data_ptr() : nullptr, scale.data_ptr(), sc_stride,
+                   shift.data_ptr(), sh_stride, y.data_ptr(), N, M, N, dt,
+                   static_cast<float>(eps), current_stream(x)),
+               "fused_add_layernorm_scale_shift");
+  return y;
+}
+
+void rmsnorm_quant_fp8(const torch::Tensor& x, const torch::Tensor& weight, double eps,
+                       torch::Tensor output_q, torch::Tensor output_s, int64_t group_size) {
+  JO_CHECK_CUDA(x);
+  JO_CHECK_CUDA(weight);
+  JO_CHECK_CUDA(output_q);
+  JO_CHECK_CUDA(output_s);
+  TORCH_CHECK(x.dim() == 2 && x.stride(-1) == 1, "x must be 2D [M, N] with contiguous rows");
+  const int64_t M = x.size(0), N = x.size(1);
+  TORCH_CHECK(x.scalar_type() == torch::kBFloat16 || x.scalar_type() == torch::kFloat16,
+              "x must be bf16 or fp16");
+  TORCH_CHECK(weight.dtype() == x.dtype() && weight.numel() == N && weight.is_contiguous(),
+              "weight must be [N] contiguous of x's dtype");
+  TORCH_CHECK(group_size == 0 || group_size == 128, "group_size must be 0 or 128");
+  TORCH_CHECK(output_q.scalar_type() == at::kFloat8_e4m3fn && output_q.is_contiguous() &&
+                  output_q.numel() == M * N,
+              "output_q must be a contiguous float8_e4m3fn tensor with M*N elements");
+  const int64_t ns = group_size == 0 ? M : (N % 128 == 0 ? M * (N / 128) : -1);
+  TORCH_CHECK(output_s.scalar_type() == torch::kFloat32 && output_s.is_contiguous() &&
+                  output_s.numel() == ns,
+              "output_s must be contiguous float32 with M (per-token) or M*N/128 elements");
+  if (M == 0) return;
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  check_status(jo_rmsnorm_quant_fp8(x.data_ptr(), row_stride(x), weight.data_ptr(),
+                                    output_q.data_ptr(), N, output_s.data_ptr<float>(), M, N,
+                                    dtype_code(x), static_cast<float>(eps), group_size,
+                                    current_stream(x)),
+               "rmsnorm_quant_fp8");
+}
+
+}  // namespace joyomni_ops
+
+TORCH_LIBRARY(joyomni_ops, m) {
+  // Reference schemas (deploy/joyomni_ops/csrc/pybind.cpp:35-43), unchanged.
+  m.def(
+      "fused_qk_norm_rope_3d_paired(Tensor! q, Tensor! k, int seq_len, int num_heads, float eps, "
+      "Tensor q_weight, Tensor k_weight, Tensor cos, Tensor sin) -> ()");
+  m.def(
+      "fused_norm_scale_shift(Tensor x, Tensor? gamma_opt, Tensor? beta_opt, "
+      "Tensor scale, Tensor shift, int norm_type, float eps) -> Tensor");
+  m.def("rmsnorm(Tensor x, Tensor weight, float eps) -> Tensor");
+  m.def("sgl_per_token_quant_fp8(Tensor input, Tensor! output_q, Tensor! output_s) -> ()");
+  // New ops.
+  m.def(
+      "fused_qk_norm_rope_3d_grid(Tensor! q, Tensor! k, int seq_len, int num_heads, float eps, "
+      "Tensor q_weight, Tensor k_weight, Tensor freqs, int pairs_t, int pairs_h, int grid_h, "
+      "int grid_w, int t0, float source_id) -> ()");
+  m.def(
+      "fused_qk_norm_rope_3d_kvcache(Tensor! q, Tensor k, Tensor! k_cache, int seq_len, "
+      "int num_heads, float eps, Tensor q_weight, Tensor k_weight, Tensor freqs, int pairs_t, "
+      "int pairs_h, int grid_h, int grid_w, int t0, float source_id, int slot_start) -> ()");
+  m.def(
+      "fused_add_layernorm_scale_shift(Tensor x, Tensor! residual, Tensor? gate, "
+      "Tensor? gamma_opt, Tensor? beta_opt, Tensor scale, Tensor shift, float eps) -> Tensor");
+  m.def(
+      "rmsnorm_quant_fp8(Tensor x, Tensor weight, float eps, Tensor! output_q, "
+      "Tensor! output_s, int group_size) -> ()");
+}
+
+TORCH_LIBRARY_IMPL(joyomni_ops, CUDA, m) {
+  m.impl("fused_qk_norm_rope_3d_paired", &joyomni_ops::fused_qk_norm_rope_3d_paired);
+  m.impl("fused_norm_scale_shift", &joyomni_ops::fused_norm_scale_shift);
+  m.impl("rmsnorm", &joyomni_ops::rmsnorm);
+  m.impl("sgl_per_token_quant_fp8", &joyomni_ops::sgl_per_token_quant_fp8);
+  m.impl("fused_qk_norm_rope_3d_grid", &joyomni_ops::fused_qk_norm_rope_3d_grid);
+  m.impl("fused_qk_norm_rope_3d_kvcache", &joyomni_ops::fused_qk_norm_rope_3d_kvcache);
+  m.impl("fused_add_layernorm_scale_shift", &joyomni_ops::fused_add_layernorm_scale_shift);
+  m.impl("rmsnorm_quant_fp8", &joyomni_ops::rmsnorm_quant_fp8);
+}

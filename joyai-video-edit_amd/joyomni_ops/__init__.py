@@ -1,0 +1,181 @@
+"""joyomni_ops — MI355X (gfx950) kernels for the per-step ops of the JoyOmni DiT.
+
+Same import surface as the reference package
+(deploy/joyomni_ops/joyomni_ops/__init__.py:1-58): loading the package loads
+the `_C*.so` torch op library (which pulls in the HIP kernel library
+libjoyomni_hip.so) and registers torch.ops.joyomni_ops.*; the thin wrappers
+below keep the reference's names, argument order, defaults and the
+"layer"/"rms" norm_type mapping. There is no CPU path: the ops are registered
+for device tensors only, and importing fails if the libraries are missing.
+
+New ops (no reference signature): fused_qk_norm_rope_3d_grid,
+fused_qk_norm_rope_3d_kvcache, fused_add_layernorm_scale_shift,
+rmsnorm_quant_fp8, plus rope_freqs() to build the [2, head_dim/2] frequency
+table the grid ops read.
+"""
+from __future__ import annotations
+
+import glob
+import os
+from typing import Optional, Sequence
+
+import torch
+
+# The extension is a pure TORCH_LIBRARY (no pybind module init): load it with
+# torch.ops.load_library to run the op registration.
+_here = os.path.dirname(__file__)
+_so = glob.glob(os.path.join(_here, "_C*.so"))
+if not _so:
+    raise ImportError(
+        f"joyomni_ops C extension not found in {_here}; build it first "
+        "(python joyai-video-edit_amd/build.py)")
+torch.ops.load_library(_so[0])
+
+__all__ = [
+    "fused_qk_norm_rope_3d_paired",
+    "fused_norm_scale_shift",
+    "rmsnorm",
+    "sgl_per_token_quant_fp8",
+    "fp8_scaled_mm",
+    "has_fp8",
+    "rope_freqs",
+    "fused_qk_norm_rope_3d_grid",
+    "fused_qk_norm_rope_3d_kvcache",
+    "fused_add_layernorm_scale_shift",
+    "rmsnorm_quant_fp8",
+    "kv_ring_slot",
+]
+
+_ops = torch.ops.joyomni_ops
+
+
+# ---------------------------------------------------------------------------
+# Reference ops (deploy/joyomni_ops/joyomni_ops/__init__.py:33-58).
+# ---------------------------------------------------------------------------
+def fused_qk_norm_rope_3d_paired(q, k, seq_len, num_heads, eps, q_weight, k_weight, cos, sin):
+    """In-place fused RMSNorm(q,k) + 3D RoPE. q/k: [B, seq_len*num_heads, head_dim] bf16."""
+    _ops.fused_qk_norm_rope_3d_paired(q, k, seq_len, num_heads, eps, q_weight, k_weight, cos, sin)
+
+
+def fused_norm_scale_shift(x, gamma, beta, scale, shift, norm_type, eps=1e-5):
+    """Norm(x; gamma, beta) * (1 + scale) + shift. norm_type: 'layer' or 'rms'.
+
+    scale/shift may also be stride-0 expanded views of one [N] row
+    (e.g. ``s.expand(M, N)``): the kernel then reads the single row.
+    """
+    nt = 0 if norm_type == "layer" else 1 if norm_type == "rms" else -1
+    return _ops.fused_norm_scale_shift(x, gamma, beta, scale, shift, nt, eps)
+
+
+def rmsnorm(x, weight, eps=1e-6):
+    """(x / RMS(x)) * weight. x: [M, N], weight: [N]."""
+    return _ops.rmsnorm(x, weight, eps)
+
+
+def has_fp8() -> bool:
+    """True when the FP8 GEMM op is registered (the reference's test, __init__.py:49-50).
+
+    This library provides the FP8 quantization ops but not fp8_scaled_mm, so
+    callers take the reference's bf16 GEMM path, as with a reference build
+    made with JOYOMNI_OPS_NO_FP8.
+    """
+    return hasattr(_ops, "fp8_scaled_mm")
+
+
+def sgl_per_token_quant_fp8(input, output_q, output_s):
+    _ops.sgl_per_token_quant_fp8(input, output_q, output_s)
+
+
+def fp8_scaled_mm(mat_a, mat_b, scales_a, scales_b, out_dtype, bias: Optional[torch.Tensor] = None):
+    """Rowwise-scaled FP8 GEMM: not implemented by this library (has_fp8() is False)."""
+    if not has_fp8():
+        raise NotImplementedError("fp8_scaled_mm is not provided by this build (has_fp8() is False)")
+    return _ops.fp8_scaled_mm(mat_a, mat_b, scales_a, scales_b, out_dtype, bias)
+
+
+# ---------------------------------------------------------------------------
+# New ops.
+# ---------------------------------------------------------------------------
+_FREQ_CACHE: dict = {}
+
+
+def rope_freqs(head_dim: int, rope_dims: Sequence[int], theta: float,
+               source_theta: float = 256.0, source_dim: Optional[int] = None,
+               device=None) -> torch.Tensor:
+    """fp32 [2, head_dim/2] frequency table read by the grid RoPE ops.
+
+    Row 0 holds, per rotation pair, the frequency of its axis: the t, h and w
+    axes take rope_dims[0]/2, rope_dims[1]/2 and rope_dims[2]/2 consecutive
+    pairs, each with 1 / theta^(2j/dim) (deploy/xvideo/models/dit/rope.py:46-48).
+    Row 1 holds the source-id frequencies 1 / source_theta^(2j/source_dim)
+    for the first source_dim/2 pairs and 0 after them
+    (deploy/xvideo/models/dit/dit.py:796-805; a zero frequency is the
+    identity rotation the reference uses there). The values are computed with
+    the same fp32 torch expressions as the reference and cached per device.
+    """
+    dims = tuple(int(d) for d in rope_dims)
+    if len(dims) != 3 or sum(dims) != head_dim or any(d % 2 for d in dims):
+        raise ValueError(f"rope_dims {dims} must be 3 even sizes summing to head_dim {head_dim}")
+    role = head_dim if source_dim is None else max(0, min(int(source_dim), head_dim))
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    key = (dev, head_dim, dims, float(theta), float(source_theta), role)
+    t = _FREQ_CACHE.get(key)
+    if t is None:
+        rows = []
+        for d in dims:
+            rows.append(1.0 / (theta ** (torch.arange(0, d, 2)[: (d // 2)].float() / d)))
+        axis = torch.cat(rows)
+        sid = torch.zeros(head_dim // 2, dtype=torch.float32)
+        if role > 0:
+            sid[: role // 2] = 1.0 / (
+                source_theta ** (torch.arange(0, role, 2, dtype=torch.float32) / role))
+        t = torch.stack([axis, sid]).to(dev)
+        _FREQ_CACHE[key] = t
+    return t
+
+
+def fused_qk_norm_rope_3d_grid(q, k, seq_len, num_heads, eps, q_weight, k_weight, freqs,
+                               rope_dims, grid_hw, t0=0, source_id=0.0):
+    """In-place RMSNorm(q,k) + 3D RoPE with angles computed from grid positions.
+
+    q/k: [B, seq_len*num_heads, head_dim] bf16; the sequence is frames of
+    grid_hw = (H, W) tokens, frame f at temporal position t0 + f.
+    freqs: rope_freqs(head_dim, rope_dims, theta, ...).
+    """
+    gh, gw = grid_hw
+    _ops.fused_qk_norm_rope_3d_grid(q, k, seq_len, num_heads, eps, q_weight, k_weight, freqs,
+                                    rope_dims[0] // 2, rope_dims[1] // 2, gh, gw, t0,
+                                    float(source_id))
+
+
+def kv_ring_slot(t0: int, frames_per_chunk: int, cache_slots: int) -> int:
+    """First ring slot of a chunk starting at temporal position t0: (t0 / frames) mod slots."""
+    return (t0 // frames_per_chunk) % cache_slots
+
+
+def fused_qk_norm_rope_3d_kvcache(q, k, k_cache, seq_len, num_heads, eps, q_weight, k_weight,
+                                  freqs, rope_dims, grid_hw, t0, slot_start, source_id=0.0):
+    """Grid RoPE with q rotated in place and the rotated k written to k_cache.
+
+    k_cache: [B, cache_slots*H*W*num_heads, head_dim] bf16; frame f of the
+    chunk lands in slot (slot_start + f) % cache_slots. k is not modified.
+    """
+    gh, gw = grid_hw
+    _ops.fused_qk_norm_rope_3d_kvcache(q, k, k_cache, seq_len, num_heads, eps, q_weight,
+                                       k_weight, freqs, rope_dims[0] // 2, rope_dims[1] // 2,
+                                       gh, gw, t0, float(source_id), slot_start)
+
+
+def fused_add_layernorm_scale_shift(x, residual, scale, shift, gate=None, gamma=None, beta=None,
+                                    eps=1e-6):
+    """residual <- residual + x (* gate); returns LayerNorm(residual) * (1 + scale) + shift.
+
+    x, residual: [M, N]; residual is updated in place. scale/shift/gate:
+    [N] (broadcast) or [M, N].
+    """
+    return _ops.fused_add_layernorm_scale_shift(x, residual, gate, gamma, beta, scale, shift, eps)
+
+
+def rmsnorm_quant_fp8(x, weight, eps, output_q, output_s, group_size=0):
+    """FP8 e4m3 quantization of RMSNorm(x) * weight (fp32), per token or per 1x128 block."""
+    _ops.rmsnorm_quant_fp8(x, weight, eps, output_q, output_s, group_size)

@@ -1,0 +1,157 @@
+"""The BASELINE workloads of the joyomni_ops hot path: shapes, seeded synthetic
+inputs, launch helpers through the C ABI, and algorithmic HBM bytes.
+
+Configs (720p 3-latent-frame chunk shapes, hidden 3072, 24 heads x 128):
+  C0   QK RMSNorm + 3D RoPE, grid angles: q,k bf16 [1, 3510, 24, 128]
+  C1   per-token FP8 e4m3 quant: x bf16 [10530, 3072]
+  C2   residual add + LayerNorm + AdaLN: x, residual bf16 [10530, 3072]
+  C3   QK RMSNorm + RoPE with K into a 7-slot ring cache: q,k [1, 10530, 24, 128]
+  C4*  RMSNorm -> FP8, T in {4725, 10530}, per-token or per-1x128-block scales
+
+Inputs are generated on the CPU with torch.Generator().manual_seed(s)
+(s = config index) in fp32, cast to bf16, and copied to the device, so the
+CPU oracle and the GPU see identical tensors. Outliers: exactly
+round(0.005 * numel) distinct entries (randperm) multiplied by 40.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _abi
+
+
+@dataclass(frozen=True)
+class Config:
+    name: str
+    op: str
+    seed: int
+    dims: dict = field(default_factory=dict)
+
+
+CONFIGS: dict[str, Config] = {
+    "C0": Config("C0", "qk_grid", 0, dict(B=1, L=3510, H=24, D=128, grid=(45, 78), t0=0,
+                                          rope_dims=(44, 42, 42), theta=10000.0, eps=1e-6)),
+    "C1": Config("C1", "quant", 1, dict(M=10530, K=3072)),
+    "C2": Config("C2", "add_ln", 2, dict(M=10530, N=3072, eps=1e-6)),
+    "C3": Config("C3", "qk_kvcache", 3, dict(B=1, L=10530, H=24, D=128, grid=(45, 78), t0=21,
+                                             frames=3, cache_slots=7, rope_dims=(44, 42, 42),
+                                             theta=10000.0, eps=1e-6)),
+    "C4_4725_tok": Config("C4_4725_tok", "rms_quant", 4, dict(M=4725, N=3072, group=0, eps=1e-6)),
+    "C4_4725_blk": Config("C4_4725_blk", "rms_quant", 4, dict(M=4725, N=3072, group=128, eps=1e-6)),
+    "C4_10530_tok": Config("C4_10530_tok", "rms_quant", 4, dict(M=10530, N=3072, group=0, eps=1e-6)),
+    "C4_10530_blk": Config("C4_10530_blk", "rms_quant", 4, dict(M=10530, N=3072, group=128, eps=1e-6)),
+}
+
+
+def with_outliers(x: torch.Tensor, gen: torch.Generator, frac: float = 0.005, mult: float = 40.0):
+    flat = x.reshape(-1)
+    n = round(frac * flat.numel())
+    idx = torch.randperm(flat.numel(), generator=gen)[:n]
+    flat[idx] *= mult
+    return x
+
+
+def make_inputs(cfg: Config, device="cpu") -> dict:
+    """Seeded inputs of a config (CPU generation, then `.to(device)`)."""
+    g = torch.Generator().manual_seed(cfg.seed)
+    d = cfg.dims
+    out: dict = {}
+    if cfg.op in ("qk_grid", "qk_kvcache"):
+        shape = (d["B"], d["L"] * d["H"], d["D"])
+        out["q"] = torch.randn(shape, generator=g).to(torch.bfloat16)
+        out["k"] = torch.randn(shape, generator=g).to(torch.bfloat16)
+        out["q_weight"] = (1 + 0.1 * torch.randn(d["D"], generator=g)).to(torch.bfloat16)
+        out["k_weight"] = (1 + 0.1 * torch.randn(d["D"], generator=g)).to(torch.bfloat16)
+        if cfg.op == "qk_kvcache":
+            gh, gw = d["grid"]
+            out["k_cache"] = torch.zeros((d["B"], d["cache_slots"] * gh * gw * d["H"], d["D"]),
+                                         dtype=torch.bfloat16)
+    elif cfg.op == "quant":
+        out["x"] = with_outliers(torch.randn(d["M"], d["K"], generator=g), g).to(torch.bfloat16)
+    elif cfg.op == "add_ln":
+        out["x"] = torch.randn(d["M"], d["N"], generator=g).to(torch.bfloat16)
+        out["residual"] = torch.randn(d["M"], d["N"], generator=g).to(torch.bfloat16)
+        out["shift"] = (0.2 * torch.randn(d["N"], generator=g)).to(torch.bfloat16)
+        out["scale"] = (0.2 * torch.randn(d["N"], generator=g)).to(torch.bfloat16)
+    elif cfg.op == "rms_quant":
+        out["x"] = with_outliers(torch.randn(d["M"], d["N"], generator=g), g).to(torch.bfloat16)
+        out["weight"] = (1 + 0.1 * torch.randn(d["N"], generator=g)).to(torch.bfloat16)
+    else:
+        raise ValueError(cfg.op)
+    return {k: v.to(device) for k, v in out.items()}
+
+
+def algorithmic_bytes(cfg: Config) -> int:
+    """Compulsory HBM bytes of one call: inputs read once + outputs written once."""
+    d = cfg.dims
+    if cfg.op == "qk_grid":
+        n = d["B"] * d["L"] * d["H"] * d["D"] * 2
+        return 4 * n + 2 * d["D"] * 2                      # q,k read + write; weights
+    if cfg.op == "qk_kvcache":
+        n = d["B"] * d["L"] * d["H"] * d["D"] * 2
+        return 4 * n + 2 * d["D"] * 2                      # q r/w, k read, cache write
+    if cfg.op == "quant":
+        return d["M"] * d["K"] * 3 + d["M"] * 4            # bf16 in, fp8 out, scales
+    if cfg.op == "add_ln":
+        return 4 * d["M"] * d["N"] * 2 + 2 * d["N"] * 2    # x, res in; res, y out; mod rows
+    if cfg.op == "rms_quant":
+        ns = d["M"] if d["group"] == 0 else d["M"] * (d["N"] // d["group"])
+        return d["M"] * d["N"] * 3 + ns * 4 + d["N"] * 2   # bf16 in, fp8 out, scales, gamma
+    raise ValueError(cfg.op)
+
+
+def alloc_outputs(cfg: Config, inputs: dict) -> dict:
+    d = cfg.dims
+    dev = next(iter(inputs.values())).device
+    if cfg.op == "quant":
+        return {"q": torch.empty(d["M"], d["K"], dtype=torch.float8_e4m3fn, device=dev),
+                "s": torch.empty(d["M"], dtype=torch.float32, device=dev)}
+    if cfg.op == "rms_quant":
+        ns = (d["M"],) if d["group"] == 0 else (d["M"], d["N"] // d["group"])
+        return {"q": torch.empty(d["M"], d["N"], dtype=torch.float8_e4m3fn, device=dev),
+                "s": torch.empty(ns, dtype=torch.float32, device=dev)}
+    if cfg.op == "add_ln":
+        return {"y": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev)}
+    return {}
+
+
+def launch(cfg: Config, t: dict, stream_handle: int, freqs: torch.Tensor | None = None) -> None:
+    """Enqueue one call of the config's op through the C ABI on `stream_handle`.
+
+    `t` holds the config's inputs and outputs (make_inputs + alloc_outputs).
+    The qk ops work in place on t["q"]/t["k"] (and t["k_cache"]).
+    """
+    d = cfg.dims
+    p = lambda x: x.data_ptr()  # noqa: E731
+    if cfg.op == "quant":
+        _abi.call("jo_sgl_per_token_quant_fp8", p(t["x"]), _abi.JO_DTYPE_BF16, d["M"], d["K"],
+                  d["K"], p(t["q"]), d["K"], p(t["s"]), stream_handle)
+    elif cfg.op == "rms_quant":
+        _abi.call("jo_rmsnorm_quant_fp8", p(t["x"]), d["N"], p(t["weight"]), p(t["q"]), d["N"],
+                  p(t["s"]), d["M"], d["N"], _abi.JO_DTYPE_BF16, d["eps"], d["group"],
+                  stream_handle)
+    elif cfg.op == "add_ln":
+        _abi.call("jo_fused_add_layernorm_scale_shift", p(t["x"]), d["N"], p(t["residual"]),
+                  d["N"], None, 0, None, None, p(t["scale"]), 0, p(t["shift"]), 0, p(t["y"]),
+                  d["N"], d["M"], d["N"], _abi.JO_DTYPE_BF16, d["eps"], stream_handle)
+    elif cfg.op in ("qk_grid", "qk_kvcache"):
+        B, L, H, D = d["B"], d["L"], d["H"], d["D"]
+        gh, gw = d["grid"]
+        pt, ph = d["rope_dims"][0] // 2, d["rope_dims"][1] // 2
+        tok = H * D
+        if cfg.op == "qk_grid":
+            _abi.call("jo_fused_qk_norm_rope_3d_grid", p(t["q"]), p(t["k"]), B, L, H, D, L * tok,
+                      tok, L * tok, tok, d["eps"], p(t["q_weight"]), p(t["k_weight"]), p(freqs),
+                      pt, ph, gh, gw, d["t0"], 0.0, stream_handle)
+        else:
+            slots = d["cache_slots"]
+            slot0 = (d["t0"] // d["frames"]) % slots
+            cache_tokens = slots * gh * gw
+            _abi.call("jo_fused_qk_norm_rope_3d_kvcache", p(t["q"]), p(t["k"]), p(t["k_cache"]),
+                      B, L, H, D, L * tok, tok, L * tok, tok, cache_tokens * tok, tok, slots,
+                      slot0, d["eps"], p(t["q_weight"]), p(t["k_weight"]), p(freqs), pt, ph, gh,
+                      gw, d["t0"], 0.0, stream_handle)
+    else:
+        raise ValueError(cfg.op)

@@ -1,0 +1,219 @@
+"""Torch-on-CPU restatements of the reference's joyomni_ops formulas.
+
+TEST INFRASTRUCTURE: imported only by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg. Every function takes and returns CPU tensors and
+computes in fp32 exactly as the cited reference lines (kernel semantics) or
+test formulas do. Paths are relative to jd-opensource/JoyAI-Video-Edit.
+"""
+from __future__ import annotations
+
+import torch
+
+FP8_MAX = 448.0
+
+
+# ---------------------------------------------------------------------------
+# FP8 per-token quantization — deploy/joyomni_ops/csrc/per_token_quant_fp8.cu:56-82
+# ---------------------------------------------------------------------------
+def fp8_quant_with_inv(v: torch.Tensor, inv: torch.Tensor) -> torch.Tensor:
+    """q = e4m3fn(fmax(fmin(v * inv, 448), -448)) as uint8 (per_token_quant_fp8.cu:72-74).
+
+    torch.fmin/fmax return the non-NaN operand like CUDA fminf/fmaxf, so a NaN
+    becomes +448. The clamp keeps the cast's input finite; torch's cast then
+    rounds to nearest-even, which equals the reference's satfinite conversion.
+    """
+    t = v * inv
+    t = torch.fmax(torch.fmin(t, torch.tensor(FP8_MAX)), torch.tensor(-FP8_MAX))
+    return t.to(torch.float8_e4m3fn).view(torch.uint8)
+
+
+def scale_and_inv(amax: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """scale = amax / 448; inv = (scale == 0) ? 0 : 1 / scale (per_token_quant_fp8.cu:63-65)."""
+    scale = amax / FP8_MAX
+    inv = torch.where(scale == 0, torch.zeros_like(scale), 1.0 / scale)
+    return scale, inv
+
+
+def nan_ignoring_amax(v: torch.Tensor, dim: int = -1) -> torch.Tensor:
+    """max(0, max |v|) with NaNs skipped, as fmaxf(max, fabsf(v)) from 0 does (:56-61)."""
+    a = v.abs()
+    a = torch.where(torch.isnan(a), torch.zeros_like(a), a)
+    return a.amax(dim=dim) if a.shape[dim] > 0 else torch.zeros(a.shape[:-1])
+
+
+def per_token_quant_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """x: bf16/fp16 [M, K] -> (q uint8 [M, K] e4m3fn bytes, s fp32 [M])."""
+    xf = x.float()
+    scale, inv = scale_and_inv(nan_ignoring_amax(xf))
+    return fp8_quant_with_inv(xf, inv[:, None]), scale
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm — deploy/joyomni_ops/csrc/rmsnorm.cu:41-60; formula of
+# deploy/joyomni_ops/tests/test_bench.py:65-67 and test_parity_light.py:31-32.
+# ---------------------------------------------------------------------------
+def rmsnorm_f32(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)) * w.float()
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    return rmsnorm_f32(x, w, eps).to(x.dtype)
+
+
+# ---------------------------------------------------------------------------
+# (Layer|RMS)Norm + AdaLN — deploy/joyomni_ops/csrc/fused_norm_scale_shift.cu:88-142;
+# formula of test_parity_light.py:47-51 / test_bench.py:91-96.
+# gamma is the affine switch (:125, :192); beta only applies with gamma (:130).
+# ---------------------------------------------------------------------------
+def norm_scale_shift_f32(x, gamma, beta, scale, shift, norm_type: int, eps: float):
+    xf = x.float()
+    affine = gamma is not None
+    if norm_type == 0:
+        mean = xf.mean(-1, keepdim=True)
+        var = (xf - mean).pow(2).mean(-1, keepdim=True)
+        n = (xf - mean) * torch.rsqrt(var + eps)
+        if affine:
+            n = n * gamma.float()
+            if beta is not None:
+                n = n + beta.float()
+    elif norm_type == 1:
+        n = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+        if affine:
+            n = n * gamma.float()
+    else:
+        raise ValueError("norm_type must be 0 (layer) or 1 (rms)")
+    return n * (1 + scale.float()) + shift.float()
+
+
+def norm_scale_shift(x, gamma, beta, scale, shift, norm_type: int, eps: float):
+    return norm_scale_shift_f32(x, gamma, beta, scale, shift, norm_type, eps).to(x.dtype)
+
+
+# ---------------------------------------------------------------------------
+# Residual (optionally gated) add + LayerNorm + AdaLN: composition of
+# deploy/xvideo/models/dit/sgl_fused_ops.py:114-117 (torch.addcmul, one
+# rounding) and the LayerNorm path above, on the rounded residual.
+# ---------------------------------------------------------------------------
+def add_layernorm_scale_shift(x, residual, gate, gamma, beta, scale, shift, eps: float):
+    xf = x.float()
+    rf = residual.float()
+    upd = rf + (xf * gate.float() if gate is not None else xf)
+    new_res = upd.to(residual.dtype)
+    y = norm_scale_shift_f32(new_res, gamma, beta, scale, shift, 0, eps)
+    return new_res, y
+
+
+# ---------------------------------------------------------------------------
+# QK RMSNorm + interleaved RoPE from tables —
+# deploy/joyomni_ops/csrc/fused_qknorm_rope_3d_kernel.cu:98-142; formula of
+# deploy/joyomni_ops/tests/test_parity_light.py:77-87 / test_bench.py:123-132.
+# ---------------------------------------------------------------------------
+def qk_norm_rope_f32(x: torch.Tensor, w: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                     eps: float) -> torch.Tensor:
+    """x: [B, L, H, D]; cos/sin: [L, D/2] (any float dtype). Returns fp32 [B, L, H, D]."""
+    B, L, H, D = x.shape
+    xf = x.float()
+    xn = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+    c = cos.float().reshape(L, 1, D // 2)
+    s = sin.float().reshape(L, 1, D // 2)
+    x1 = xn[..., 0::2]
+    x2 = xn[..., 1::2]
+    o = torch.empty_like(xn)
+    o[..., 0::2] = x1 * c - x2 * s
+    o[..., 1::2] = x1 * s + x2 * c
+    return o
+
+
+# ---------------------------------------------------------------------------
+# RoPE tables — deploy/xvideo/models/dit/rope.py:31-52 (1-D tables),
+# dit.py:745-783 (t/h/w axes, meshgrid "ij", concatenation) and
+# dit.py:785-809, 918-933 (source-id rotation composed by angle addition).
+# ---------------------------------------------------------------------------
+def axis_freqs(dim: int, theta: float) -> torch.Tensor:
+    """1 / theta^(2j/dim) for j < dim/2, fp32 (rope.py:46-48)."""
+    return 1.0 / (theta ** (torch.arange(0, dim, 2)[: (dim // 2)].float() / dim))
+
+
+def rope_1d(dim: int, pos: torch.Tensor, theta: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """(cos, sin) [len(pos), dim] with repeat_interleave(2) (rope.py:31-52)."""
+    freqs = torch.outer(pos.float(), axis_freqs(dim, theta))
+    return freqs.cos().repeat_interleave(2, dim=1), freqs.sin().repeat_interleave(2, dim=1)
+
+
+def grid_positions(num_frames: int, grid_h: int, grid_w: int, t0: int):
+    """(t, h, w) fp32 positions of every token, frame-major, then h, then w (dit.py:757-764)."""
+    t = (torch.arange(num_frames, dtype=torch.float32) + t0).repeat_interleave(grid_h * grid_w)
+    hg, wg = torch.meshgrid(torch.arange(grid_h, dtype=torch.float32),
+                            torch.arange(grid_w, dtype=torch.float32), indexing="ij")
+    h = hg.reshape(-1).repeat(num_frames)
+    w = wg.reshape(-1).repeat(num_frames)
+    return t, h, w
+
+
+def rope_grid_tables(num_frames: int, grid_h: int, grid_w: int, t0: int, rope_dims,
+                     theta: float, source_id: float = 0.0, source_theta: float = 256.0,
+                     source_dim: int | None = None):
+    """Full-width fp32 (cos, sin) [L, D] exactly as Transformer3DModel builds them.
+
+    The 3D tables concatenate the t/h/w 1-D tables (dit.py:775-781). A non-zero
+    source id composes a second rotation over the first `source_dim` dims
+    (default all) by angle addition (dit.py:792-808, 931-932).
+    """
+    t, h, w = grid_positions(num_frames, grid_h, grid_w, t0)
+    cs, ss = [], []
+    for dim, pos in zip(rope_dims, (t, h, w)):
+        c, s = rope_1d(dim, pos, theta)
+        cs.append(c)
+        ss.append(s)
+    cos3, sin3 = torch.cat(cs, dim=1), torch.cat(ss, dim=1)
+    if source_id == 0.0:
+        return cos3, sin3
+    D = cos3.shape[1]
+    role_dim = D if source_dim is None else max(0, min(int(source_dim), D))
+    L = cos3.shape[0]
+    sid = torch.full((L,), float(source_id), dtype=torch.float32)
+    cos_half = torch.ones(L, D // 2, dtype=torch.float32)
+    sin_half = torch.zeros(L, D // 2, dtype=torch.float32)
+    inv_freq = 1.0 / (source_theta ** (torch.arange(0, role_dim, 2, dtype=torch.float32) / role_dim))
+    ang = sid.unsqueeze(-1) * inv_freq
+    cos_half[..., : role_dim // 2] = torch.cos(ang)
+    sin_half[..., : role_dim // 2] = torch.sin(ang)
+    cr = cos_half.repeat_interleave(2, dim=-1)
+    sr = sin_half.repeat_interleave(2, dim=-1)
+    return cos3 * cr - sin3 * sr, sin3 * cr + cos3 * sr
+
+
+def half_tables(cos_full: torch.Tensor, sin_full: torch.Tensor):
+    """[L, D] -> [L, D/2] by taking every other column (sgl_fused_ops.py:87-89)."""
+    return cos_full[..., ::2].contiguous(), sin_full[..., ::2].contiguous()
+
+
+def qk_norm_rope_grid_f32(x, w, num_frames, grid_h, grid_w, t0, rope_dims, theta, eps,
+                          source_id=0.0, source_theta=256.0):
+    """Grid-mode oracle: the table-mode formula fed with fp32 (unrounded) tables."""
+    cos, sin = half_tables(*rope_grid_tables(num_frames, grid_h, grid_w, t0, rope_dims, theta,
+                                             source_id, source_theta))
+    return qk_norm_rope_f32(x, w, cos, sin, eps)
+
+
+def ring_slots(num_frames: int, cache_slots: int, slot_start: int) -> list[int]:
+    """Cache frame slot of each chunk frame: (slot_start + f) % cache_slots."""
+    return [(slot_start + f) % cache_slots for f in range(num_frames)]
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm -> FP8 (per token / per 1x128 block): rmsnorm.cu:41-60 in fp32
+# (no rounding to the input type) followed by per_token_quant_fp8.cu:56-82.
+# ---------------------------------------------------------------------------
+def rmsnorm_quant_fp8(x, w, eps: float, group_size: int = 0, v: torch.Tensor | None = None):
+    """Returns (q uint8 [M, N], s fp32 [M] or [M, N/128], v fp32 [M, N])."""
+    if v is None:
+        v = rmsnorm_f32(x, w, eps)
+    M, N = v.shape
+    if group_size == 0:
+        scale, inv = scale_and_inv(nan_ignoring_amax(v))
+        return fp8_quant_with_inv(v, inv[:, None]), scale, v
+    g = v.reshape(M, N // group_size, group_size)
+    scale, inv = scale_and_inv(nan_ignoring_amax(g))
+    return fp8_quant_with_inv(g, inv[..., None]).reshape(M, N), scale, v

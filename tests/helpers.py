@@ -1,0 +1,76 @@
+"""Comparison helpers shared by the parity tests."""
+from __future__ import annotations
+
+import torch
+
+
+def bf16_ulp(ref: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 numbers at |ref| (8 significant bits), floored at the smallest normal."""
+    a = ref.abs().float().clamp_min(2.0 ** -126)
+    return torch.exp2(torch.floor(torch.log2(a)) - 7)
+
+
+def assert_bf16_within_ulp(out: torch.Tensor, ref_f32: torch.Tensor, floor_scale=None,
+                           n_ulp: float = 1.0, what: str = ""):
+    """|out - ref| <= n_ulp bf16 ulps of ref, element-wise.
+
+    The fp32 reference and the kernel accumulate in different orders; where a
+    result is the difference of nearly equal terms (a rotated pair, x - mean)
+    the fp32 rounding of the terms dominates a tiny result. `floor_scale`
+    (a tensor broadcastable to ref, e.g. the row/head max |ref|) floors the
+    ulp at that of floor_scale * 2^-10 to absorb that cancellation.
+    """
+    out = out.float().cpu()
+    ref = ref_f32.float().cpu()
+    ulp = bf16_ulp(ref)
+    if floor_scale is not None:
+        ulp = torch.maximum(ulp, bf16_ulp(floor_scale.float().cpu() * 2.0 ** -10))
+    err = (out - ref).abs()
+    nan_ok = torch.isnan(out) == torch.isnan(ref)
+    assert bool(nan_ok.all()), f"{what}: NaN pattern differs"
+    fin = torch.isfinite(ref)
+    bad = (err > n_ulp * ulp) & fin
+    if bool(bad.any()):
+        i = int(bad.reshape(-1).nonzero()[0])
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} elements beyond {n_ulp} bf16 ulp; first at flat index {i}: "
+            f"out={out.reshape(-1)[i].item()!r} ref={ref.reshape(-1)[i].item()!r} "
+            f"ulp={ulp.reshape(-1)[i].item()!r}; max err/ulp={(err / ulp)[fin].max().item():.3f}")
+
+
+def f32_ulp(v: torch.Tensor) -> torch.Tensor:
+    a = v.abs().float().clamp_min(2.0 ** -126)
+    return torch.exp2(torch.floor(torch.log2(a)) - 23)
+
+
+MANTISSA_BITS = {torch.bfloat16: 7, torch.float16: 10, torch.float32: 23}
+
+
+def assert_within_ulp(out: torch.Tensor, ref_f32: torch.Tensor, dtype, floor_scale=None,
+                      n_ulp: float = 1.0, what: str = ""):
+    """Like assert_bf16_within_ulp for any output dtype (bf16: 7, fp16: 10,
+    fp32: 23 fraction bits). fp32 outputs are allowed n_ulp * 8 ulps, the
+    spread of fp32 sums accumulated in different orders."""
+    mb = MANTISSA_BITS[dtype]
+    out = out.float().cpu()
+    ref = ref_f32.float().cpu()
+
+    def ulp_of(v):
+        a = v.abs().clamp_min(2.0 ** -126)
+        return torch.exp2(torch.floor(torch.log2(a)) - mb)
+
+    ulp = ulp_of(ref)
+    if floor_scale is not None:
+        ulp = torch.maximum(ulp, ulp_of(floor_scale.float().cpu() * 2.0 ** -10))
+    if dtype == torch.float32:
+        n_ulp = n_ulp * 8
+    err = (out - ref).abs()
+    fin = torch.isfinite(ref)
+    assert bool((torch.isnan(out) == torch.isnan(ref)).all()), f"{what}: NaN pattern differs"
+    bad = (err > n_ulp * ulp) & fin
+    if bool(bad.any()):
+        i = int(bad.reshape(-1).nonzero()[0])
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} of {bad.numel()} elements beyond {n_ulp} ulp ({dtype}); "
+            f"first at flat index {i}: out={out.reshape(-1)[i].item()!r} "
+            f"ref={ref.reshape(-1)[i].item()!r}; max err/ulp={(err / ulp)[fin].max().item():.3f}")

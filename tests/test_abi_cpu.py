@@ -1,0 +1,164 @@
+"""CPU tests of the boundary: the C ABI library loads and exports every entry
+point of include/joyomni_hip.h, the ctypes binding matches the header, the
+validation errors come back as status codes without touching a GPU, and the
+torch op library registers the reference's schemas byte-for-byte."""
+from __future__ import annotations
+
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "joyomni_hip.h"
+
+
+def header_functions() -> dict[str, int]:
+    """name -> number of parameters, for every function declared in the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:int|const char\*)\s+(jo_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else len(params.split(","))
+    return out
+
+
+def test_header_declares_all_entry_points():
+    fns = header_functions()
+    for name in ("jo_last_error", "jo_abi_version", "jo_sgl_per_token_quant_fp8",
+                 "jo_fused_qk_norm_rope_3d_paired", "jo_fused_qk_norm_rope_3d_grid",
+                 "jo_fused_qk_norm_rope_3d_kvcache", "jo_fused_norm_scale_shift", "jo_rmsnorm",
+                 "jo_fused_add_layernorm_scale_shift", "jo_rmsnorm_quant_fp8"):
+        assert name in fns, name
+
+
+def test_library_exports_every_header_symbol(abi):
+    lib = abi.lib()
+    for name in header_functions():
+        assert hasattr(lib, name), f"{name} not exported by {abi.lib_path()}"
+    nm = subprocess.run(["nm", "-D", "--defined-only", abi.lib_path()], capture_output=True,
+                        text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in nm.splitlines() if " T " in ln}
+    assert set(header_functions()) <= exported
+
+
+def test_ctypes_signatures_match_header(abi):
+    fns = header_functions()
+    for name, argtypes in abi.SIGNATURES.items():
+        assert fns[name] == len(argtypes), name
+    assert set(abi.SIGNATURES) == set(fns) - {"jo_last_error", "jo_abi_version"}
+
+
+def test_abi_version(abi):
+    assert abi.lib().jo_abi_version() == 1
+
+
+# Validation paths return before any HIP call, so they run without a GPU.
+BAD_CALLS = [
+    ("jo_sgl_per_token_quant_fp8", (8, 0, 4, 8, 8, 8, 8, 8, None), "bf16 or fp16"),
+    ("jo_sgl_per_token_quant_fp8", (8, 2, 4, 6, 6, 8, 6, 8, None), "divisible by 4"),
+    ("jo_sgl_per_token_quant_fp8", (None, 2, 4, 8, 8, 8, 8, 8, None), "null pointer"),
+    ("jo_sgl_per_token_quant_fp8", (8, 2, 4, 8, 4, 8, 8, 8, None), "row stride"),
+    ("jo_fused_qk_norm_rope_3d_paired",
+     (16, 16, 1, 4, 2, 96, 768, 192, 768, 192, 1e-6, 16, 16, 16, 16, None), "head_dim"),
+    ("jo_fused_qk_norm_rope_3d_paired",
+     (16, 16, 1, 4, 2, 128, 1024, 256, 1024, 256, 1e-6, 16, 16, None, 16, None), "cos/sin"),
+    ("jo_fused_qk_norm_rope_3d_paired",
+     (16, 16, 1, 4, 2, 128, 1024, 250, 1024, 256, 1e-6, 16, 16, 16, 16, None), "token stride"),
+    ("jo_fused_qk_norm_rope_3d_grid",
+     (16, 16, 1, 10, 2, 128, 2560, 256, 2560, 256, 1e-6, 16, 16, 16, 11, 21, 3, 3, 0, 0.0, None),
+     "whole number"),
+    ("jo_fused_qk_norm_rope_3d_grid",
+     (16, 16, 1, 9, 2, 128, 2304, 256, 2304, 256, 1e-6, 16, 16, 16, 40, 30, 3, 3, 0, 0.0, None),
+     "pairs_t"),
+    ("jo_fused_qk_norm_rope_3d_kvcache",
+     (16, 16, 16, 1, 9, 2, 128, 2304, 256, 2304, 256, 4608, 256, 1, 0, 1e-6, 16, 16, 16, 22, 21,
+      3, 3, 0, 0.0, None), None),  # 1 frame, 1 slot: valid geometry, but null-free pointers -> ok check below
+    ("jo_fused_qk_norm_rope_3d_kvcache",
+     (16, 16, 16, 1, 18, 2, 128, 4608, 256, 4608, 256, 4608, 256, 1, 0, 1e-6, 16, 16, 16, 22, 21,
+      3, 3, 0, 0.0, None), "more frames"),
+    ("jo_fused_qk_norm_rope_3d_kvcache",
+     (16, 16, 16, 1, 9, 2, 128, 2304, 256, 2304, 256, 4608, 256, 2, 2, 1e-6, 16, 16, 16, 22, 21,
+      3, 3, 0, 0.0, None), "slot_start"),
+    ("jo_fused_norm_scale_shift", (16, 8, None, None, 16, 8, 16, 8, 16, 8, 4, 8, 2, 2, 1e-6, None),
+     "norm_type"),
+    ("jo_fused_norm_scale_shift", (16, 6, None, None, 16, 6, 16, 6, 16, 6, 4, 6, 2, 0, 1e-6, None),
+     "divisible by 4"),
+    ("jo_fused_norm_scale_shift", (16, 8, None, None, 16, 8, 16, 8, 16, 8, 4, 8, 7, 0, 1e-6, None),
+     "dtype"),
+    ("jo_rmsnorm", (16, 8, 16, None, 8, 4, 8, 2, 1e-6, None), "null pointer"),
+    ("jo_fused_add_layernorm_scale_shift",
+     (16, 12, 16, 12, None, 0, None, None, 16, 0, 16, 0, 16, 8, 4, 12, 2, 1e-6, None),
+     "bad row stride"),
+    ("jo_rmsnorm_quant_fp8", (16, 256, 16, 16, 256, 16, 4, 256, 2, 1e-6, 64, None), "group_size"),
+    ("jo_rmsnorm_quant_fp8", (16, 200, 16, 16, 200, 16, 4, 200, 2, 1e-6, 128, None), "divisible by 128"),
+    ("jo_rmsnorm_quant_fp8", (16, 256, 16, 16, 256, 16, 4, 256, 0, 1e-6, 0, None), "bf16 or fp16"),
+]
+
+
+@pytest.mark.parametrize("name,args,msg", [b for b in BAD_CALLS if b[2] is not None])
+def test_validation_errors_without_gpu(abi, name, args, msg):
+    status = getattr(abi.lib(), name)(*args)
+    assert status == abi.JO_ERR_INVALID
+    assert msg in abi.last_error()
+
+
+def test_empty_inputs_are_noops(abi):
+    lib = abi.lib()
+    # zero rows / zero tokens: valid, nothing to launch
+    assert lib.jo_sgl_per_token_quant_fp8(None, 2, 0, 8, 8, None, 8, None, None) == abi.JO_OK
+    assert lib.jo_rmsnorm(None, 8, None, None, 8, 0, 8, 2, 1e-6, None) == abi.JO_OK
+    assert lib.jo_fused_norm_scale_shift(None, 8, None, None, None, 0, None, 0, None, 8, 0, 8, 2,
+                                         0, 1e-6, None) == abi.JO_OK
+    assert lib.jo_fused_qk_norm_rope_3d_paired(None, None, 1, 0, 2, 128, 0, 256, 0, 256, 1e-6,
+                                               None, None, None, None, None) == abi.JO_OK
+
+
+REFERENCE_SCHEMAS = {
+    # deploy/joyomni_ops/csrc/pybind.cpp:35-43, verbatim.
+    "fused_qk_norm_rope_3d_paired":
+        "fused_qk_norm_rope_3d_paired(Tensor! q, Tensor! k, int seq_len, int num_heads, float eps, "
+        "Tensor q_weight, Tensor k_weight, Tensor cos, Tensor sin) -> ()",
+    "fused_norm_scale_shift":
+        "fused_norm_scale_shift(Tensor x, Tensor? gamma_opt, Tensor? beta_opt, "
+        "Tensor scale, Tensor shift, int norm_type, float eps) -> Tensor",
+    "rmsnorm": "rmsnorm(Tensor x, Tensor weight, float eps) -> Tensor",
+    "sgl_per_token_quant_fp8":
+        "sgl_per_token_quant_fp8(Tensor input, Tensor! output_q, Tensor! output_s) -> ()",
+}
+
+
+def test_torch_ops_register_reference_schemas():
+    import joyomni_ops as jo  # noqa: F401  (loads _C.so)
+    for name, schema in REFERENCE_SCHEMAS.items():
+        expected = torch._C.parse_schema("joyomni_ops::" + schema)
+        assert getattr(torch.ops.joyomni_ops, name).default._schema == expected, name
+    for name in ("fused_qk_norm_rope_3d_grid", "fused_qk_norm_rope_3d_kvcache",
+                 "fused_add_layernorm_scale_shift", "rmsnorm_quant_fp8"):
+        assert hasattr(torch.ops.joyomni_ops, name)
+    assert not jo.has_fp8()
+
+
+def test_ops_have_no_cpu_kernel():
+    """The product has no CPU path: CPU tensors are rejected by the dispatcher."""
+    import joyomni_ops as jo
+    x = torch.randn(4, 8, dtype=torch.bfloat16)
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        jo.rmsnorm(x, torch.ones(8, dtype=torch.bfloat16))
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        jo.sgl_per_token_quant_fp8(x, torch.empty(4, 8, dtype=torch.float8_e4m3fn),
+                                   torch.empty(4))
+
+
+def test_wrapper_norm_type_mapping_matches_reference():
+    """'layer'->0, 'rms'->1, anything else -> -1 (rejected), __init__.py:38-41."""
+    import inspect
+
+    import joyomni_ops as jo
+    src = inspect.getsource(jo.fused_norm_scale_shift)
+    assert '0 if norm_type == "layer" else 1 if norm_type == "rms" else -1' in src
+    sig = inspect.signature(jo.fused_norm_scale_shift)
+    assert sig.parameters["eps"].default == 1e-5
+    assert inspect.signature(jo.rmsnorm).parameters["eps"].default == 1e-6

@@ -1,0 +1,175 @@
+"""GPU parity of the FP8 quantization ops through the C ABI (and the torch op).
+
+Bar: bit-exact e4m3fn bytes and bit-exact fp32 scales against the CPU oracle
+(per_token_quant_fp8.cu:56-82 restated in oracle/ops.py, itself pinned by the
+C brute-force encoder), on random rows with outliers, hand known-answer rows,
+every row-shape dispatch class, strided and unaligned views, and the full C1
+shape. RMSNorm->FP8 (C4) compares scales within 2 fp32 ulps and bytes exactly
+after re-quantizing the oracle's fp32 values with the GPU's scales, except on
+provable near-ties of the fp32 sums.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import kat
+from oracle import fp8ref, ops
+from joyomni_ops import workloads as W
+from helpers import f32_ulp
+
+pytestmark = pytest.mark.gpu
+
+
+def quant_gpu(abi, stream, x_dev, M=None, K=None, in_stride=None):
+    M = x_dev.shape[0] if M is None else M
+    K = x_dev.shape[1] if K is None else K
+    q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=x_dev.device)
+    s = torch.full((M,), -1.0, dtype=torch.float32, device=x_dev.device)
+    abi.call("jo_sgl_per_token_quant_fp8", x_dev.data_ptr(), abi.dtype_code(x_dev.dtype), M, K,
+             x_dev.stride(0) if in_stride is None else in_stride, q.data_ptr(), K, s.data_ptr(),
+             stream)
+    torch.cuda.synchronize()
+    return q.view(torch.uint8).cpu(), s.cpu()
+
+
+def assert_quant_equal(q, s, x_cpu, what):
+    qo, so = ops.per_token_quant_fp8(x_cpu)
+    nbad = int((q != qo).sum())
+    assert nbad == 0, f"{what}: {nbad} fp8 bytes differ from the oracle"
+    assert torch.equal(s, so) or bool(((s == so) | (torch.isinf(s) & torch.isinf(so))).all()), \
+        f"{what}: scales differ"
+
+
+SHAPES = [(1, 4), (3, 12), (7, 64), (33, 128), (5, 256), (9, 512), (17, 1000), (17, 3072),
+          (64, 4096), (9, 8192), (3, 16384), (2, 32768), (2, 40000), (5, 100), (4, 1020), (1, 8)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,K", SHAPES)
+def test_quant_random_rows(abi, dev, stream_handle, dtype, M, K):
+    g = torch.Generator().manual_seed(M * 100003 + K)
+    x = W.with_outliers(torch.randn(M, K, generator=g), g).to(dtype)
+    q, s = quant_gpu(abi, stream_handle, x.to(dev))
+    assert_quant_equal(q, s, x, f"{dtype} [{M},{K}]")
+
+
+def test_quant_known_answer_rows(abi, dev, stream_handle):
+    rows = [r for r, _, _ in kat.KAT_ROWS]
+    x = torch.tensor(rows, dtype=torch.float32).to(torch.bfloat16)
+    for width in (8, 64, 3072):  # replicate each row to hit several kernel shapes
+        xr = x.repeat(1, width // 8)
+        q, s = quant_gpu(abi, stream_handle, xr.to(dev))
+        for i, (_, scale, codes) in enumerate(kat.KAT_ROWS):
+            assert q[i].tolist() == codes * (width // 8), f"KAT row {i} width {width}"
+            assert s[i].item() == np.float32(scale) or (np.isinf(scale) and np.isinf(s[i].item()))
+
+
+def test_quant_strided_and_unaligned_views(abi, dev, stream_handle):
+    g = torch.Generator().manual_seed(11)
+    big = W.with_outliers(torch.randn(40, 3200, generator=g), g).to(torch.bfloat16)
+    bd = big.to(dev)
+    # row-strided view (16-byte aligned rows): vector path
+    q, s = quant_gpu(abi, stream_handle, bd[:, :3072])
+    assert_quant_equal(q, s, big[:, :3072], "strided")
+    # view starting 1 element in: unaligned, generic path
+    q, s = quant_gpu(abi, stream_handle, bd[:, 1:1 + 3072])
+    assert_quant_equal(q, s, big[:, 1:1 + 3072], "unaligned")
+
+
+def test_quant_full_c1(abi, dev, stream_handle):
+    cfg = W.CONFIGS["C1"]
+    x = W.make_inputs(cfg)["x"]
+    q, s = quant_gpu(abi, stream_handle, x.to(dev))
+    assert_quant_equal(q, s, x, "C1 [10530,3072]")
+    # cross-check with the C restatement as well
+    qc, sc = fp8ref.per_token_quant(x[:512].float().numpy())
+    assert (q[:512].numpy() == qc).all() and (s[:512].numpy() == sc).all()
+
+
+def test_quant_torch_op_matches_abi(dev):
+    import joyomni_ops as jo
+    g = torch.Generator().manual_seed(12)
+    x = W.with_outliers(torch.randn(300, 4096, generator=g), g).to(torch.bfloat16)
+    xq = torch.empty(300, 4096, dtype=torch.float8_e4m3fn, device=dev)
+    xs = torch.empty(300, 1, dtype=torch.float32, device=dev)  # Fp8Linear's [M, 1] scales
+    jo.sgl_per_token_quant_fp8(x.to(dev), xq, xs)
+    torch.cuda.synchronize()
+    assert_quant_equal(xq.view(torch.uint8).cpu(), xs.view(-1).cpu(), x, "torch op")
+    with pytest.raises(RuntimeError):
+        jo.sgl_per_token_quant_fp8(x.to(dev), torch.empty(300, 4096, dtype=torch.uint8, device=dev), xs)
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm -> FP8
+# ---------------------------------------------------------------------------
+def rms_quant_gpu(abi, stream, x_dev, w_dev, eps, group):
+    M, N = x_dev.shape
+    q = torch.empty(M, N, dtype=torch.float8_e4m3fn, device=x_dev.device)
+    s = torch.empty((M,) if group == 0 else (M, N // group), dtype=torch.float32,
+                    device=x_dev.device)
+    abi.call("jo_rmsnorm_quant_fp8", x_dev.data_ptr(), x_dev.stride(0), w_dev.data_ptr(),
+             q.data_ptr(), N, s.data_ptr(), M, N, abi.dtype_code(x_dev.dtype), eps, group, stream)
+    torch.cuda.synchronize()
+    return q.view(torch.uint8).cpu(), s.cpu()
+
+
+def check_rms_quant(q, s, x, w, eps, group, what):
+    _, so, v = ops.rmsnorm_quant_fp8(x, w, eps, group)
+    # scales: amax/448 of fp32 values whose row sums were accumulated in a
+    # different order -> within 2 fp32 ulps
+    ds = (s - so).abs()
+    assert bool((ds <= 2 * f32_ulp(so)).all()), f"{what}: scale off by {(ds / f32_ulp(so)).max()} ulp"
+    # bytes: re-quantize the oracle's fp32 values with the GPU's scales
+    sg = s if group == 0 else s.reshape(-1)
+    inv = torch.where(sg == 0, torch.zeros_like(sg), 1.0 / sg)
+    if group == 0:
+        qo = ops.fp8_quant_with_inv(v, inv[:, None])
+    else:
+        M, N = v.shape
+        qo = ops.fp8_quant_with_inv(v.reshape(M, N // group, group),
+                                    inv.reshape(M, N // group, 1)).reshape(M, N)
+    diff = q != qo
+    n = int(diff.sum())
+    if n:
+        # Only near-ties may differ: the oracle's value must sit within 8 fp32
+        # ulps of a rounding midpoint, and the codes must be neighbours.
+        t = (v * (inv[:, None] if group == 0 else inv.reshape(v.shape[0], -1).repeat_interleave(group, 1)))[diff]
+        dec = torch.from_numpy(np.array([fp8ref.decode(k) for k in range(256)])).float()
+        a, b = dec[q[diff].long()], dec[qo[diff].long()]
+        mid = (a + b) / 2
+        assert bool(((t - mid).abs() <= 8 * f32_ulp(t)).all()), f"{what}: non-tie byte mismatch"
+        assert n <= max(4, v.numel() // 100000), f"{what}: {n} near-tie mismatches"
+
+
+@pytest.mark.parametrize("group", [0, 128])
+@pytest.mark.parametrize("M,N", [(1, 128), (7, 256), (33, 1024), (17, 3072), (5, 4096),
+                                 (3, 16384), (2, 24576)])
+def test_rmsnorm_quant_random(abi, dev, stream_handle, group, M, N):
+    g = torch.Generator().manual_seed(M * 7 + N + group)
+    x = W.with_outliers(torch.randn(M, N, generator=g), g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    q, s = rms_quant_gpu(abi, stream_handle, x.to(dev), w.to(dev), 1e-6, group)
+    check_rms_quant(q, s, x, w, 1e-6, group, f"[{M},{N}] g{group}")
+
+
+@pytest.mark.parametrize("name", ["C4_4725_tok", "C4_4725_blk", "C4_10530_tok", "C4_10530_blk"])
+def test_rmsnorm_quant_full_c4(abi, dev, stream_handle, name):
+    cfg = W.CONFIGS[name]
+    t = W.make_inputs(cfg)
+    q, s = rms_quant_gpu(abi, stream_handle, t["x"].to(dev), t["weight"].to(dev),
+                         cfg.dims["eps"], cfg.dims["group"])
+    check_rms_quant(q, s, t["x"], t["weight"], cfg.dims["eps"], cfg.dims["group"], name)
+
+
+def test_rmsnorm_quant_torch_op(dev):
+    import joyomni_ops as jo
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(64, 3072, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(3072, generator=g)).to(torch.bfloat16)
+    q = torch.empty(64, 3072, dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty(64, 24, dtype=torch.float32, device=dev)
+    jo.rmsnorm_quant_fp8(x.to(dev), w.to(dev), 1e-6, q, s, 128)
+    torch.cuda.synchronize()
+    check_rms_quant(q.view(torch.uint8).cpu(), s.cpu(), x, w, 1e-6, 128, "torch op")

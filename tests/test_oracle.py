@@ -1,0 +1,254 @@
+"""CPU tests that pin the oracle before it is trusted as the parity checker.
+
+The reference ships no golden vectors (its tests print fp32-formula diffs), so
+each oracle function is checked against something independent of it: hand
+known answers, a brute-force C encoder, torch library routines, complex
+arithmetic, float64 closed forms and invariants. A few tests plant a mistake
+in a copy of the oracle and show the check catches it.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import fp8ref, ops
+import kat
+
+
+# ---------------------------------------------------------------------------
+# FP8 encoding and per-token quantization
+# ---------------------------------------------------------------------------
+def test_kat_table_is_self_consistent():
+    kat.check_table()
+
+
+@pytest.mark.parametrize("idx", range(len(kat.KAT_ROWS)))
+def test_quant_kat_rows(idx):
+    row, scale, codes = kat.KAT_ROWS[idx]
+    x = torch.tensor([row], dtype=torch.float32).to(torch.bfloat16)
+    assert torch.equal(x.float(), torch.tensor([row], dtype=torch.float32), ) or any(
+        math.isnan(v) for v in row)
+    q, s = ops.per_token_quant_fp8(x)
+    assert q[0].tolist() == codes
+    exp_s = torch.tensor(scale, dtype=torch.float32)
+    assert torch.equal(s[0], exp_s) or (math.isinf(scale) and math.isinf(s[0].item()))
+    qc, sc = fp8ref.per_token_quant(x.float().numpy())
+    assert qc[0].tolist() == codes
+    assert sc[0] == np.float32(scale)
+
+
+def test_torch_cast_matches_bruteforce_on_all_bf16():
+    bits = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float()
+    v = bits[(bits.abs() <= 448)]
+    t = v.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    c = fp8ref.encode_array(v.numpy())
+    assert (t == c).all()
+
+
+def test_torch_cast_matches_bruteforce_on_midpoints_and_random():
+    vals = np.array([fp8ref.decode(k) for k in range(0, 0x7f)])
+    mids = ((vals[:-1] + vals[1:]) / 2).astype(np.float32)
+    # midpoints +- 1 fp32 ulp on both sides as well
+    near = np.concatenate([mids, np.nextafter(mids, np.float32(0)), np.nextafter(mids, np.float32(1e9))])
+    near = np.concatenate([near, -near]).astype(np.float32)
+    g = torch.Generator().manual_seed(0)
+    r = ((torch.rand(500_000, generator=g) * 2 - 1) * 448).numpy()
+    for arr in (near, r):
+        t = torch.from_numpy(arr).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        assert (t == fp8ref.encode_array(arr)).all()
+
+
+def test_quant_oracle_matches_c_on_random_rows_with_outliers():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(300, 3072, generator=g)
+    from joyomni_ops.workloads import with_outliers
+    x = with_outliers(x, g).to(torch.bfloat16)
+    q, s = ops.per_token_quant_fp8(x)
+    qc, sc = fp8ref.per_token_quant(x.float().numpy())
+    assert (q.numpy() == qc).all() and (s.numpy() == sc).all()
+    # and every code decodes to within half a code step of the fp32 x*inv
+    inv = torch.where(s == 0, torch.zeros_like(s), 1.0 / s)
+    dec = torch.from_numpy(np.array([fp8ref.decode(k) for k in range(256)]))
+    err = (dec[q.long()] - (x.float() * inv[:, None]).double()).abs()
+    step = torch.where(dec[q.long()].abs() < 2 ** -6, torch.tensor(2.0 ** -9),
+                       dec[q.long()].abs() * 2.0 ** -3)
+    assert bool((err <= step / 2 + 1e-12).all())
+
+
+def test_planted_mistake_x_over_s_is_caught():
+    """x / s instead of x * (1/s) (a plausible slip) changes a few codes; the
+    C restatement of the reference rule disagrees with it."""
+    g = torch.Generator().manual_seed(2)
+    x = (torch.randn(2048, 3072, generator=g) * 3).to(torch.bfloat16)
+    q, s = ops.per_token_quant_fp8(x)
+    xf = x.float()
+    qc, _ = fp8ref.per_token_quant(xf.numpy())
+    assert (q.numpy() == qc).all()
+    wrong = torch.fmax(torch.fmin(xf / s[:, None], torch.tensor(448.0)), torch.tensor(-448.0))
+    wrong = wrong.to(torch.float8_e4m3fn).view(torch.uint8)
+    n_diff = int((wrong.numpy() != qc).sum())
+    assert 0 < n_diff < xf.numel() // 1000
+    # a sign slip in the clamp is visible everywhere below zero
+    wrong2 = torch.fmax(torch.fmin(xf * (1 / s[:, None]), torch.tensor(448.0)),
+                        torch.tensor(448.0)).to(torch.float8_e4m3fn).view(torch.uint8)
+    assert (wrong2.numpy() != qc).any()
+
+
+def test_group_quant_oracle_matches_c():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(40, 1024, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(1024, generator=g)).to(torch.bfloat16)
+    for group in (0, 128):
+        q, s, v = ops.rmsnorm_quant_fp8(x, w, 1e-6, group)
+        if group == 0:
+            qc, sc = fp8ref.per_token_quant(v.numpy())
+        else:
+            qc, sc = fp8ref.group_quant(v.numpy(), group)
+        assert (q.numpy() == qc).all() and (s.numpy() == sc).all()
+
+
+# ---------------------------------------------------------------------------
+# Norms
+# ---------------------------------------------------------------------------
+def test_rmsnorm_oracle_matches_library_and_invariant():
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(64, 512, generator=g)
+    w = torch.randn(512, generator=g)
+    ref = F.rms_norm(x, (512,), w, eps=1e-6)
+    assert torch.allclose(ops.rmsnorm_f32(x, w, 1e-6), ref, rtol=1e-5, atol=1e-6)
+    unit = ops.rmsnorm_f32(x, torch.ones(512), 0.0)
+    assert torch.allclose(unit.pow(2).mean(-1), torch.ones(64), rtol=1e-5)
+
+
+@pytest.mark.parametrize("affine", [False, True])
+def test_layernorm_modulate_oracle_matches_library(affine):
+    g = torch.Generator().manual_seed(5)
+    M, N = 32, 256
+    x = torch.randn(M, N, generator=g) * 3 + 1
+    gamma = torch.randn(N, generator=g) if affine else None
+    beta = torch.randn(N, generator=g) if affine else None
+    sc = torch.randn(M, N, generator=g)
+    sh = torch.randn(M, N, generator=g)
+    ref = F.layer_norm(x.double(), (N,), None if gamma is None else gamma.double(),
+                       None if beta is None else beta.double(), eps=1e-5)
+    ref = ref * (1 + sc.double()) + sh.double()
+    out = ops.norm_scale_shift_f32(x, gamma, beta, sc, sh, 0, 1e-5)
+    assert torch.allclose(out.double(), ref, rtol=1e-5, atol=1e-5)
+    # RMS flavour vs F.rms_norm
+    ref_rms = F.rms_norm(x.double(), (N,), None if gamma is None else gamma.double(), eps=1e-5)
+    ref_rms = ref_rms * (1 + sc.double()) + sh.double()
+    out_rms = ops.norm_scale_shift_f32(x, gamma, beta, sc, sh, 1, 1e-5)
+    assert torch.allclose(out_rms.double(), ref_rms, rtol=1e-5, atol=1e-5)
+
+
+def test_layernorm_beta_without_gamma_is_ignored_like_reference():
+    x = torch.randn(4, 16)
+    sc = torch.zeros(4, 16)
+    sh = torch.zeros(4, 16)
+    a = ops.norm_scale_shift_f32(x, None, torch.ones(16), sc, sh, 0, 1e-6)
+    b = ops.norm_scale_shift_f32(x, None, None, sc, sh, 0, 1e-6)
+    assert torch.equal(a, b)
+
+
+def test_add_layernorm_oracle_is_addcmul_then_layernorm():
+    g = torch.Generator().manual_seed(6)
+    M, N = 16, 384
+    x = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    gate = torch.randn(N, generator=g).to(torch.bfloat16)
+    sc = (0.2 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    sh = (0.2 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    new_res, y = ops.add_layernorm_scale_shift(x, res, gate, None, None, sc, sh, 1e-6)
+    ref_res = torch.addcmul(res.float(), x.float(), gate.float()).to(torch.bfloat16)
+    assert torch.equal(new_res, ref_res)
+    ref_y = F.layer_norm(ref_res.double(), (N,), eps=1e-6) * (1 + sc.double()) + sh.double()
+    assert torch.allclose(y.double(), ref_y, rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# QK norm + RoPE
+# ---------------------------------------------------------------------------
+def _complex_rope(xn, cos, sin):
+    """Rotation of interleaved pairs as complex multiplication (float64)."""
+    B, L, H, D = xn.shape
+    z = torch.view_as_complex(xn.double().reshape(B, L, H, D // 2, 2).contiguous())
+    rot = torch.complex(cos.double(), sin.double()).reshape(1, L, 1, D // 2)
+    return torch.view_as_real(z * rot).reshape(B, L, H, D)
+
+
+def test_qk_rope_oracle_is_complex_rotation():
+    g = torch.Generator().manual_seed(7)
+    B, L, H, D = 2, 9, 3, 64
+    x = torch.randn(B, L, H, D, generator=g)
+    w = torch.randn(D, generator=g)
+    ang = torch.randn(L, D // 2, generator=g) * 4
+    out = ops.qk_norm_rope_f32(x, w, ang.cos(), ang.sin(), 1e-6)
+    xn = F.rms_norm(x.double(), (D,), w.double(), eps=1e-6)
+    ref = _complex_rope(xn, ang.cos(), ang.sin())
+    assert torch.allclose(out.double(), ref, rtol=1e-5, atol=1e-5)
+    # norm preservation per pair and identity rotation
+    assert torch.allclose(out.reshape(B, L, H, D // 2, 2).norm(dim=-1).double(),
+                          xn.reshape(B, L, H, D // 2, 2).norm(dim=-1), rtol=1e-5, atol=1e-6)
+    ident = ops.qk_norm_rope_f32(x, w, torch.ones(L, D // 2), torch.zeros(L, D // 2), 1e-6)
+    assert torch.allclose(ident.double(), xn, rtol=1e-6, atol=1e-6)
+
+
+def test_planted_sign_mistake_in_rotation_is_caught():
+    g = torch.Generator().manual_seed(8)
+    B, L, H, D = 1, 5, 2, 64
+    x = torch.randn(B, L, H, D, generator=g)
+    w = torch.ones(D)
+    ang = torch.randn(L, D // 2, generator=g)
+    xn = ops.rmsnorm_f32(x, w, 1e-6)
+    c = ang.cos().reshape(L, 1, D // 2)
+    s = ang.sin().reshape(L, 1, D // 2)
+    wrong = torch.empty_like(xn)
+    wrong[..., 0::2] = xn[..., 0::2] * c + xn[..., 1::2] * s   # sign slip
+    wrong[..., 1::2] = xn[..., 0::2] * s + xn[..., 1::2] * c
+    ref = _complex_rope(xn, ang.cos(), ang.sin())
+    assert not torch.allclose(wrong.double(), ref, rtol=1e-3, atol=1e-3)
+
+
+def test_rope_grid_tables_closed_form():
+    frames, gh, gw, t0 = 2, 5, 7, 21
+    dims = (44, 42, 42)
+    cos, sin = ops.rope_grid_tables(frames, gh, gw, t0, dims, 10000.0)
+    L, D = cos.shape
+    assert (L, D) == (frames * gh * gw, 128)
+    n = torch.arange(L)
+    t = (t0 + n // (gh * gw)).double()
+    h = ((n % (gh * gw)) // gw).double()
+    w = (n % gw).double()
+    cols_c, cols_s = [], []
+    for dim, pos in zip(dims, (t, h, w)):
+        f = 1.0 / (10000.0 ** (torch.arange(0, dim, 2).double() / dim))
+        a = pos[:, None] * f[None, :]
+        cols_c.append(a.cos().repeat_interleave(2, 1))
+        cols_s.append(a.sin().repeat_interleave(2, 1))
+    ref_c, ref_s = torch.cat(cols_c, 1), torch.cat(cols_s, 1)
+    # fp32 angle rounding at |angle| <= 77 rad moves cos/sin by < 1e-5
+    assert torch.allclose(cos.double(), ref_c, atol=2e-5)
+    assert torch.allclose(sin.double(), ref_s, atol=2e-5)
+    assert torch.allclose(cos.double() ** 2 + sin.double() ** 2, torch.ones(L, D, dtype=torch.float64), atol=1e-6)
+
+
+def test_source_id_composition_is_angle_addition():
+    frames, gh, gw, t0 = 1, 3, 4, 5
+    dims = (16, 56, 56)
+    c0, s0 = ops.rope_grid_tables(frames, gh, gw, t0, dims, 256.0)
+    c1, s1 = ops.rope_grid_tables(frames, gh, gw, t0, dims, 256.0, source_id=2.0, source_theta=256.0)
+    a0 = torch.atan2(s0.double(), c0.double())
+    fr = 1.0 / (256.0 ** (torch.arange(0, 128, 2).double() / 128))
+    ar = (2.0 * fr).repeat_interleave(2)
+    ref_c, ref_s = torch.cos(a0 + ar), torch.sin(a0 + ar)
+    assert torch.allclose(c1.double(), ref_c, atol=1e-5)
+    assert torch.allclose(s1.double(), ref_s, atol=1e-5)
+
+
+def test_ring_slots():
+    assert ops.ring_slots(3, 7, 0) == [0, 1, 2]
+    assert ops.ring_slots(3, 7, 6) == [6, 0, 1]
