@@ -71,7 +71,10 @@ __device__ __forceinline__ float elem<F16>(const u32x4& c, int j) {
 }
 template <>
 __device__ __forceinline__ float elem<F32>(const u32x4& c, int j) {
-  return __builtin_bit_cast(float, c[j]);
+  // Copy the element out first: __builtin_bit_cast applied directly to an
+  // ext-vector element expression reads element 0 with this compiler.
+  const uint32_t w = c[j];
+  return __builtin_bit_cast(float, w);
 }
 
 // All kVec elements of a chunk as fp32.
@@ -208,6 +211,67 @@ __device__ __forceinline__ float allreduce(float v) {
   if constexpr (W >= 32) v = Op::apply(v, swizzle_xor16(v));
   if constexpr (W == 64) v = Op::apply(readlane(v, 0), readlane(v, 32));
   return v;
+}
+
+// float64 sum over aligned groups of W lanes (W in {8, 16, 32, 64}); DPP and
+// swizzle move the two 32-bit halves separately. Every lane of a group ends
+// with bit-identical values (same argument as allreduce).
+template <int kCtrl>
+__device__ __forceinline__ double dpp64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(u & 0xffffffffu), kCtrl, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(u >> 32), kCtrl, 0xf, 0xf, false);
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                        static_cast<uint32_t>(lo));
+}
+__device__ __forceinline__ double swizzle_xor16_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_ds_swizzle(static_cast<int>(u & 0xffffffffu), 0x401f);
+  const int hi = __builtin_amdgcn_ds_swizzle(static_cast<int>(u >> 32), 0x401f);
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                        static_cast<uint32_t>(lo));
+}
+__device__ __forceinline__ double readlane64(double v, int lane) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(u & 0xffffffffu), lane);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(u >> 32), lane);
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+template <int W>
+__device__ __forceinline__ double allreduce_sum64(double v) {
+  static_assert(W == 8 || W == 16 || W == 32 || W == 64, "group width");
+  if constexpr (W == 8) {
+    v += dpp64<kDppHalfMirror>(v);
+  } else {
+    v += dpp64<kDppRor8>(v);
+    v += dpp64<kDppRor4>(v);
+  }
+  v += dpp64<kDppXor2>(v);
+  v += dpp64<kDppXor1>(v);
+  if constexpr (W >= 32) v += swizzle_xor16_f64(v);
+  if constexpr (W == 64) v = readlane64(v, 0) + readlane64(v, 32);
+  return v;
+}
+
+// float64 sum over LPR lanes of a 256-thread block; `slot` is __shared__ double[4].
+template <int LPR>
+__device__ __forceinline__ double row_reduce_sum64(double v, double* slot) {
+  if constexpr (LPR <= kWave) {
+    return allreduce_sum64<LPR>(v);
+  } else {
+    static_assert(LPR == 128 || LPR == 256, "lanes per row");
+    v = allreduce_sum64<kWave>(v);
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) slot[wave] = v;
+    __syncthreads();
+    constexpr int kWavesPerRow = LPR / kWave;
+    const int first = (wave / kWavesPerRow) * kWavesPerRow;
+    double r = slot[first];
+#pragma unroll
+    for (int i = 1; i < kWavesPerRow; ++i) r += slot[first + i];
+    return r;
+  }
 }
 
 // Reduction over LPR lanes of a 256-thread block (LPR in {8..256}). Groups

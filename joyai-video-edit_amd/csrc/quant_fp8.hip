@@ -111,9 +111,10 @@ int launch_quant(const void* x, int64_t M, int64_t N, int64_t xs, void* q, int64
 
 // ---------------------------------------------------------------------------
 // RMSNorm -> FP8. v = (x * r) * w in fp32 (rmsnorm.cu:41-60 without the
-// rounding to the input type), r = 1/sqrt(sum(x^2)/N + eps) with IEEE sqrt
-// and division; then the per_token_quant_fp8.cu:56-82 rule over the row
-// (GROUP == 0) or over each 1x128 block (GROUP == 128, 16 lanes x 8 values).
+// rounding to the input type), r = 1/sqrt(mean(x^2) + eps) with the mean
+// square rounded once from its exact value and IEEE sqrt and division; then
+// the per_token_quant_fp8.cu:56-82 rule over the row (GROUP == 0) or over
+// each 1x128 block (GROUP == 128, 16 lanes x 8 values).
 // ---------------------------------------------------------------------------
 template <class Tag, int LPR, int CH, int GROUP>
 __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
   static_assert(Tag::kVec == 8, "fp8 rows are built from 8-element chunks");
   static_assert(GROUP == 0 || (GROUP == 128 && LPR >= 16), "group layout");
   constexpr int RPB = kBlock / LPR;
-  __shared__ float red_ss[kBlock / kWave];
+  __shared__ double red_ss[kBlock / kWave];
   __shared__ float red_max[kBlock / kWave];
   const int lane = threadIdx.x % LPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
@@ -136,17 +137,22 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
     c[i] = (row_ok && e < N) ? ld16(byte_off(xr, static_cast<int64_t>(e) * Tag::kBytes))
                              : u32x4{0u, 0u, 0u, 0u};
   }
-  float ss = 0.f;
+  // The squares of bf16/fp16 values are exact in fp32; summing them in fp64
+  // makes the mean square the correctly rounded fp32 value of the exact
+  // mean, independent of the summation order. r then follows with two IEEE
+  // fp32 operations, so r, v and the scales do not depend on the launch shape.
+  double ss = 0.0;
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float v = elem<Tag>(c[i], j);
-      ss += v * v;
+      ss += static_cast<double>(v * v);
     }
   }
-  ss = row_reduce<LPR, OpSum>(ss, red_ss);
-  const float r = 1.0f / sqrtf(ss / static_cast<float>(N) + eps);
+  ss = row_reduce_sum64<LPR>(ss, red_ss);
+  const float ms = static_cast<float>(ss / static_cast<double>(N));
+  const float r = 1.0f / sqrtf(ms + eps);
 
   // v = (x * r) * w, kept in registers for the quantization pass.
   float v[CH][8];

@@ -61,6 +61,38 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     return rmsnorm_f32(x, w, eps).to(x.dtype)
 
 
+def f32_op(fn, *args: torch.Tensor) -> torch.Tensor:
+    """One IEEE binary32 operation (+, -, *, /, sqrt) on fp32 operands, evaluated
+    in float64 and rounded once to fp32. For these operations float64 carries
+    more than 2*24+2 bits, so the double rounding is innocuous and the result
+    is the correctly rounded fp32 value (torch's own CPU sqrt is not)."""
+    return fn(*(a.double() for a in args)).float()
+
+
+def rms_rstd_exact(x: torch.Tensor, eps: float) -> torch.Tensor:
+    """r = 1 / sqrt(ms + eps) with ms the exact mean square rounded once to fp32.
+
+    The reference sums x^2 in fp32 in its kernel's own order (rmsnorm.cu:47-53);
+    any fp32 sum lands within a few ulps of the exact value, in an
+    order-dependent way. This restatement takes the sum exactly (squares of
+    bf16/fp16 are exact in fp32, their float64 sum is exact to ~1e-16), rounds
+    the mean once to fp32, then applies the fp32 add of eps (eps itself as
+    fp32), an IEEE sqrt and an IEEE division.
+    """
+    xf = x.float()
+    ms = (xf.double().pow(2).sum(-1, keepdim=True) / xf.shape[-1]).float()
+    e = torch.tensor(eps, dtype=torch.float32)
+    t = f32_op(torch.add, ms, e)
+    s = f32_op(torch.sqrt, t)
+    return f32_op(torch.div, torch.ones_like(s), s)
+
+
+def rmsnorm_exact_f32(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """(x * r) * w in fp32 with r from rms_rstd_exact (order of rmsnorm.cu:57)."""
+    xr = f32_op(torch.mul, x.float(), rms_rstd_exact(x, eps))
+    return f32_op(torch.mul, xr, w.float())
+
+
 # ---------------------------------------------------------------------------
 # (Layer|RMS)Norm + AdaLN — deploy/joyomni_ops/csrc/fused_norm_scale_shift.cu:88-142;
 # formula of test_parity_light.py:47-51 / test_bench.py:91-96.
@@ -204,12 +236,13 @@ def ring_slots(num_frames: int, cache_slots: int, slot_start: int) -> list[int]:
 
 # ---------------------------------------------------------------------------
 # RMSNorm -> FP8 (per token / per 1x128 block): rmsnorm.cu:41-60 in fp32
-# (no rounding to the input type) followed by per_token_quant_fp8.cu:56-82.
+# (no rounding to the input type; exact mean square, see rms_rstd_exact)
+# followed by per_token_quant_fp8.cu:56-82 over each row or 1x128 block.
 # ---------------------------------------------------------------------------
 def rmsnorm_quant_fp8(x, w, eps: float, group_size: int = 0, v: torch.Tensor | None = None):
     """Returns (q uint8 [M, N], s fp32 [M] or [M, N/128], v fp32 [M, N])."""
     if v is None:
-        v = rmsnorm_f32(x, w, eps)
+        v = rmsnorm_exact_f32(x, w, eps)
     M, N = v.shape
     if group_size == 0:
         scale, inv = scale_and_inv(nan_ignoring_amax(v))

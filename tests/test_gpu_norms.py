@@ -109,9 +109,9 @@ def test_rmsnorm_strided_rows_abi(abi, dev, stream_handle):
     g = torch.Generator().manual_seed(3)
     big = torch.randn(M, N + 64, generator=g).to(torch.bfloat16)
     w = torch.randn(N, generator=g).to(torch.bfloat16)
-    bd = big.to(dev)
+    bd, wd = big.to(dev), w.to(dev)
     out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-    abi.call("jo_rmsnorm", bd.data_ptr(), N + 64, w.to(dev).data_ptr(), out.data_ptr(), N, M, N,
+    abi.call("jo_rmsnorm", bd.data_ptr(), N + 64, wd.data_ptr(), out.data_ptr(), N, M, N,
              abi.JO_DTYPE_BF16, 1e-6, stream_handle)
     torch.cuda.synchronize()
     ref = ops.rmsnorm_f32(big[:, :N], w, 1e-6)

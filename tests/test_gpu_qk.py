@@ -54,11 +54,13 @@ def test_table_mode(abi, dev, stream_handle, B, L, H, D, tables):
         dims = {64: (16, 24, 24), 128: (16, 56, 56), 256: (64, 96, 96)}[D]
         c, s = ops.half_tables(*ops.rope_grid_tables(1, 1, L, 3, dims, 256.0))
         cos, sin = c.to(torch.bfloat16), s.to(torch.bfloat16)
-    qd, kd = q.to(dev), k.to(dev)
+    # Device copies are kept in named variables: a temporary's memory would be
+    # returned to the caching allocator before the asynchronous kernel runs.
+    qd, kd, qwd, kwd, cd, sd = (t.to(dev) for t in (q, k, qw, kw, cos, sin))
     tok = H * D
     abi.call("jo_fused_qk_norm_rope_3d_paired", qd.data_ptr(), kd.data_ptr(), B, L, H, D, L * tok,
-             tok, L * tok, tok, 1e-6, qw.to(dev).data_ptr(), kw.to(dev).data_ptr(),
-             cos.to(dev).data_ptr(), sin.to(dev).data_ptr(), stream_handle)
+             tok, L * tok, tok, 1e-6, qwd.data_ptr(), kwd.data_ptr(), cd.data_ptr(), sd.data_ptr(),
+             stream_handle)
     torch.cuda.synchronize()
     check_qk(qd.cpu(), q, qw, cos, sin, B, L, H, D, "q")
     check_qk(kd.cpu(), k, kw, cos, sin, B, L, H, D, "k")
@@ -73,10 +75,10 @@ def test_table_mode_strided_qkv_views(abi, dev, stream_handle):
     kw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
     ang = torch.randn(L, D // 2, generator=g)
     cos, sin = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
-    d = qkv.to(dev)
+    d, qwd, kwd, cd, sd = (t.to(dev) for t in (qkv, qw, kw, cos, sin))
     abi.call("jo_fused_qk_norm_rope_3d_paired", d[:, :, 0].data_ptr(), d[:, :, 1].data_ptr(), B, L,
-             H, D, L * 3 * H * D, 3 * H * D, L * 3 * H * D, 3 * H * D, 1e-6, qw.to(dev).data_ptr(),
-             kw.to(dev).data_ptr(), cos.to(dev).data_ptr(), sin.to(dev).data_ptr(), stream_handle)
+             H, D, L * 3 * H * D, 3 * H * D, L * 3 * H * D, 3 * H * D, 1e-6, qwd.data_ptr(),
+             kwd.data_ptr(), cd.data_ptr(), sd.data_ptr(), stream_handle)
     torch.cuda.synchronize()
     out = d.cpu()
     check_qk(out[:, :, 0].contiguous(), qkv[:, :, 0].contiguous(), qw, cos, sin, B, L, H, D, "q view")

@@ -98,6 +98,23 @@ def test_planted_mistake_x_over_s_is_caught():
     assert (wrong2.numpy() != qc).any()
 
 
+def test_exact_mean_square_rstd():
+    """rms_rstd_exact: the mean square is the fp64 value rounded once; it sits
+    within a few fp32 ulps of the reference's fp32-accumulated formula and
+    within 1 ulp (plus the two IEEE roundings) of the float64 closed form."""
+    g = torch.Generator().manual_seed(31)
+    from joyomni_ops.workloads import with_outliers
+    x = with_outliers(torch.randn(256, 3072, generator=g), g).to(torch.bfloat16)
+    r = ops.rms_rstd_exact(x, 1e-6)
+    r64 = 1.0 / torch.sqrt(x.double().pow(2).mean(-1, keepdim=True) + 1e-6)
+    assert bool(((r.double() - r64).abs() <= 2 * torch.exp2(torch.floor(torch.log2(r64)) - 23)).all())
+    r32 = torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-6)
+    assert bool(((r - r32).abs() <= 8 * torch.exp2(torch.floor(torch.log2(r.abs())) - 23)).all())
+    # a planted slip (mean over N-1) is far outside that band
+    rw = 1.0 / torch.sqrt((x.double().pow(2).sum(-1, keepdim=True) / 3071).float() + 1e-6)
+    assert not torch.allclose(rw, r, rtol=1e-5, atol=0)
+
+
 def test_group_quant_oracle_matches_c():
     g = torch.Generator().manual_seed(3)
     x = torch.randn(40, 1024, generator=g).to(torch.bfloat16)
