@@ -42,9 +42,26 @@ __device__ __forceinline__ float residual_update(float res, float x, float gate,
   return gated ? res + x * gate : res + x;
 }
 
+// Chunk e of the row that starts row_elems elements into base. ld_chunk is
+// cached (reused data: gamma, beta, a broadcast row); ld_row / st_row stream
+// row data that is touched once.
 template <class Tag>
 __device__ __forceinline__ u32x4 ld_chunk(const void* base, int64_t row_elems, int e) {
   return ld16(byte_off(base, (row_elems + e) * Tag::kBytes));
+}
+template <class Tag>
+__device__ __forceinline__ u32x4 ld_row(const void* base, int64_t row_elems, int e) {
+  return ld16_nt(byte_off(base, (row_elems + e) * Tag::kBytes));
+}
+template <class Tag>
+__device__ __forceinline__ void st_row(void* base, int64_t row_elems, int e, const u32x4& v) {
+  st16_nt(byte_off(base, (row_elems + e) * Tag::kBytes), v);
+}
+// A modulation row: streamed when every row has its own (stride != 0),
+// cached when one row is broadcast to all rows (stride == 0).
+template <class Tag>
+__device__ __forceinline__ u32x4 ld_mod(const void* base, int64_t stride, int64_t row, int e) {
+  return stride ? ld_row<Tag>(base, row * stride, e) : ld_chunk<Tag>(base, 0, e);
 }
 
 // ---------------------------------------------------------------------------
@@ -67,7 +84,7 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * V;
-    c[i] = (row_ok && e < N) ? ld_chunk<Tag>(a.x, row * a.xs, e) : u32x4{0u, 0u, 0u, 0u};
+    c[i] = (row_ok && e < N) ? ld_row<Tag>(a.x, row * a.xs, e) : u32x4{0u, 0u, 0u, 0u};
   }
   if constexpr (ADD) {
     u32x4 rc[CH];
@@ -76,8 +93,8 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
     for (int i = 0; i < CH; ++i) {
       const int e = (i * LPR + lane) * V;
       const bool ok = row_ok && e < N;
-      rc[i] = ok ? ld_chunk<Tag>(a.res, row * a.rs, e) : u32x4{0u, 0u, 0u, 0u};
-      gc[i] = (ok && a.gate) ? ld_chunk<Tag>(a.gate, row * a.gs, e) : u32x4{0u, 0u, 0u, 0u};
+      rc[i] = ok ? ld_row<Tag>(a.res, row * a.rs, e) : u32x4{0u, 0u, 0u, 0u};
+      gc[i] = (ok && a.gate) ? ld_mod<Tag>(a.gate, a.gs, row, e) : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
@@ -88,7 +105,7 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
         u[j] = residual_update(elem<Tag>(rc[i], j), elem<Tag>(c[i], j), elem<Tag>(gc[i], j),
                                a.gate != nullptr);
       c[i] = pack<Tag>(u);  // the rounded residual is what gets normalized
-      if (row_ok && e < N) st16(byte_off(a.res, (row * a.rs + e) * Tag::kBytes), c[i]);
+      if (row_ok && e < N) st_row<Tag>(a.res, row * a.rs, e, c[i]);
     }
   }
 
@@ -136,8 +153,8 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * V;
     if (!(row_ok && e < N)) continue;
-    const u32x4 sc = ld_chunk<Tag>(a.scale, row * a.scs, e);
-    const u32x4 sh = ld_chunk<Tag>(a.shift, row * a.shs, e);
+    const u32x4 sc = ld_mod<Tag>(a.scale, a.scs, row, e);
+    const u32x4 sh = ld_mod<Tag>(a.shift, a.shs, row, e);
     u32x4 gm = u32x4{0u, 0u, 0u, 0u}, bt = u32x4{0u, 0u, 0u, 0u};
     if (affine) gm = ld_chunk<Tag>(a.gamma, 0, e);
     if (has_beta) bt = ld_chunk<Tag>(a.beta, 0, e);
@@ -149,7 +166,7 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
       if (has_beta) t = t + elem<Tag>(bt, j);
       o[j] = t * (1.f + elem<Tag>(sc, j)) + elem<Tag>(sh, j);
     }
-    st16(byte_off(a.y, (row * a.ys + e) * Tag::kBytes), pack<Tag>(o));
+    st_row<Tag>(a.y, row * a.ys, e, pack<Tag>(o));
   }
 }
 
@@ -256,7 +273,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const void* __restrict_
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * V;
-    c[i] = (row_ok && e < N) ? ld_chunk<Tag>(x, row * xs, e) : u32x4{0u, 0u, 0u, 0u};
+    c[i] = (row_ok && e < N) ? ld_row<Tag>(x, row * xs, e) : u32x4{0u, 0u, 0u, 0u};
   }
   float ss = 0.f;
 #pragma unroll
@@ -277,7 +294,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const void* __restrict_
     float o[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) o[j] = (elem<Tag>(c[i], j) * r) * elem<Tag>(wc, j);
-    st16(byte_off(out, (row * os + e) * Tag::kBytes), pack<Tag>(o));
+    st_row<Tag>(out, row * os, e, pack<Tag>(o));
   }
 }
 

@@ -122,8 +122,8 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
     for (int g = 0; g < G; ++g) {
       const int e = (g0 + g) * 512 + lane * 8;
       const bool ok = e < a.row_elems;
-      xq[g] = ok ? ld16(qrow + e * 2) : u32x4{0u, 0u, 0u, 0u};
-      xk[g] = ok ? ld16(krow + e * 2) : u32x4{0u, 0u, 0u, 0u};
+      xq[g] = ok ? ld16_nt(qrow + e * 2) : u32x4{0u, 0u, 0u, 0u};
+      xk[g] = ok ? ld16_nt(krow + e * 2) : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -151,9 +151,9 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
         }
         if (e < a.row_elems) {
           if (half == 0)
-            st16(qrow + e * 2, pack<BF16>(o));
+            st16_nt(qrow + e * 2, pack<BF16>(o));
           else
-            st16(kdst + e * 2, pack<BF16>(o));
+            st16_nt(kdst + e * 2, pack<BF16>(o));
         }
       }
     }

@@ -38,7 +38,7 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restri
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * 8;
-    c[i] = (row_ok && e < N) ? ld16(byte_off(xr, static_cast<int64_t>(e) * Tag::kBytes))
+    c[i] = (row_ok && e < N) ? ld16_nt(byte_off(xr, static_cast<int64_t>(e) * Tag::kBytes))
                              : u32x4{0u, 0u, 0u, 0u};
   }
   float amax = 0.f;
@@ -59,7 +59,7 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restri
     if (row_ok && e < N) {
       float v[8];
       unpack<Tag>(c[i], v);
-      st8(qr + e, quant8(v, inv));
+      st8_nt(qr + e, quant8(v, inv));
     }
   }
 }
@@ -134,7 +134,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * 8;
-    c[i] = (row_ok && e < N) ? ld16(byte_off(xr, static_cast<int64_t>(e) * Tag::kBytes))
+    c[i] = (row_ok && e < N) ? ld16_nt(byte_off(xr, static_cast<int64_t>(e) * Tag::kBytes))
                              : u32x4{0u, 0u, 0u, 0u};
   }
   // The squares of bf16/fp16 values are exact in fp32; summing them in fp64
@@ -175,7 +175,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
       const float ginv = (gs == 0.f) ? 0.f : 1.0f / gs;
       if (row_ok && e < N) {
         if ((lane & 15) == 0) s[row * (N / 128) + e / 128] = gs;
-        st8(q + row * qs + e, quant8(v[i], ginv));
+        st8_nt(q + row * qs + e, quant8(v[i], ginv));
       }
     } else {
       amax = fmaxf(amax, gmax);
@@ -189,7 +189,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int e = (i * LPR + lane) * 8;
-      if (row_ok && e < N) st8(q + row * qs + e, quant8(v[i], inv));
+      if (row_ok && e < N) st8_nt(q + row * qs + e, quant8(v[i], inv));
     }
   }
 }
