@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace jo {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -191,6 +193,11 @@ struct OpSum {
 struct OpMax {
   __device__ __forceinline__ static float apply(float a, float b) { return fmaxf(a, b); }
 };
+// Max of non-negative, non-NaN values (|x| maxima built with fmaxf from 0):
+// the wave-level steps compare bit patterns as unsigned integers.
+struct OpAmax {
+  __device__ __forceinline__ static float apply(float a, float b) { return fmaxf(a, b); }
+};
 
 template <int kCtrl>
 __device__ __forceinline__ float dpp(float v) {
@@ -226,6 +233,36 @@ __device__ __forceinline__ float allreduce(float v) {
   if constexpr (W >= 32) v = Op::apply(v, swizzle_xor16(v));
   if constexpr (W == 64) v = Op::apply(readlane(v, 0), readlane(v, 32));
   return v;
+}
+
+// Maximum of non-negative, non-NaN floats over aligned groups of W lanes.
+// For such values the IEEE order equals the unsigned order of the bit
+// patterns, so the reduction runs on integers (no NaN canonicalization
+// between DPP steps). Used for amax values built with fmaxf from 0, which
+// skips NaNs and is never negative.
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xf, 0xf, false));
+}
+template <int W>
+__device__ __forceinline__ float allreduce_amax(float x) {
+  static_assert(W == 8 || W == 16 || W == 32 || W == 64, "group width");
+  uint32_t v = __builtin_bit_cast(uint32_t, x);
+  if constexpr (W == 8) {
+    v = max(v, dpp_u32<kDppHalfMirror>(v));
+  } else {
+    v = max(v, dpp_u32<kDppRor8>(v));
+    v = max(v, dpp_u32<kDppRor4>(v));
+  }
+  v = max(v, dpp_u32<kDppXor2>(v));
+  v = max(v, dpp_u32<kDppXor1>(v));
+  if constexpr (W >= 32)
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x401f)));
+  if constexpr (W == 64)
+    v = max(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 0)),
+            static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 32)));
+  return __builtin_bit_cast(float, v);
 }
 
 // float64 sum over aligned groups of W lanes (W in {8, 16, 32, 64}); DPP and
@@ -293,13 +330,21 @@ __device__ __forceinline__ double row_reduce_sum64(double v, double* slot) {
 // wider than a wave exchange per-wave partials through LDS; `slot` is a
 // __shared__ float[4] scratch owned by the caller (one per reduction in
 // flight). All threads of the block must call it (it may hit a barrier).
+template <int W, class Op>
+__device__ __forceinline__ float wave_reduce(float v) {
+  if constexpr (std::is_same_v<Op, OpAmax>)
+    return allreduce_amax<W>(v);
+  else
+    return allreduce<W, Op>(v);
+}
+
 template <int LPR, class Op>
 __device__ __forceinline__ float row_reduce(float v, float* slot) {
   if constexpr (LPR <= kWave) {
-    return allreduce<LPR, Op>(v);
+    return wave_reduce<LPR, Op>(v);
   } else {
     static_assert(LPR == 128 || LPR == 256, "lanes per row");
-    v = allreduce<kWave, Op>(v);
+    v = wave_reduce<kWave, Op>(v);
     const int wave = threadIdx.x / kWave;
     if ((threadIdx.x & (kWave - 1)) == 0) slot[wave] = v;
     __syncthreads();
@@ -315,7 +360,7 @@ __device__ __forceinline__ float row_reduce(float v, float* slot) {
 // Block-wide reduction for the generic (one row per block) kernels.
 template <class Op>
 __device__ __forceinline__ float block_reduce(float v, float* slot) {
-  v = allreduce<kWave, Op>(v);
+  v = wave_reduce<kWave, Op>(v);
   const int wave = threadIdx.x / kWave;
   __syncthreads();  // slot may still be read by a previous reduction
   if ((threadIdx.x & (kWave - 1)) == 0) slot[wave] = v;

@@ -13,6 +13,8 @@
 //          and the wave redistributes them with ds_bpermute;
 //   KVC    GRID, with the rotated k written to a frame ring buffer instead
 //          of in place.
+#include <stdlib.h>
+
 #include "jo_device.hpp"
 #include "jo_host.hpp"
 
@@ -62,13 +64,20 @@ __device__ __forceinline__ void grid_pair_cs(const QKArgs& a, int P, int p, floa
   }
 }
 
-template <int HD, int G, int MODE>
+// SPLIT = 1: one wave does q and k of its token. SPLIT = 2: two waves per
+// token, the even one q and the odd one k (twice the waves, for sequences
+// too short to fill the chip; the rotation coefficients are then evaluated
+// by both waves).
+template <int HD, int G, int MODE, int SPLIT>
 __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
   constexpr int LPH = HD / 8;      // lanes per head
   constexpr int P = HD / 2;        // rotation pairs per head
   constexpr int K = P > 64 ? P / 64 : 1;  // pairs evaluated per lane in grid modes
   const int lane = threadIdx.x % kWave;
-  const int64_t tok = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + threadIdx.x / kWave;
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + threadIdx.x / kWave;
+  const int64_t tok = wid / SPLIT;
+  const bool do_q = SPLIT == 1 || (wid % SPLIT) == 0;
+  const bool do_k = SPLIT == 1 || (wid % SPLIT) == 1;
   if (tok >= a.tokens) return;
   const int64_t b = tok / a.seq_len;
   const int n = static_cast<int>(tok - b * a.seq_len);
@@ -122,11 +131,12 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
     for (int g = 0; g < G; ++g) {
       const int e = (g0 + g) * 512 + lane * 8;
       const bool ok = e < a.row_elems;
-      xq[g] = ok ? ld16_nt(qrow + e * 2) : u32x4{0u, 0u, 0u, 0u};
-      xk[g] = ok ? ld16_nt(krow + e * 2) : u32x4{0u, 0u, 0u, 0u};
+      xq[g] = (ok && do_q) ? ld16_nt(qrow + e * 2) : u32x4{0u, 0u, 0u, 0u};
+      xk[g] = (ok && do_k) ? ld16_nt(krow + e * 2) : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
+      if ((half == 0 && !do_q) || (half == 1 && !do_k)) continue;  // wave-uniform
       const u32x4& wv = half == 0 ? wq : wk;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -160,27 +170,47 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
   }
 }
 
+// Waves per token. Two (q and k on separate waves) measured faster on MI355X
+// at every BASELINE shape (3510 tokens: 19.0 -> 17.5 us; 10530 tokens:
+// 46.4 -> 45.2 us): the extra waves hide HBM latency better than the saved
+// rotation-coefficient work. JO_QK_SPLIT=1|2 overrides the choice (launch
+// shape only; results are identical).
+int qk_split(int64_t /*tokens*/) {
+  const char* e = getenv("JO_QK_SPLIT");
+  const int forced = e ? atoi(e) : 0;
+  if (forced == 1 || forced == 2) return forced;
+  return 2;
+}
+
 template <int MODE>
 int launch_qk(const QKArgs& a, int head_dim, hipStream_t stream, const char* op) {
   const int groups = (a.row_elems + 511) / 512;
-  const dim3 grid(static_cast<unsigned>((a.tokens + 3) / 4));
-  auto go = [&](auto hd) {
+  const int split = qk_split(a.tokens);
+  const dim3 grid(static_cast<unsigned>((a.tokens * split + 3) / 4));
+  auto go = [&](auto hd, auto sp) {
     constexpr int HD = decltype(hd)::value;
+    constexpr int S = decltype(sp)::value;
     if (groups <= 1)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 1, MODE>), grid, dim3(kBlock), 0, stream, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 1, MODE, S>), grid, dim3(kBlock), 0, stream, a);
     else if (groups <= 2)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 2, MODE>), grid, dim3(kBlock), 0, stream, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 2, MODE, S>), grid, dim3(kBlock), 0, stream, a);
     else if (groups <= 4)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 4, MODE>), grid, dim3(kBlock), 0, stream, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 4, MODE, S>), grid, dim3(kBlock), 0, stream, a);
     else if (groups <= 6)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 6, MODE>), grid, dim3(kBlock), 0, stream, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 6, MODE, S>), grid, dim3(kBlock), 0, stream, a);
     else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 8, MODE>), grid, dim3(kBlock), 0, stream, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 8, MODE, S>), grid, dim3(kBlock), 0, stream, a);
+  };
+  auto go_hd = [&](auto hd) {
+    if (split == 2)
+      go(hd, std::integral_constant<int, 2>{});
+    else
+      go(hd, std::integral_constant<int, 1>{});
   };
   switch (head_dim) {
-    case 64: go(std::integral_constant<int, 64>{}); break;
-    case 128: go(std::integral_constant<int, 128>{}); break;
-    default: go(std::integral_constant<int, 256>{}); break;
+    case 64: go_hd(std::integral_constant<int, 64>{}); break;
+    case 128: go_hd(std::integral_constant<int, 128>{}); break;
+    default: go_hd(std::integral_constant<int, 256>{}); break;
   }
   return launch_status(op);
 }

@@ -47,7 +47,7 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restri
 #pragma unroll
     for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(elem<Tag>(c[i], j)));
   }
-  amax = row_reduce<LPR, OpMax>(amax, red);
+  amax = row_reduce<LPR, OpAmax>(amax, red);
   const float scale = amax / kFp8Max;
   if (row_ok && lane == 0) s[row] = scale;
   const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(kBlock) void quant_generic_kernel(const void* __res
   const int64_t xo = row * xs;
   float amax = 0.f;
   for (int i = threadIdx.x; i < N; i += kBlock) amax = fmaxf(amax, fabsf(load_elem<Tag>(x, xo + i)));
-  amax = block_reduce<OpMax>(amax, red);
+  amax = block_reduce<OpAmax>(amax, red);
   const float scale = amax / kFp8Max;
   if (threadIdx.x == 0) s[row] = scale;
   const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;
@@ -146,8 +146,8 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
   for (int i = 0; i < CH; ++i) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float v = elem<Tag>(c[i], j);
-      ss += static_cast<double>(v * v);
+      const double v = static_cast<double>(elem<Tag>(c[i], j));
+      ss = __builtin_fma(v, v, ss);  // v*v is exact: one rounding per step, as a sum of squares
     }
   }
   ss = row_reduce_sum64<LPR>(ss, red_ss);
@@ -156,33 +156,66 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
 
   // v = (x * r) * w, kept in registers for the quantization pass.
   float v[CH][8];
-  float amax = 0.f;
+  float gmax[CH];
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * 8;
     u32x4 wc = u32x4{0u, 0u, 0u, 0u};
     if (e < N) wc = ld16(byte_off(w, static_cast<int64_t>(e) * Tag::kBytes));
-    float gmax = 0.f;
+    gmax[i] = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       v[i][j] = (elem<Tag>(c[i], j) * r) * elem<Tag>(wc, j);
-      gmax = fmaxf(gmax, fabsf(v[i][j]));
+      gmax[i] = fmaxf(gmax[i], fabsf(v[i][j]));
     }
-    if constexpr (GROUP == 128) {
-      // The 16 lanes of this DPP row hold one 128-element block.
-      gmax = allreduce<16, OpMax>(gmax);
-      const float gs = gmax / kFp8Max;
-      const float ginv = (gs == 0.f) ? 0.f : 1.0f / gs;
-      if (row_ok && e < N) {
-        if ((lane & 15) == 0) s[row * (N / 128) + e / 128] = gs;
-        st8_nt(q + row * qs + e, quant8(v[i], ginv));
+  }
+  if constexpr (GROUP == 128) {
+    // Each 16-lane DPP row of a chunk holds one 1x128 block.
+#pragma unroll
+    for (int i = 0; i < CH; ++i) gmax[i] = allreduce_amax<16>(gmax[i]);
+    float ginv[CH];
+    if constexpr (LPR >= kWave) {
+      // A wave holds 4*CH blocks: gather their maxima into lanes 0..4*CH-1
+      // so the two IEEE divisions run once per block, then hand each chunk
+      // its inverse scale back.
+      const int wl = threadIdx.x % kWave;
+      const int wave_in_row = lane / kWave;
+      float mine = 0.f;
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const float t = __builtin_bit_cast(
+            float, __builtin_amdgcn_ds_bpermute((wl & 3) * 16 * 4, __builtin_bit_cast(int, gmax[i])));
+        if ((wl >> 2) == i) mine = t;
       }
+      const float gs = mine / kFp8Max;
+      const float gi = (gs == 0.f) ? 0.f : 1.0f / gs;
+      const int gc = wl >> 2;  // chunk of the block this lane owns
+      const int ge = (gc * LPR + wave_in_row * kWave + (wl & 3) * 16) * 8;  // its first element
+      if (row_ok && wl < 4 * CH && ge < N) s[row * (N / 128) + ge / 128] = gs;
+#pragma unroll
+      for (int i = 0; i < CH; ++i)
+        ginv[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                (i * 4 + (wl >> 4)) * 4, __builtin_bit_cast(int, gi)));
     } else {
-      amax = fmaxf(amax, gmax);
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int e = (i * LPR + lane) * 8;
+        const float gs = gmax[i] / kFp8Max;
+        ginv[i] = (gs == 0.f) ? 0.f : 1.0f / gs;
+        if (row_ok && e < N && (lane & 15) == 0) s[row * (N / 128) + e / 128] = gs;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int e = (i * LPR + lane) * 8;
+      if (row_ok && e < N) st8_nt(q + row * qs + e, quant8(v[i], ginv[i]));
     }
   }
   if constexpr (GROUP == 0) {
-    amax = row_reduce<LPR, OpMax>(amax, red_max);
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) amax = fmaxf(amax, gmax[i]);
+    amax = row_reduce<LPR, OpAmax>(amax, red_max);
     const float scale = amax / kFp8Max;
     if (row_ok && lane == 0) s[row] = scale;
     const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;

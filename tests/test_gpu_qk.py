@@ -17,6 +17,17 @@ from joyomni_ops import workloads as W
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(params=["auto", "1", "2"], autouse=True)
+def qk_split(request, monkeypatch):
+    """Run every QK test with the automatic launch shape and with one and two
+    waves per token forced (JO_QK_SPLIT): results must not depend on it."""
+    if request.param != "auto":
+        monkeypatch.setenv("JO_QK_SPLIT", request.param)
+    else:
+        monkeypatch.delenv("JO_QK_SPLIT", raising=False)
+    return request.param
+
+
 def head_floor(ref):
     return ref.abs().amax(dim=-1, keepdim=True)
 
