@@ -173,11 +173,35 @@ __device__ __forceinline__ void* byte_off(void* p, int64_t bytes) {
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float fp8_clamp(float v) { return fmaxf(fminf(v, kFp8Max), -kFp8Max); }
 
-// Four clamped values -> four e4m3fn bytes (element 0 in the lowest byte).
+// Four values -> four e4m3fn bytes (element 0 in the lowest byte).
+// CLAMP = true applies the clamp first (any input, NaN -> +448).
+// CLAMP = false is for finite inputs with |v| <= 464: v_cvt_pk_fp8_f32 then
+// rounds to nearest-even onto the finite codes (measured on MI355X: values in
+// (448, 464] give 448, above 464 NaN), which equals clamping first. The
+// quantizers use it for rows whose values and inverse scale are finite, where
+// |x * inv| <= amax * inv <= 448 * (1 + 3 * 2^-24).
+template <bool CLAMP = true>
 __device__ __forceinline__ uint32_t fp8x4(float a, float b, float c, float d) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(a), fp8_clamp(b), 0, false);
-  w = __builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(c), fp8_clamp(d), w, true);
+  if constexpr (CLAMP) {
+    a = fp8_clamp(a);
+    b = fp8_clamp(b);
+    c = fp8_clamp(c);
+    d = fp8_clamp(d);
+  }
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return static_cast<uint32_t>(w);
+}
+
+// max(m, |v|) propagating NaN (IEEE maximum; v_maximum3_f32 on gfx950).
+// Starting from 0, a row maximum built with it is +0..+inf, or a NaN whose
+// bit pattern sorts above +inf; allreduce_amax's unsigned compare keeps that
+// order, so "row maximum is finite" means "no NaN and no inf in the row".
+__device__ __forceinline__ float nan_max_abs(float m, float v) {
+  return __builtin_elementwise_maximum(m, __builtin_fabsf(v));
+}
+__device__ __forceinline__ bool finite_bits(float v) {
+  return (__builtin_bit_cast(uint32_t, v) & 0x7fffffffu) < 0x7f800000u;
 }
 
 // ---------------------------------------------------------------------------
@@ -193,10 +217,14 @@ struct OpSum {
 struct OpMax {
   __device__ __forceinline__ static float apply(float a, float b) { return fmaxf(a, b); }
 };
-// Max of non-negative, non-NaN values (|x| maxima built with fmaxf from 0):
-// the wave-level steps compare bit patterns as unsigned integers.
+// Max of non-negative values (|x| maxima from 0, possibly a positive NaN
+// pattern): compares bit patterns as unsigned integers at every step, so a
+// NaN (which sorts above +inf) survives the cross-wave combine as well.
 struct OpAmax {
-  __device__ __forceinline__ static float apply(float a, float b) { return fmaxf(a, b); }
+  __device__ __forceinline__ static float apply(float a, float b) {
+    return __builtin_bit_cast(
+        float, max(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)));
+  }
 };
 
 template <int kCtrl>

@@ -12,15 +12,21 @@ namespace jo {
 namespace {
 
 // Quantizes 8 fp32 values with the reference's rule and returns 8 bytes.
+// CLAMP = false only where the inputs are finite and inv is finite (see fp8x4).
+template <bool CLAMP = true>
 __device__ __forceinline__ u32x2 quant8(const float (&v)[8], float inv) {
-  return u32x2{fp8x4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv),
-               fp8x4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv)};
+  return u32x2{fp8x4<CLAMP>(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv),
+               fp8x4<CLAMP>(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv)};
 }
 
 // ---------------------------------------------------------------------------
 // Per-token quantization: follows per_token_quant_fp8.cu:56-82.
 //   amax = max |x| (NaN ignored: fmaxf), scale = amax / 448 (IEEE division),
 //   inv = (scale == 0) ? 0 : 1 / scale, q = e4m3fn(clamp(x * inv, +-448)).
+// The row maximum is first taken NaN-propagating; when it is finite (no NaN,
+// no inf in the row) it is the reference's amax and, with a finite inv, the
+// clamp cannot change a code, so it is skipped. Any workgroup holding a
+// non-finite row recomputes the NaN-skipping maximum and clamps that row.
 // ---------------------------------------------------------------------------
 template <class Tag, int LPR, int CH>
 __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restrict__ x, int64_t xs,
@@ -29,6 +35,7 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restri
   static_assert(Tag::kVec == 8, "fp8 rows are built from 8-element chunks");
   constexpr int RPB = kBlock / LPR;
   __shared__ float red[kBlock / kWave];
+  __shared__ float red2[kBlock / kWave];
   const int lane = threadIdx.x % LPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
   const bool row_ok = row < M;
@@ -45,12 +52,24 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restri
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(elem<Tag>(c[i], j)));
+    for (int j = 0; j < 8; ++j) amax = nan_max_abs(amax, elem<Tag>(c[i], j));
   }
   amax = row_reduce<LPR, OpAmax>(amax, red);
+  const bool finite_row = finite_bits(amax);
+  if (__syncthreads_or(!finite_row)) {
+    // Reference amax: NaNs skipped (fmaxf from 0).
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(elem<Tag>(c[i], j)));
+    }
+    amax = row_reduce<LPR, OpAmax>(m, red2);
+  }
   const float scale = amax / kFp8Max;
   if (row_ok && lane == 0) s[row] = scale;
   const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;
+  const bool fast = finite_row && finite_bits(inv);
 
   uint8_t* qr = q + row * qs;
 #pragma unroll
@@ -59,7 +78,7 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restri
     if (row_ok && e < N) {
       float v[8];
       unpack<Tag>(c[i], v);
-      st8_nt(qr + e, quant8(v, inv));
+      st8_nt(qr + e, fast ? quant8<false>(v, inv) : quant8<true>(v, inv));
     }
   }
 }
@@ -125,6 +144,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
   constexpr int RPB = kBlock / LPR;
   __shared__ double red_ss[kBlock / kWave];
   __shared__ float red_max[kBlock / kWave];
+  __shared__ float red_max2[kBlock / kWave];
   const int lane = threadIdx.x % LPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
   const bool row_ok = row < M;
@@ -136,6 +156,15 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
     const int e = (i * LPR + lane) * 8;
     c[i] = (row_ok && e < N) ? ld16_nt(byte_off(xr, static_cast<int64_t>(e) * Tag::kBytes))
                              : u32x4{0u, 0u, 0u, 0u};
+  }
+  // Weight chunks are issued with the row loads so their (cached) latency
+  // overlaps the HBM latency instead of following the row reduction.
+  u32x4 wc[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * 8;
+    wc[i] = (e < N) ? ld16(byte_off(w, static_cast<int64_t>(e) * Tag::kBytes))
+                    : u32x4{0u, 0u, 0u, 0u};
   }
   // The squares of bf16/fp16 values are exact in fp32; summing them in fp64
   // makes the mean square the correctly rounded fp32 value of the exact
@@ -154,25 +183,43 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
   const float ms = static_cast<float>(ss / static_cast<double>(N));
   const float r = 1.0f / sqrtf(ms + eps);
 
-  // v = (x * r) * w, kept in registers for the quantization pass.
+  // v = (x * r) * w, kept in registers for the quantization pass. The
+  // per-chunk maxima are NaN-propagating (see quant_rows_kernel): a finite
+  // maximum is the reference's and lets the clamp be skipped.
   float v[CH][8];
   float gmax[CH];
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
-    const int e = (i * LPR + lane) * 8;
-    u32x4 wc = u32x4{0u, 0u, 0u, 0u};
-    if (e < N) wc = ld16(byte_off(w, static_cast<int64_t>(e) * Tag::kBytes));
     gmax[i] = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      v[i][j] = (elem<Tag>(c[i], j) * r) * elem<Tag>(wc, j);
-      gmax[i] = fmaxf(gmax[i], fabsf(v[i][j]));
+      v[i][j] = (elem<Tag>(c[i], j) * r) * elem<Tag>(wc[i], j);
+      gmax[i] = nan_max_abs(gmax[i], v[i][j]);
     }
   }
+  // NaN-skipping maximum of chunk i's part of this lane (the reference's
+  // fmaxf rule), for workgroups that hold a non-finite value.
+  auto skip_nan_max = [&](int i) {
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[i][j]));
+    return m;
+  };
   if constexpr (GROUP == 128) {
     // Each 16-lane DPP row of a chunk holds one 1x128 block.
+    bool all_finite = true;
 #pragma unroll
-    for (int i = 0; i < CH; ++i) gmax[i] = allreduce_amax<16>(gmax[i]);
+    for (int i = 0; i < CH; ++i) {
+      gmax[i] = allreduce_amax<16>(gmax[i]);
+      all_finite = all_finite && finite_bits(gmax[i]);
+    }
+    bool fast[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) fast[i] = finite_bits(gmax[i]);
+    if (__syncthreads_or(!all_finite)) {
+#pragma unroll
+      for (int i = 0; i < CH; ++i) gmax[i] = allreduce_amax<16>(skip_nan_max(i));
+    }
     float ginv[CH];
     if constexpr (LPR >= kWave) {
       // A wave holds 4*CH blocks: gather their maxima into lanes 0..4*CH-1
@@ -208,21 +255,32 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int e = (i * LPR + lane) * 8;
-      if (row_ok && e < N) st8_nt(q + row * qs + e, quant8(v[i], ginv[i]));
+      if (row_ok && e < N)
+        st8_nt(q + row * qs + e, (fast[i] && finite_bits(ginv[i])) ? quant8<false>(v[i], ginv[i])
+                                                                   : quant8<true>(v[i], ginv[i]));
     }
   }
   if constexpr (GROUP == 0) {
     float amax = 0.f;
 #pragma unroll
-    for (int i = 0; i < CH; ++i) amax = fmaxf(amax, gmax[i]);
+    for (int i = 0; i < CH; ++i) amax = __builtin_elementwise_maximum(amax, gmax[i]);
     amax = row_reduce<LPR, OpAmax>(amax, red_max);
+    const bool finite_row = finite_bits(amax);
+    if (__syncthreads_or(!finite_row)) {
+      float m = 0.f;
+#pragma unroll
+      for (int i = 0; i < CH; ++i) m = fmaxf(m, skip_nan_max(i));
+      amax = row_reduce<LPR, OpAmax>(m, red_max2);
+    }
     const float scale = amax / kFp8Max;
     if (row_ok && lane == 0) s[row] = scale;
     const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;
+    const bool fast = finite_row && finite_bits(inv);
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int e = (i * LPR + lane) * 8;
-      if (row_ok && e < N) st8_nt(q + row * qs + e, quant8(v[i], inv));
+      if (row_ok && e < N)
+        st8_nt(q + row * qs + e, fast ? quant8<false>(v[i], inv) : quant8<true>(v[i], inv));
     }
   }
 }

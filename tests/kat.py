@@ -39,6 +39,12 @@ KAT_ROWS = [
     ([448.0, 2.0 ** -10, 1.5 * 2.0 ** -10, 3 * 2.0 ** -10, 2.0 ** -7, -(2.0 ** -10),
       -(1.5 * 2.0 ** -10), 0.0], 1.0,
      [0x7e, 0x00, 0x01, 0x02, 0x04, 0x80, 0x81, 0x00]),
+    # Tiny row: amax 2^-126 -> scale = 2^-126/448 = 2^-132/7, a denormal that
+    # rounds to 18725 * 2^-149; 1/scale overflows to inf. Nonzero x*inf = +-inf
+    # clamps to +-448; +-0 * inf = NaN -> 448.
+    ([2.0 ** -127, -(2.0 ** -127), 0.0, 2.0 ** -128, -0.0, 2.0 ** -127, 2.0 ** -126,
+      -(2.0 ** -126)], 18725 * 2.0 ** -149,
+     [0x7e, 0xfe, 0x7e, 0x7e, 0x7e, 0x7e, 0x7e, 0xfe]),
     # amax 7 -> scale 7/448 = 1/64 exactly, inv 64: x*64 exact; 7*64 = 448;
     # 3.5*64 = 224 = 0x76; 0.0078125*64 = 0.5 = 0x30; 5*64 = 320 = 0x7a;
     # 1*64 = 64 = 0x68; 0.25*64 = 16 = 0x58.

@@ -66,6 +66,36 @@ def test_quant_known_answer_rows(abi, dev, stream_handle):
             assert s[i].item() == np.float32(scale) or (np.isinf(scale) and np.isinf(s[i].item()))
 
 
+def inject_nonfinite(x: torch.Tensor, seed: int) -> torch.Tensor:
+    """Rows 1, 5, 9, ... get a NaN, rows 2, 6, ... an inf, rows 3, 7, ... a -inf,
+    every 4th row is scaled to 2^-127 (1/scale overflows); row 0 stays finite."""
+    x = x.clone().float()
+    g = torch.Generator().manual_seed(seed)
+    M, N = x.shape
+    for r in range(1, M):
+        j = int(torch.randint(0, N, (1,), generator=g))
+        kind = r % 4
+        if kind == 1:
+            x[r, j] = float("nan")
+        elif kind == 2:
+            x[r, j] = float("inf")
+        elif kind == 3:
+            x[r, j] = float("-inf")
+        else:
+            x[r] = torch.sign(x[r]) * 2.0 ** -127
+    return x
+
+
+@pytest.mark.parametrize("N", [64, 3072, 16384])
+def test_quant_nonfinite_rows(abi, dev, stream_handle, N):
+    """Rows with NaN/inf and rows whose inverse scale overflows take the
+    clamped path; finite rows sharing their workgroup must be unaffected."""
+    g = torch.Generator().manual_seed(N)
+    x = inject_nonfinite(torch.randn(13, N, generator=g), N).to(torch.bfloat16)
+    q, s = quant_gpu(abi, stream_handle, x.to(dev))
+    assert_quant_equal(q, s, x, f"nonfinite [13,{N}]")
+
+
 def test_quant_strided_and_unaligned_views(abi, dev, stream_handle):
     g = torch.Generator().manual_seed(11)
     big = W.with_outliers(torch.randn(40, 3200, generator=g), g).to(torch.bfloat16)
@@ -135,6 +165,25 @@ def test_rmsnorm_quant_random(abi, dev, stream_handle, group, M, N):
     w = (1 + 0.1 * torch.randn(N, generator=g)).to(torch.bfloat16)
     q, s = rms_quant_gpu(abi, stream_handle, x.to(dev), w.to(dev), 1e-6, group)
     check_rms_quant(q, s, x, w, 1e-6, group, f"[{M},{N}] g{group}")
+
+
+@pytest.mark.parametrize("group", [0, 128])
+@pytest.mark.parametrize("N", [128, 3072, 16384])
+@pytest.mark.parametrize("where", ["x", "w"])
+def test_rmsnorm_quant_nonfinite(abi, dev, stream_handle, group, N, where):
+    """NaN/inf in a row, in the weight, or rows so small that 1/scale overflows."""
+    g = torch.Generator().manual_seed(N + group)
+    x = torch.randn(13, N, generator=g)
+    w = 1 + 0.1 * torch.randn(N, generator=g)
+    if where == "x":
+        x = inject_nonfinite(x, N)
+    else:
+        w[N // 3] = float("nan")
+        w[N // 2] = float("inf")
+        x[5] = 2.0 ** -127
+    x, w = x.to(torch.bfloat16), w.to(torch.bfloat16)
+    q, s = rms_quant_gpu(abi, stream_handle, x.to(dev), w.to(dev), 1e-6, group)
+    check_rms_quant(q, s, x, w, 1e-6, group, f"nonfinite {where} [13,{N}] g{group}")
 
 
 @pytest.mark.parametrize("name", ["C4_4725_tok", "C4_4725_blk", "C4_10530_tok", "C4_10530_blk"])
