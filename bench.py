@@ -51,7 +51,25 @@ def tensor_bytes(d: dict) -> int:
     return sum(t.numel() * t.element_size() for t in d.values())
 
 
-def time_gpu(cfg, steps: int, warmup: int, dev) -> dict:
+def copy_probe(mb: int, steps: int, dev) -> dict:
+    """Plain device copy of `mb` MiB (torch copy_), the calibration kernel for
+    the FETCH_SIZE / WRITE_SIZE counters: it moves a known mb MiB each way."""
+    import torch
+    n = mb << 20
+    sets = [(torch.empty(n, dtype=torch.uint8, device=dev), torch.empty(n, dtype=torch.uint8, device=dev))
+            for _ in range(max(2, math.ceil(ROT_BYTES / (2 * n))))]
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        sets[i % len(sets)][1].copy_(sets[i % len(sets)][0])
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / steps
+    return {"bytes_each_way": n, "us_per_call": round(us, 3), "gbps": round(2 * n / (us * 1e-6) / 1e9, 1)}
+
+
+def time_gpu(cfg, steps: int, warmup: int, dev, use_graph: bool = True) -> dict:
     import torch
 
     import joyomni_ops as jo
@@ -86,6 +104,12 @@ def time_gpu(cfg, steps: int, warmup: int, dev) -> dict:
         e1.record(stream)
     torch.cuda.synchronize()
     eager_us = e0.elapsed_time(e1) * 1000.0 / steps
+    alg = W.algorithmic_bytes(cfg)
+    if not use_graph:
+        gbps = alg / (eager_us * 1e-6) / 1e9
+        return {"us_per_call": round(eager_us, 3), "eager_us_per_call": round(eager_us, 3),
+                "gbps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_GBPS, 4),
+                "algorithmic_bytes": alg, "buffer_sets": n_sets, "timing": "eager"}
 
     # HIP graph of `steps` launches
     graph = torch.cuda.CUDAGraph()
@@ -102,14 +126,13 @@ def time_gpu(cfg, steps: int, warmup: int, dev) -> dict:
     e1.record(cur)
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1000.0 / steps
-    alg = W.algorithmic_bytes(cfg)
     gbps = alg / (us * 1e-6) / 1e9
     del graph, sets
     torch.cuda.empty_cache()
     return {"us_per_call": round(us, 3), "eager_us_per_call": round(eager_us, 3),
             "gbps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_GBPS, 4),
             "algorithmic_bytes": alg, "buffer_sets": n_sets,
-            "rotated_mb": round(n_sets * set_bytes / 1e6, 1)}
+            "rotated_mb": round(n_sets * set_bytes / 1e6, 1), "timing": "hip-graph"}
 
 
 def cpu_fn(cfg):
@@ -184,6 +207,10 @@ def main() -> int:
     ap.add_argument("--only", default="", help="comma-separated config names")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-iters", type=int, default=10)
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time eager launches only (for profiler counter runs)")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="also run a plain copy of this many MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -205,9 +232,13 @@ def main() -> int:
     results = {}
     for n in names:
         cfg = W.CONFIGS[n]
-        log(f"{n}: timing {args.steps} graph-replayed calls")
-        results[n] = time_gpu(cfg, args.steps, args.warmup, dev)
+        log(f"{n}: timing {args.steps} {'eager' if args.no_graph else 'graph-replayed'} calls")
+        results[n] = time_gpu(cfg, args.steps, args.warmup, dev, use_graph=not args.no_graph)
         log(f"{n}: {results[n]}")
+    copy = None
+    if args.copy_mb:
+        copy = copy_probe(args.copy_mb, args.steps, dev)
+        log(f"copy {args.copy_mb} MiB: {copy}")
 
     cpu = None
     if not args.no_cpu:
@@ -244,6 +275,8 @@ def main() -> int:
                       f"{os.cpu_count()} logical CPUs"},
         "ops": results,
     }
+    if copy is not None:
+        line["copy_probe"] = copy
     print(json.dumps(line), flush=True)
     return 0
 

@@ -199,28 +199,53 @@ namespace {
 
 struct QKGeom {
   int64_t batch, seq_len, num_heads, head_dim;
+  int64_t q_bs, q_ts, k_bs, k_ts;  // batch / token strides in elements
 };
+
+// Batch and token strides of a q/k tensor: either [B, seq_len*num_heads, D]
+// contiguous (the paired op's layout) or a [B, seq_len, num_heads, D] view
+// whose heads are contiguous within a token (e.g. q = qkv[:, :, 0] of a
+// packed [B, L, 3, H, D] projection).
+void qk_strides(const torch::Tensor& t, int64_t seq_len, int64_t num_heads, int64_t head_dim,
+                const char* name, int64_t* bs, int64_t* ts) {
+  if (t.dim() == 3) {
+    TORCH_CHECK(t.is_contiguous(), name, " must be contiguous when 3D");
+    TORCH_CHECK(t.size(1) == seq_len * num_heads, name, ".size(1) must equal seq_len*num_heads");
+    *bs = seq_len * num_heads * head_dim;
+    *ts = num_heads * head_dim;
+  } else {
+    TORCH_CHECK(t.dim() == 4 && t.size(1) == seq_len && t.size(2) == num_heads,
+                name, " must be [B, seq_len*num_heads, D] or [B, seq_len, num_heads, D]");
+    TORCH_CHECK(t.stride(3) == 1 && t.stride(2) == head_dim,
+                name, ": heads of a token must be contiguous");
+    *bs = t.size(0) == 1 ? seq_len * t.stride(1) : t.stride(0);
+    *ts = seq_len == 1 ? num_heads * head_dim : t.stride(1);
+  }
+}
 
 QKGeom check_qk_common(const torch::Tensor& q, const torch::Tensor& k, int64_t seq_len,
                        int64_t num_heads, const torch::Tensor& q_weight,
                        const torch::Tensor& k_weight, const torch::Tensor& freqs) {
-  TORCH_CHECK(q.dim() == 3, "q must be 3D [batch, seq_len*num_heads, head_dim]");
-  TORCH_CHECK(k.dim() == 3, "k must be 3D [batch, seq_len*num_heads, head_dim]");
+  TORCH_CHECK(q.dim() == 3 || q.dim() == 4, "q must be 3D or 4D");
   TORCH_CHECK(q.sizes() == k.sizes(), "q and k must have the same shape");
-  JO_CHECK_INPUT(q, torch::kBFloat16);
-  JO_CHECK_INPUT(k, torch::kBFloat16);
+  JO_CHECK_CUDA(q);
+  JO_CHECK_CUDA(k);
+  JO_CHECK_DTYPE(q, torch::kBFloat16);
+  JO_CHECK_DTYPE(k, torch::kBFloat16);
   JO_CHECK_INPUT(q_weight, torch::kBFloat16);
   JO_CHECK_INPUT(k_weight, torch::kBFloat16);
   JO_CHECK_INPUT(freqs, torch::kFloat32);
-  const int64_t head_dim = q.size(2);
-  TORCH_CHECK(q.size(1) == seq_len * num_heads, "q.size(1) must equal seq_len*num_heads");
+  const int64_t head_dim = q.size(q.dim() - 1);
   TORCH_CHECK(q_weight.numel() == head_dim && k_weight.numel() == head_dim,
               "weight size must match head_dim");
   TORCH_CHECK(freqs.dim() == 2 && freqs.size(0) == 2 && freqs.size(1) == head_dim / 2,
               "freqs must be [2, head_dim/2] float32");
   TORCH_CHECK(head_dim == 64 || head_dim == 128 || head_dim == 256,
               "Unsupported head_dim: ", head_dim);
-  return {q.size(0), seq_len, num_heads, head_dim};
+  QKGeom g{q.size(0), seq_len, num_heads, head_dim, 0, 0, 0, 0};
+  qk_strides(q, seq_len, num_heads, head_dim, "q", &g.q_bs, &g.q_ts);
+  qk_strides(k, seq_len, num_heads, head_dim, "k", &g.k_bs, &g.k_ts);
+  return g;
 }
 
 }  // namespace
@@ -232,10 +257,9 @@ void fused_qk_norm_rope_3d_grid(torch::Tensor& q, torch::Tensor& k, int64_t seq_
                                 double source_id) {
   const QKGeom g = check_qk_common(q, k, seq_len, num_heads, q_weight, k_weight, freqs);
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(q.device());
-  const int64_t tok = g.num_heads * g.head_dim;
   check_status(jo_fused_qk_norm_rope_3d_grid(
                    q.data_ptr(), k.data_ptr(), g.batch, g.seq_len, g.num_heads, g.head_dim,
-                   g.seq_len * tok, tok, g.seq_len * tok, tok, static_cast<float>(eps),
+                   g.q_bs, g.q_ts, g.k_bs, g.k_ts, static_cast<float>(eps),
                    q_weight.data_ptr(), k_weight.data_ptr(), freqs.data_ptr<float>(),
                    static_cast<int32_t>(pairs_t), static_cast<int32_t>(pairs_h),
                    static_cast<int32_t>(grid_h), static_cast<int32_t>(grid_w),
@@ -263,7 +287,7 @@ void fused_qk_norm_rope_3d_kvcache(torch::Tensor& q, const torch::Tensor& k,
   const int64_t tok = g.num_heads * g.head_dim;
   check_status(jo_fused_qk_norm_rope_3d_kvcache(
                    q.data_ptr(), k.data_ptr(), k_cache.data_ptr(), g.batch, g.seq_len,
-                   g.num_heads, g.head_dim, g.seq_len * tok, tok, g.seq_len * tok, tok,
+                   g.num_heads, g.head_dim, g.q_bs, g.q_ts, g.k_bs, g.k_ts,
                    k_cache.size(1) * g.head_dim, tok, cache_slots, slot_start,
                    static_cast<float>(eps), q_weight.data_ptr(), k_weight.data_ptr(),
                    freqs.data_ptr<float>(), static_cast<int32_t>(pairs_t),

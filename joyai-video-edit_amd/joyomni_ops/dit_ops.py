@@ -1,0 +1,199 @@
+"""DiT-side call shims over joyomni_ops, with the reference's names and signatures.
+
+Counterpart of deploy/xvideo/models/dit/sgl_fused_ops.py:1-117 (the functions
+MMDoubleStreamBlock.forward calls, dit.py:351-476) and of the activation
+quantization step of Fp8Linear.forward (deploy/xvideo/models/dit/fp8_linear.py:138-169).
+Same arguments, same results; the differences are in the HBM traffic:
+
+  fused_layernorm_modulate  passes per-sample shift/scale as stride-0 rows
+                            instead of materialising [B*L, D] copies
+                            (sgl_fused_ops.py:44-51 expands and copies them).
+  fused_qk_norm_rope_3d     identical contract (contiguous copies of q/k, tables
+                            halved and cast to bf16 as sgl_fused_ops.py:73-94).
+
+Additional entry points for callers that can use the new fused ops:
+
+  fused_qk_norm_rope_3d_grid_views  RMSNorm + RoPE in place on q/k views of the
+                            packed qkv [B, L, 3, H, D] with angles computed from
+                            grid positions (no tables, no .contiguous() copies).
+  fused_add_gate_layernorm_modulate residual + x * gate and the following
+                            fused_layernorm_modulate in one pass (dit.py:447-457).
+  quantize_activation_fp8   x_q, x_scale of Fp8Linear.forward (fp8_linear.py:140-166).
+"""
+from __future__ import annotations
+
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import (fused_add_layernorm_scale_shift, fused_norm_scale_shift,
+               fused_qk_norm_rope_3d_grid, fused_qk_norm_rope_3d_paired, rmsnorm, rope_freqs,
+               sgl_per_token_quant_fp8)
+
+
+def available() -> bool:
+    """The reference's availability probe (sgl_fused_ops.py:14-27): the ops load at import."""
+    return True
+
+
+def _mod_rows(t: torch.Tensor, B: int, L: int, D: int) -> torch.Tensor:
+    """shift/scale as [B*L, D] without copying a per-sample vector: [B, D] or
+    [B, 1, D] with B == 1 becomes a stride-0 expanded view; per-token tensors
+    are reshaped (copied only if their layout needs it)."""
+    if t.dim() == 2:
+        t = t.unsqueeze(1)
+    if t.shape[1] == 1 and L != 1:
+        if B == 1:
+            return t.reshape(1, D).expand(L, D)
+        t = t.expand(B, L, D)
+    return t.reshape(B * L, D)
+
+
+def fused_layernorm_modulate(
+    x: torch.Tensor,
+    shift: torch.Tensor,
+    scale: torch.Tensor,
+    *,
+    weight: Optional[torch.Tensor] = None,
+    bias: Optional[torch.Tensor] = None,
+    eps: float = 1e-6,
+) -> torch.Tensor:
+    """LayerNorm(x; weight, bias) * (1 + scale) + shift for x [B, L, D]
+    (sgl_fused_ops.py:30-54). shift/scale: [B, D], [B, 1, D] or [B, L, D]."""
+    B, L, D = x.shape
+    x_2d = x.reshape(-1, D)
+    out = fused_norm_scale_shift(x_2d, weight, bias, _mod_rows(scale, B, L, D),
+                                 _mod_rows(shift, B, L, D), "layer", eps)
+    return out.reshape(B, L, D)
+
+
+def fused_qk_norm_rope_3d(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    q_norm_weight: torch.Tensor,
+    k_norm_weight: torch.Tensor,
+    freqs_cis: Tuple[torch.Tensor, torch.Tensor],
+    *,
+    eps: float = 1e-6,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-head RMSNorm + interleaved RoPE of q, k [B, L, H, D] from
+    (cos, sin) tables [1, L, D] or [L, D/2] (sgl_fused_ops.py:57-99). Returns
+    new contiguous (q, k); the inputs are not modified."""
+    if q.dtype != torch.bfloat16:
+        raise RuntimeError(f"fused_qk_norm_rope_3d requires bf16 q/k, got {q.dtype}")
+    B, L, H, D = q.shape
+    q = q.contiguous()
+    k = k.contiguous()
+    q_r = q.view(B, L * H, D)
+    k_r = k.view(B, L * H, D)
+    cos, sin = freqs_cis
+    cos = cos.to(q.device)
+    sin = sin.to(q.device)
+    while cos.dim() > 2:
+        if cos.shape[0] != 1:
+            raise RuntimeError(f"freqs_cis cos has non-singleton leading dim: {cos.shape}")
+        cos = cos.squeeze(0)
+        sin = sin.squeeze(0)
+    if cos.shape[-1] == D:
+        cos = cos[..., ::2]
+        sin = sin[..., ::2]
+    cos_bf16 = cos.contiguous().to(torch.bfloat16)
+    sin_bf16 = sin.contiguous().to(torch.bfloat16)
+    qw = q_norm_weight.to(torch.bfloat16)
+    kw = k_norm_weight.to(torch.bfloat16)
+    fused_qk_norm_rope_3d_paired(q_r, k_r, L, H, eps, qw, kw, cos_bf16, sin_bf16)
+    return q, k
+
+
+def rmsnorm_qk_bf16(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm over the last dim of a bf16 tensor (sgl_fused_ops.py:102-111)."""
+    assert x.dtype == torch.bfloat16, f"rmsnorm_qk_bf16 needs bf16, got {x.dtype}"
+    orig_shape = x.shape
+    D = orig_shape[-1]
+    x_flat = x.reshape(-1, D)
+    if x_flat.stride(-1) != 1:
+        x_flat = x_flat.contiguous()
+    out = rmsnorm(x_flat, weight.to(dtype=torch.bfloat16), eps)
+    return out.reshape(orig_shape)
+
+
+def fused_add_gate(residual: torch.Tensor, x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+    """residual + x * gate[:, None] (sgl_fused_ops.py:114-117), a torch op as in the reference."""
+    return torch.addcmul(residual, x, gate.unsqueeze(1))
+
+
+# ---------------------------------------------------------------------------
+# Fused forms for callers that can use them.
+# ---------------------------------------------------------------------------
+def fused_add_gate_layernorm_modulate(
+    residual: torch.Tensor,
+    x: torch.Tensor,
+    gate: torch.Tensor,
+    shift: torch.Tensor,
+    scale: torch.Tensor,
+    *,
+    weight: Optional[torch.Tensor] = None,
+    bias: Optional[torch.Tensor] = None,
+    eps: float = 1e-6,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(residual', modulated) with residual' = residual + x * gate[:, None] and
+    modulated = fused_layernorm_modulate(residual', shift, scale) — the pair of
+    calls at dit.py:447-457 in one pass. residual [B, L, D] is updated in place
+    (it must be contiguous in its rows) and returned; gate/shift/scale [B, D]."""
+    B, L, D = x.shape
+    if not residual.is_contiguous():
+        raise RuntimeError("residual must be contiguous (it is updated in place)")
+    x_2d = x.reshape(B * L, D)
+    r_2d = residual.view(B * L, D)
+    if B == 1:
+        out = fused_add_layernorm_scale_shift(x_2d, r_2d, scale.reshape(D), shift.reshape(D),
+                                              gate=gate.reshape(D), gamma=weight, beta=bias, eps=eps)
+        return residual, out.reshape(B, L, D)
+    out = torch.empty_like(x)
+    for b in range(B):
+        out[b] = fused_add_layernorm_scale_shift(x[b], residual[b], scale.reshape(B, D)[b],
+                                                 shift.reshape(B, D)[b], gate=gate.reshape(B, D)[b],
+                                                 gamma=weight, beta=bias, eps=eps)
+    return residual, out
+
+
+def fused_qk_norm_rope_3d_grid_views(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    q_norm_weight: torch.Tensor,
+    k_norm_weight: torch.Tensor,
+    *,
+    grid_hw: Tuple[int, int],
+    t0: int,
+    rope_dims: Sequence[int],
+    theta: float,
+    source_id: float = 0.0,
+    source_theta: float = 256.0,
+    eps: float = 1e-6,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """In-place RMSNorm + RoPE of q, k [B, L, H, D] that may be strided views of
+    a packed qkv [B, L, 3, H, D] (heads contiguous per token). Angles come from
+    the grid position (frame f of L / (H_grid * W_grid) at t0 + f), with the
+    optional source-id rotation, exactly as Transformer3DModel builds its
+    tables (dit.py:745-809, 918-933); no tables are read. Returns (q, k)."""
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+        raise RuntimeError("q/k must be bf16")
+    B, L, H, D = q.shape
+    if q.stride(-1) != 1 or q.stride(-2) != D or k.stride(-1) != 1 or k.stride(-2) != D:
+        raise RuntimeError("heads of a token must be contiguous in q and k")
+    freqs = rope_freqs(D, rope_dims, theta, source_theta, device=q.device)
+    qw = q_norm_weight.to(torch.bfloat16).contiguous()
+    kw = k_norm_weight.to(torch.bfloat16).contiguous()
+    fused_qk_norm_rope_3d_grid(q, k, L, H, eps, qw, kw, freqs, rope_dims, grid_hw, t0, source_id)
+    return q, k
+
+
+def quantize_activation_fp8(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The activation side of Fp8Linear.forward (fp8_linear.py:140-144, 166):
+    x [..., K] -> (x_q fp8 e4m3fn [M, K], x_scale fp32 [M, 1]) with M = numel / K."""
+    x_2d = x.reshape(-1, x.shape[-1]).contiguous()
+    M, K = x_2d.shape
+    x_q = torch.empty((M, K), device=x_2d.device, dtype=torch.float8_e4m3fn)
+    x_scale = torch.empty((M, 1), device=x_2d.device, dtype=torch.float32)
+    sgl_per_token_quant_fp8(x_2d, x_q, x_scale)
+    return x_q, x_scale

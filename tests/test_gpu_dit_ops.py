@@ -1,0 +1,136 @@
+"""GPU tests of the DiT call shims (joyomni_ops.dit_ops), the counterparts of
+deploy/xvideo/models/dit/sgl_fused_ops.py and of Fp8Linear's activation
+quantization, against the CPU oracle composed the way the reference composes
+those calls. Tolerances as in the op tests (1 output ulp, floored at 2^-10 of
+the row/head scale); FP8 bytes and the gated residual bit-exact."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import assert_bf16_within_ulp, assert_within_ulp
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def rowmax(t):
+    return t.abs().amax(dim=-1, keepdim=True)
+
+
+@pytest.mark.parametrize("B,L,D", [(1, 1560, 3072), (2, 33, 512), (1, 1, 256)])
+@pytest.mark.parametrize("affine", [False, True])
+@pytest.mark.parametrize("mod_shape", ["BD", "B1D", "BLD"])
+def test_fused_layernorm_modulate(dev, B, L, D, affine, mod_shape):
+    from joyomni_ops import dit_ops
+    g = torch.Generator().manual_seed(B * L + D)
+    x = torch.randn(B, L, D, generator=g).to(torch.bfloat16)
+    shp = {"BD": (B, D), "B1D": (B, 1, D), "BLD": (B, L, D)}[mod_shape]
+    shift = (0.2 * torch.randn(shp, generator=g)).to(torch.bfloat16)
+    scale = (0.2 * torch.randn(shp, generator=g)).to(torch.bfloat16)
+    w = torch.randn(D, generator=g).to(torch.bfloat16) if affine else None
+    b = torch.randn(D, generator=g).to(torch.bfloat16) if affine else None
+    y = dit_ops.fused_layernorm_modulate(x.to(dev), shift.to(dev), scale.to(dev),
+                                         weight=None if w is None else w.to(dev),
+                                         bias=None if b is None else b.to(dev), eps=1e-6)
+    torch.cuda.synchronize()
+    # reference composition: sgl_fused_ops.py:41-54
+    sc = scale.unsqueeze(1) if scale.dim() == 2 else scale
+    sh = shift.unsqueeze(1) if shift.dim() == 2 else shift
+    sc = sc.expand(B, L, D).reshape(-1, D)
+    sh = sh.expand(B, L, D).reshape(-1, D)
+    ref = ops.norm_scale_shift_f32(x.reshape(-1, D), w, b, sc, sh, 0, 1e-6).reshape(B, L, D)
+    assert y.shape == (B, L, D)
+    assert_within_ulp(y.cpu(), ref, torch.bfloat16, rowmax(ref), what="layernorm_modulate")
+
+
+def test_fused_qk_norm_rope_3d_dit_tables(dev):
+    """Reference contract: q/k views of qkv, fp32 [1, L, D] tables; returns new tensors."""
+    from joyomni_ops import dit_ops
+    B, L, H, D = 1, 1560, 32, 128
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn(B, L, 3, H, D, generator=g).to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    cos, sin = ops.rope_grid_tables(1, 30, 52, 4, (16, 56, 56), 256.0, 1.0, 256.0)
+    d = qkv.to(dev)
+    q2, k2 = dit_ops.fused_qk_norm_rope_3d(d[:, :, 0], d[:, :, 1], qw.to(dev), kw.to(dev),
+                                           (cos[None].to(dev), sin[None].to(dev)), eps=1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(d.cpu(), qkv), "inputs must not be modified"
+    c16, s16 = (t.to(torch.bfloat16) for t in ops.half_tables(cos, sin))
+    for out, x, w in ((q2, qkv[:, :, 0], qw), (k2, qkv[:, :, 1], kw)):
+        ref = ops.qk_norm_rope_f32(x.contiguous(), w, c16, s16, 1e-6)
+        assert_bf16_within_ulp(out.cpu(), ref, rowmax(ref), what="dit qk tables")
+
+
+@pytest.mark.parametrize("sid", [0.0, 1.0, 2.0])
+def test_grid_views_on_packed_qkv(dev, sid):
+    """In place on strided views of qkv [B, L, 3, H, D]; v untouched; angles
+    from the DiT's grid (30x52, rope dims 16/56/56, theta 256, source id)."""
+    from joyomni_ops import dit_ops
+    B, L, H, D = 1, 1560, 32, 128
+    g = torch.Generator().manual_seed(6)
+    qkv = torch.randn(B, L, 3, H, D, generator=g).to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    d = qkv.to(dev)
+    dit_ops.fused_qk_norm_rope_3d_grid_views(d[:, :, 0], d[:, :, 1], qw.to(dev), kw.to(dev),
+                                             grid_hw=(30, 52), t0=9, rope_dims=(16, 56, 56),
+                                             theta=256.0, source_id=sid)
+    torch.cuda.synchronize()
+    out = d.cpu()
+    assert torch.equal(out[:, :, 2], qkv[:, :, 2])
+    cos, sin = ops.half_tables(*ops.rope_grid_tables(1, 30, 52, 9, (16, 56, 56), 256.0, sid, 256.0))
+    for j, w in ((0, qw), (1, kw)):
+        ref = ops.qk_norm_rope_f32(qkv[:, :, j].contiguous(), w, cos, sin, 1e-6)
+        assert_bf16_within_ulp(out[:, :, j], ref, rowmax(ref), what=f"grid views sid={sid}")
+
+
+def test_rmsnorm_qk_bf16_strided(dev):
+    from joyomni_ops import dit_ops
+    B, L, H, D = 1, 200, 8, 128
+    g = torch.Generator().manual_seed(7)
+    qkv = torch.randn(B, L, 3, H, D, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    y = dit_ops.rmsnorm_qk_bf16(qkv.to(dev)[:, :, 1], w.to(dev), eps=1e-6)
+    torch.cuda.synchronize()
+    ref = ops.rmsnorm_f32(qkv[:, :, 1].reshape(-1, D), w, 1e-6).reshape(B, L, H, D)
+    assert_bf16_within_ulp(y.cpu(), ref, rowmax(ref), what="rmsnorm_qk_bf16")
+
+
+@pytest.mark.parametrize("B", [1, 2])
+def test_fused_add_gate_layernorm_modulate(dev, B):
+    from joyomni_ops import dit_ops
+    L, D = 300, 3072
+    g = torch.Generator().manual_seed(8 + B)
+    res = torch.randn(B, L, D, generator=g).to(torch.bfloat16)
+    x = torch.randn(B, L, D, generator=g).to(torch.bfloat16)
+    six = torch.randn(B, 6 * D, generator=g).to(torch.bfloat16)  # modulation vector, chunked views
+    shift, scale, gate = six[:, :D], six[:, D:2 * D], six[:, 2 * D:3 * D]
+    rd = res.to(dev)
+    sd = six.to(dev)
+    r2, y = dit_ops.fused_add_gate_layernorm_modulate(rd, x.to(dev), sd[:, 2 * D:3 * D],
+                                                      sd[:, :D], sd[:, D:2 * D], eps=1e-6)
+    torch.cuda.synchronize()
+    # reference: fused_add_gate then fused_layernorm_modulate (dit.py:447-457)
+    ref_res = torch.addcmul(res.float(), x.float(), gate.float().unsqueeze(1)).to(torch.bfloat16)
+    assert r2.data_ptr() == rd.data_ptr()
+    assert torch.equal(rd.cpu(), ref_res), "gated residual not bit-exact"
+    ref = torch.stack([ops.norm_scale_shift_f32(ref_res[b], None, None, scale[b].expand(L, D),
+                                                shift[b].expand(L, D), 0, 1e-6) for b in range(B)])
+    assert_within_ulp(y.cpu(), ref, torch.bfloat16, rowmax(ref), what="add_gate_ln")
+    # the unfused shim keeps the reference contract
+    assert torch.equal(dit_ops.fused_add_gate(res.to(dev), x.to(dev), gate.to(dev)).cpu(),
+                       torch.addcmul(res.to(dev), x.to(dev), gate.to(dev).unsqueeze(1)).cpu())
+
+
+def test_quantize_activation_fp8(dev):
+    from joyomni_ops import dit_ops
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(2, 1560, 4096, generator=g).to(torch.bfloat16)
+    xq, xs = dit_ops.quantize_activation_fp8(x.to(dev))
+    torch.cuda.synchronize()
+    qo, so = ops.per_token_quant_fp8(x.reshape(-1, 4096))
+    assert xq.shape == (3120, 4096) and xs.shape == (3120, 1)
+    assert torch.equal(xq.view(torch.uint8).cpu(), qo) and torch.equal(xs.view(-1).cpu(), so)
