@@ -46,17 +46,17 @@ struct QKArgs {
   int cache_slots, slot_start;  // KVC
 };
 
-// Rotation coefficients of pair p of a token at grid position (t, h, w),
-// following the table builders rope.py:46-51 (angle = pos * freq in fp32)
-// and the source-id composition dit.py:931-932.
-__device__ __forceinline__ void grid_pair_cs(const QKArgs& a, int P, int p, float t, float h,
-                                             float w, float& c, float& s) {
-  const float pos = p < a.pairs_t ? t : (p < a.pairs_t + a.pairs_h ? h : w);
-  const float ang = pos * a.freqs[p];
+// Rotation coefficients of a pair at grid position pos on its axis, from its
+// axis frequency f and source-id frequency fr, following the table builders
+// rope.py:46-51 (angle = pos * freq in fp32) and the source-id composition
+// dit.py:931-932 (angle addition, skipped when the source id is 0).
+__device__ __forceinline__ void grid_pair_cs(float pos, float f, float source_id, float fr,
+                                             float& c, float& s) {
+  const float ang = pos * f;
   sincosf(ang, &s, &c);
-  if (a.source_id != 0.f) {
+  if (source_id != 0.f) {
     float sr, cr;
-    sincosf(a.source_id * a.freqs[P + p], &sr, &cr);
+    sincosf(source_id * fr, &sr, &cr);
     const float c2 = c * cr - s * sr;
     const float s2 = s * cr + c * sr;
     c = c2;
@@ -65,88 +65,140 @@ __device__ __forceinline__ void grid_pair_cs(const QKArgs& a, int P, int p, floa
 }
 
 // SPLIT = 1: one wave does q and k of its token. SPLIT = 2: two waves per
-// token, the even one q and the odd one k (twice the waves, for sequences
-// too short to fill the chip; the rotation coefficients are then evaluated
-// by both waves).
+// token, the even one q and the odd one k. SPLIT = 4: four waves per token,
+// q and k each split into two halves of their head groups. The rotation
+// coefficients are evaluated by every wave.
+//
+// Issue order matters: the memory counter retires loads in order, so the
+// small parameter loads (rotation table or frequencies, weights) go out
+// first, then the row loads, and only then is anything waited on — the
+// sincos then overlaps the row loads instead of delaying their issue.
 template <int HD, int G, int MODE, int SPLIT>
 __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
   constexpr int LPH = HD / 8;      // lanes per head
   constexpr int P = HD / 2;        // rotation pairs per head
   constexpr int K = P > 64 ? P / 64 : 1;  // pairs evaluated per lane in grid modes
+  constexpr int NS = SPLIT == 1 ? 2 : 1;  // tensor streams per wave (q and k, or one)
   const int lane = threadIdx.x % kWave;
   const int64_t wid = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + threadIdx.x / kWave;
   const int64_t tok = wid / SPLIT;
-  const bool do_q = SPLIT == 1 || (wid % SPLIT) == 0;
-  const bool do_k = SPLIT == 1 || (wid % SPLIT) == 1;
+  const int part = static_cast<int>(wid % SPLIT);
   if (tok >= a.tokens) return;
   const int64_t b = tok / a.seq_len;
   const int n = static_cast<int>(tok - b * a.seq_len);
   const int pl = lane % LPH;  // this lane holds elements 8*pl .. 8*pl+7 of its head
 
-  char* qrow = static_cast<char*>(a.q) + (b * a.q_bs + n * a.q_ts) * 2;
-  const char* krow = static_cast<const char*>(a.k) + (b * a.k_bs + n * a.k_ts) * 2;
-
-  const int groups = (a.row_elems + 511) / 512;
-  // Rotation coefficients for pairs 4*pl .. 4*pl+3.
-  float c[4], s[4];
-  int64_t kdst_tok;  // destination token of the rotated k
-  if constexpr (MODE == kTable) {
-    const u32x2 cw = *reinterpret_cast<const u32x2*>(static_cast<const char*>(a.cos) +
-                                                     (static_cast<int64_t>(n) * P + 4 * pl) * 2);
-    const u32x2 sw = *reinterpret_cast<const u32x2*>(static_cast<const char*>(a.sin) +
-                                                     (static_cast<int64_t>(n) * P + 4 * pl) * 2);
-    c[0] = bf16_lo(cw.x); c[1] = bf16_hi(cw.x); c[2] = bf16_lo(cw.y); c[3] = bf16_hi(cw.y);
-    s[0] = bf16_lo(sw.x); s[1] = bf16_hi(sw.x); s[2] = bf16_lo(sw.y); s[3] = bf16_hi(sw.y);
-    kdst_tok = n;
-  } else {
+  // Destination token of the rotated k (grid modes: frame ring slot).
+  int64_t kdst_tok = n;
+  int f = 0, rr = 0;
+  if constexpr (MODE != kTable) {
     const int frame_tokens = a.grid_h * a.grid_w;
-    const int f = n / frame_tokens;
-    const int rr = n - f * frame_tokens;
-    const int hh = rr / a.grid_w;
-    const int ww = rr - hh * a.grid_w;
-    const float t = static_cast<float>(a.t0 + f);
-    float mc[K], ms[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) grid_pair_cs(a, P, (lane * K + k) % P, t, hh, ww, mc[k], ms[k]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = 4 * pl + i;
-      const int src = (p / K) << 2;  // ds_bpermute byte address of the owning lane
-      c[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, mc[i % K])));
-      s[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, ms[i % K])));
-    }
+    f = n / frame_tokens;
+    rr = n - f * frame_tokens;
     if constexpr (MODE == kKvCache)
       kdst_tok = static_cast<int64_t>((a.slot_start + f) % a.cache_slots) * frame_tokens + rr;
-    else
-      kdst_tok = n;
   }
+  char* qrow = static_cast<char*>(a.q) + (b * a.q_bs + n * a.q_ts) * 2;
+  const char* krow = static_cast<const char*>(a.k) + (b * a.k_bs + n * a.k_ts) * 2;
   char* kdst = static_cast<char*>(a.kout) + (b * a.o_bs + kdst_tok * a.o_ts) * 2;
+  const char* src[NS];
+  char* dst[NS];
+  const char* wsrc[NS];
+  if constexpr (NS == 2) {
+    src[0] = qrow; dst[0] = qrow; wsrc[0] = static_cast<const char*>(a.qw);
+    src[1] = krow; dst[1] = kdst; wsrc[1] = static_cast<const char*>(a.kw);
+  } else {
+    const bool is_k = (part & 1) != 0;  // wave-uniform
+    src[0] = is_k ? krow : qrow;
+    dst[0] = is_k ? kdst : qrow;
+    wsrc[0] = static_cast<const char*>(is_k ? a.kw : a.qw);
+  }
+  // Head groups (512 elements each) this wave handles: all, or one half.
+  const int all_groups = (a.row_elems + 511) / 512;
+  const int half_groups = (all_groups + 1) / 2;
+  const int gbeg = SPLIT == 4 ? (part >> 1) * half_groups : 0;
+  const int groups = SPLIT == 4 ? min(all_groups, gbeg + half_groups) : all_groups;
 
-  const u32x4 wq = ld16(static_cast<const char*>(a.qw) + pl * 16);
-  const u32x4 wk = ld16(static_cast<const char*>(a.kw) + pl * 16);
+  // 1. Parameter loads: rotation table row or frequencies, weights.
+  u32x2 cw, sw;
+  float fq[K], fr[K];
+  if constexpr (MODE == kTable) {
+    const int64_t off = (static_cast<int64_t>(n) * P + 4 * pl) * 2;
+    cw = *reinterpret_cast<const u32x2*>(static_cast<const char*>(a.cos) + off);
+    sw = *reinterpret_cast<const u32x2*>(static_cast<const char*>(a.sin) + off);
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int p = (lane * K + k) % P;
+      fq[k] = a.freqs[p];
+      fr[k] = a.source_id != 0.f ? a.freqs[P + p] : 0.f;
+    }
+  }
+  u32x4 wv[NS];
+#pragma unroll
+  for (int t = 0; t < NS; ++t) wv[t] = ld16(wsrc[t] + pl * 16);
 
-  for (int g0 = 0; g0 < groups; g0 += G) {
-    u32x4 xq[G], xk[G];
+  // 2. Row loads of the first batch of head groups. Loads are never
+  // predicated (a predicated load's join forces an early wait): a chunk
+  // outside this wave's range reads a valid chunk of the same row instead.
+  // Its lanes form whole heads (a chunk holds 512/HD complete heads), so
+  // their values stay within heads that are never stored.
+  const int e_safe = (lane * 8) % a.row_elems;
+  u32x4 x[NS][G];
+  auto load_batch = [&](int g0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int e = (g0 + g) * 512 + lane * 8;
-      const bool ok = e < a.row_elems;
-      xq[g] = (ok && do_q) ? ld16_nt(qrow + e * 2) : u32x4{0u, 0u, 0u, 0u};
-      xk[g] = (ok && do_k) ? ld16_nt(krow + e * 2) : u32x4{0u, 0u, 0u, 0u};
+      const bool ok = (g0 + g) < groups && e < a.row_elems;  // own range, inside the row
+      const int el = ok ? e : e_safe;
+#pragma unroll
+      for (int t = 0; t < NS; ++t) x[t][g] = ld16_nt(src[t] + el * 2);
+    }
+  };
+  load_batch(gbeg);
+  // Keep every row load of the first batch ahead of the angle math below,
+  // which waits for the parameter loads.
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. Rotation coefficients for pairs 4*pl .. 4*pl+3 (overlaps the row loads).
+  float c[4], s[4];
+  if constexpr (MODE == kTable) {
+    c[0] = bf16_lo(cw.x); c[1] = bf16_hi(cw.x); c[2] = bf16_lo(cw.y); c[3] = bf16_hi(cw.y);
+    s[0] = bf16_lo(sw.x); s[1] = bf16_hi(sw.x); s[2] = bf16_lo(sw.y); s[3] = bf16_hi(sw.y);
+  } else {
+    const int hh = rr / a.grid_w;
+    const int ww = rr - hh * a.grid_w;
+    const float tpos = static_cast<float>(a.t0 + f);
+    float mc[K], ms[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int p = (lane * K + k) % P;
+      const float pos = p < a.pairs_t ? tpos
+                      : (p < a.pairs_t + a.pairs_h ? static_cast<float>(hh) : static_cast<float>(ww));
+      grid_pair_cs(pos, fq[k], a.source_id, fr[k], mc[k], ms[k]);
     }
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      if ((half == 0 && !do_q) || (half == 1 && !do_k)) continue;  // wave-uniform
-      const u32x4& wv = half == 0 ? wq : wk;
+    for (int i = 0; i < 4; ++i) {
+      const int p = 4 * pl + i;
+      const int owner = (p / K) << 2;  // ds_bpermute byte address of the owning lane
+      c[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(owner, __builtin_bit_cast(int, mc[i % K])));
+      s[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(owner, __builtin_bit_cast(int, ms[i % K])));
+    }
+  }
+
+  // 4. Normalize, rotate, store; further batches only when H*D > G*512.
+  for (int g0 = gbeg; g0 < groups; g0 += G) {
+    if (g0 != gbeg) load_batch(g0);
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const int e = (g0 + g) * 512 + lane * 8;
-        const u32x4& xv = half == 0 ? xq[g] : xk[g];
-        float x[8];
-        unpack<BF16>(xv, x);
+        float xv[8];
+        unpack<BF16>(x[t][g], xv);
         float ss = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+        for (int j = 0; j < 8; ++j) ss += xv[j] * xv[j];
         ss = allreduce<LPH, OpSum>(ss);
         const float r = rsqrtf(ss * (1.0f / HD) + a.eps);
         float o[8];
@@ -154,38 +206,38 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
         for (int i = 0; i < 4; ++i) {
           // e = x * (r * w) as fused_qknorm_rope_3d_kernel.cu:117, then the
           // pair rotation of :128-131.
-          const float e0 = x[2 * i] * (r * elem<BF16>(wv, 2 * i));
-          const float e1 = x[2 * i + 1] * (r * elem<BF16>(wv, 2 * i + 1));
+          const float e0 = xv[2 * i] * (r * elem<BF16>(wv[t], 2 * i));
+          const float e1 = xv[2 * i + 1] * (r * elem<BF16>(wv[t], 2 * i + 1));
           o[2 * i] = e0 * c[i] - e1 * s[i];
           o[2 * i + 1] = e0 * s[i] + e1 * c[i];
         }
-        if (e < a.row_elems) {
-          if (half == 0)
-            st16_nt(qrow + e * 2, pack<BF16>(o));
-          else
-            st16_nt(kdst + e * 2, pack<BF16>(o));
-        }
+        if ((g0 + g) < groups && e < a.row_elems) st16_nt(dst[t] + e * 2, pack<BF16>(o));
       }
     }
   }
 }
 
 // Waves per token. Two (q and k on separate waves) measured faster on MI355X
-// at every BASELINE shape (3510 tokens: 19.0 -> 17.5 us; 10530 tokens:
-// 46.4 -> 45.2 us): the extra waves hide HBM latency better than the saved
-// rotation-coefficient work. JO_QK_SPLIT=1|2 overrides the choice (launch
-// shape only; results are identical).
-int qk_split(int64_t /*tokens*/) {
+// than one at every BASELINE shape (3510 tokens: 19.0 -> 17.5 us; 10530
+// tokens: 46.4 -> 45.2 us): the extra waves hide HBM latency better than the
+// saved rotation-coefficient work. Four (each of q and k split into halves of
+// its head groups) helps further when the grid is small (3510 tokens:
+// 17.3 -> 17.0 us) and costs at 10530 tokens (44.5 -> 45.5 us), so it is used
+// below 8192 tokens. JO_QK_SPLIT=1|2|4 overrides the choice (launch shape
+// only; results are identical).
+int qk_split(int64_t tokens, int all_groups) {
   const char* e = getenv("JO_QK_SPLIT");
   const int forced = e ? atoi(e) : 0;
   if (forced == 1 || forced == 2) return forced;
-  return 2;
+  if (forced == 4) return all_groups >= 2 ? 4 : 2;
+  return (tokens < 8192 && all_groups >= 2) ? 4 : 2;
 }
 
 template <int MODE>
 int launch_qk(const QKArgs& a, int head_dim, hipStream_t stream, const char* op) {
-  const int groups = (a.row_elems + 511) / 512;
-  const int split = qk_split(a.tokens);
+  const int all_groups = (a.row_elems + 511) / 512;
+  const int split = qk_split(a.tokens, all_groups);
+  const int groups = split == 4 ? (all_groups + 1) / 2 : all_groups;  // per wave
   const dim3 grid(static_cast<unsigned>((a.tokens * split + 3) / 4));
   auto go = [&](auto hd, auto sp) {
     constexpr int HD = decltype(hd)::value;
@@ -194,6 +246,8 @@ int launch_qk(const QKArgs& a, int head_dim, hipStream_t stream, const char* op)
       hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 1, MODE, S>), grid, dim3(kBlock), 0, stream, a);
     else if (groups <= 2)
       hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 2, MODE, S>), grid, dim3(kBlock), 0, stream, a);
+    else if (groups <= 3)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 3, MODE, S>), grid, dim3(kBlock), 0, stream, a);
     else if (groups <= 4)
       hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 4, MODE, S>), grid, dim3(kBlock), 0, stream, a);
     else if (groups <= 6)
@@ -202,7 +256,9 @@ int launch_qk(const QKArgs& a, int head_dim, hipStream_t stream, const char* op)
       hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 8, MODE, S>), grid, dim3(kBlock), 0, stream, a);
   };
   auto go_hd = [&](auto hd) {
-    if (split == 2)
+    if (split == 4)
+      go(hd, std::integral_constant<int, 4>{});
+    else if (split == 2)
       go(hd, std::integral_constant<int, 2>{});
     else
       go(hd, std::integral_constant<int, 1>{});
