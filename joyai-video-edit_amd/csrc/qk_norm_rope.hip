@@ -46,6 +46,43 @@ struct QKArgs {
   int cache_slots, slot_start;  // KVC
 };
 
+// sin and cos of an fp32 angle a. For |a| <= 65536: Cody-Waite reduction by
+// pi/2 with pi/2 split into three fp32 parts (the first FMA step is exact for
+// |a| >= 1 because k*P1 and a are multiples of 2^-23 there), then the Taylor
+// series of sin (to r^9) and cos (to r^10) on [-pi/4, pi/4], whose truncation
+// is below 2e-9. The absolute error is a few 2^-25, far inside the bf16 output
+// rounding. Larger or non-finite angles take sincosf.
+__device__ __forceinline__ void sincos_reduced(float a, float& s, float& c) {
+  if (__builtin_expect(!(fabsf(a) <= 65536.f), 0)) {
+    sincosf(a, &s, &c);
+    return;
+  }
+  constexpr float kTwoOverPi = 0x1.45f306p-1f;
+  constexpr float kP1 = 0x1.921fb6p+0f;   // fp32(pi/2)
+  constexpr float kP2 = -0x1.777a5cp-25f;  // fp32(pi/2 - P1)
+  constexpr float kP3 = -0x1.ee59dap-50f;  // fp32(pi/2 - P1 - P2)
+  const float k = __builtin_rintf(a * kTwoOverPi);
+  float r = __builtin_fmaf(-k, kP1, a);
+  r = __builtin_fmaf(-k, kP2, r);
+  r = __builtin_fmaf(-k, kP3, r);
+  const float z = r * r;
+  float ps = __builtin_fmaf(z, 1.f / 362880.f, -1.f / 5040.f);
+  ps = __builtin_fmaf(z, ps, 1.f / 120.f);
+  ps = __builtin_fmaf(z, ps, -1.f / 6.f);
+  const float sr = __builtin_fmaf(r * z, ps, r);
+  float pc = __builtin_fmaf(z, -1.f / 3628800.f, 1.f / 40320.f);
+  pc = __builtin_fmaf(z, pc, -1.f / 720.f);
+  pc = __builtin_fmaf(z, pc, 1.f / 24.f);
+  pc = __builtin_fmaf(z, pc, -0.5f);
+  const float cr = __builtin_fmaf(z, pc, 1.f);
+  // Quadrant q = k mod 4: (sin, cos) = (S, C), (C, -S), (-S, -C), (-C, S).
+  const int q = static_cast<int>(k) & 3;
+  const float sv = (q & 1) ? cr : sr;
+  const float cv = (q & 1) ? sr : cr;
+  s = (q & 2) ? -sv : sv;
+  c = ((q + 1) & 2) ? -cv : cv;
+}
+
 // Rotation coefficients of a pair at grid position pos on its axis, from its
 // axis frequency f and source-id frequency fr, following the table builders
 // rope.py:46-51 (angle = pos * freq in fp32) and the source-id composition
@@ -53,10 +90,10 @@ struct QKArgs {
 __device__ __forceinline__ void grid_pair_cs(float pos, float f, float source_id, float fr,
                                              float& c, float& s) {
   const float ang = pos * f;
-  sincosf(ang, &s, &c);
+  sincos_reduced(ang, s, c);
   if (source_id != 0.f) {
     float sr, cr;
-    sincosf(source_id * fr, &sr, &cr);
+    sincos_reduced(source_id * fr, sr, cr);
     const float c2 = c * cr - s * sr;
     const float s2 = s * cr + c * sr;
     c = c2;

@@ -127,6 +127,10 @@ GRID_CASES = [
     (1, 3, 4, 4, 5, 64, 100, (16, 24, 24), 10000.0, 2.0),
     (1, 2, 3, 5, 2, 256, 3, (64, 96, 96), 10000.0, 0.0),
     (1, 1, 45, 78, 24, 128, 0, (44, 42, 42), 10000.0, 0.0),   # C0
+    # Large angles: many multiples of pi/2 to reduce, and (t0 and source id
+    # above 65536) the library-sincos branch, mixed with small angles in a wave.
+    (1, 2, 3, 4, 2, 128, 4000, (44, 42, 42), 10000.0, 3.0),
+    (1, 1, 4, 6, 2, 128, 70000, (44, 42, 42), 10000.0, 70001.0),
 ]
 
 
