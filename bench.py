@@ -5,7 +5,8 @@
 A "step" is one call of an op over one batch of synthetic input. The headline
 workload (`value`) is BASELINE config 1: per-token FP8 e4m3 quantization of a
 bf16 [10530, 3072] activation. Every other BASELINE config is timed the same
-way and reported under "ops".
+way and reported under "ops", as is N3 (the gated residual + LayerNorm +
+AdaLN with the per-token FP8 epilogue, a next-row workload at the C2 shape).
 
 Timing: W eager warmup calls, then K calls captured into one HIP graph and
 replayed once untimed and once timed between HIP events recorded on the
@@ -146,6 +147,9 @@ def cpu_fn(cfg):
     if cfg.op == "add_ln":
         return lambda t: ops.add_layernorm_scale_shift(t["x"], t["residual"], None, None, None,
                                                        t["scale"], t["shift"], d["eps"])
+    if cfg.op == "add_ln_quant":
+        return lambda t: ops.norm_scale_shift_quant_fp8(t["x"], t["residual"], t["gate"], None,
+                                                        None, t["scale"], t["shift"], 0, d["eps"])
     B, L, H, D = d["B"], d["L"], d["H"], d["D"]
     frames = L // (d["grid"][0] * d["grid"][1])
     cos, sin = ops.half_tables(*ops.rope_grid_tables(frames, *d["grid"], d["t0"], d["rope_dims"],

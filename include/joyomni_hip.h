@@ -208,6 +208,34 @@ int jo_rmsnorm_quant_fp8(const void* x, int64_t x_stride, const void* weight, vo
                          int64_t q_stride, float* out_s, int64_t M, int64_t N, int dtype,
                          float eps, int64_t group_size, void* stream);
 
+/* ------------------------------------------------------------------------
+ * (Gated residual add +) Layer|RMS norm + AdaLN, quantized per token to FP8
+ * instead of written:
+ *   residual <- round(residual + x * gate)   when residual != NULL (gate = 1
+ *                                            if NULL), then v = residual;
+ *   v = x                                    when residual == NULL;
+ *   y = round_dtype(Norm(v)(g, b) * (1 + scale) + shift)   (never stored);
+ *   s[m] = amax|y[m,:]| / 448; q = e4m3fn_rne(clamp(y * inv, +-448)),
+ *   inv = (s == 0) ? 0 : 1/s.
+ * Equal, byte for byte, to jo_fused_add_layernorm_scale_shift (or
+ * jo_fused_norm_scale_shift) followed by jo_sgl_per_token_quant_fp8 on its y.
+ * No reference counterpart: it fuses the DiT block's gated residual and
+ * modulated norm (deploy/xvideo/models/dit/dit.py:447-476,
+ * sgl_fused_ops.py:30-54,114-117, fused_norm_scale_shift.cu:88-142) with the
+ * activation quantization Fp8Linear.forward runs on that y
+ * (fp8_linear.py:138-169, per_token_quant_fp8.cu:56-82).
+ * x: [M, N]; residual: [M, N] or NULL; gate, scale, shift: row-strided,
+ * stride 0 = one [N] row for all; gamma/beta as in jo_fused_norm_scale_shift;
+ * out_q: fp8 [M, N] with row stride q_stride; out_s: fp32 [M].
+ * dtype bf16 or fp16; norm_type JO_NORM_LAYER or JO_NORM_RMS; N % 4 == 0.
+ * ------------------------------------------------------------------------ */
+int jo_norm_scale_shift_quant_fp8(const void* x, int64_t x_stride, void* residual,
+                                  int64_t res_stride, const void* gate, int64_t gate_stride,
+                                  const void* gamma, const void* beta, const void* scale,
+                                  int64_t scale_stride, const void* shift, int64_t shift_stride,
+                                  void* out_q, int64_t q_stride, float* out_s, int64_t M,
+                                  int64_t N, int dtype, int norm_type, float eps, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -106,6 +106,23 @@ __device__ __forceinline__ u32x4 pack<F32>(const float (&f)[4]) {
                __builtin_bit_cast(uint32_t, f[2]), __builtin_bit_cast(uint32_t, f[3])};
 }
 
+// v rounded (nearest-even) to the element type and widened back to fp32:
+// the value a store of v followed by a load would give.
+template <class Tag>
+__device__ __forceinline__ float round_to(float v);
+template <>
+__device__ __forceinline__ float round_to<BF16>(float v) {
+  return float(__bf16(v));
+}
+template <>
+__device__ __forceinline__ float round_to<F16>(float v) {
+  return float(_Float16(v));
+}
+template <>
+__device__ __forceinline__ float round_to<F32>(float v) {
+  return v;
+}
+
 // Scalar element load / store (generic fallback kernels).
 template <class Tag>
 __device__ __forceinline__ float load_elem(const void* p, int64_t i);
@@ -191,6 +208,19 @@ __device__ __forceinline__ uint32_t fp8x4(float a, float b, float c, float d) {
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return static_cast<uint32_t>(w);
+}
+
+// Quantizes 8 fp32 values with the reference's rule and returns 8 bytes.
+// CLAMP = false only where the inputs are finite and inv is finite (see fp8x4).
+template <bool CLAMP = true>
+__device__ __forceinline__ u32x2 quant8(const float (&v)[8], float inv) {
+  return u32x2{fp8x4<CLAMP>(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv),
+               fp8x4<CLAMP>(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv)};
+}
+
+// One value -> its e4m3fn byte, with the clamp (any input).
+__device__ __forceinline__ uint8_t fp8_byte(float v) {
+  return static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(v), 0.f, 0, false) & 0xff);
 }
 
 // max(m, |v|) propagating NaN (IEEE maximum; v_maximum3_f32 on gfx950).

@@ -1,5 +1,6 @@
-// LayerNorm / RMSNorm with AdaLN modulation, standalone RMSNorm, and the
-// fused (gated) residual add + LayerNorm + AdaLN.
+// LayerNorm / RMSNorm with AdaLN modulation, standalone RMSNorm, the fused
+// (gated) residual add + LayerNorm + AdaLN, and both with a per-token FP8
+// epilogue in place of the bf16/fp16 output.
 //
 // Row kernels: LPR lanes per row, CH 16-byte chunks per lane held in
 // registers, so x (and the residual) are read from HBM once and y (and the
@@ -30,6 +31,9 @@ struct NormArgs {
   int64_t M;
   int N;
   float eps;
+  uint8_t* q = nullptr;  // FP8 epilogue: e4m3fn rows (stride qs) and fp32 scales [M]
+  int64_t qs = 0;
+  float* s = nullptr;
 };
 
 constexpr int kLayer = JO_NORM_LAYER;
@@ -68,13 +72,20 @@ __device__ __forceinline__ u32x4 ld_mod(const void* base, int64_t stride, int64_
 // y = Norm(v)(gamma, beta) * (1 + scale) + shift, follows
 // fused_norm_scale_shift.cu:88-142. With ADD, v is first formed as
 // round(res + x * gate) and written back to res (sgl_fused_ops.py:114-117).
+// With QNT, y is rounded to the row dtype as the unfused op would store it,
+// and that row is quantized per token by the rule of per_token_quant_fp8.cu:
+// 56-82 (the input Fp8Linear.forward quantizes, fp8_linear.py:138-169)
+// instead of being written.
 // ---------------------------------------------------------------------------
-template <class Tag, int LPR, int CH, int NT, bool ADD>
+template <class Tag, int LPR, int CH, int NT, bool ADD, bool QNT>
 __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
   constexpr int V = Tag::kVec;
   constexpr int RPB = kBlock / LPR;
+  static_assert(!QNT || V == 8, "the FP8 epilogue takes 16-bit rows");
   __shared__ float red_a[kBlock / kWave];
   __shared__ float red_b[kBlock / kWave];
+  __shared__ float red_c[kBlock / kWave];
+  __shared__ float red_d[kBlock / kWave];
   const int lane = threadIdx.x % LPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
   const bool row_ok = row < a.M;
@@ -149,9 +160,15 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
   // Output.
   const bool affine = a.gamma != nullptr;
   const bool has_beta = affine && a.beta != nullptr && NT == kLayer;
+  float yq[QNT ? CH : 1][8];  // FP8 epilogue: the rounded y of this lane
+  float ymax = 0.f;           // and its NaN-propagating maximum |y|
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * V;
+    if constexpr (QNT) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) yq[i][j] = 0.f;
+    }
     if (!(row_ok && e < N)) continue;
     const u32x4 sc = ld_mod<Tag>(a.scale, a.scs, row, e);
     const u32x4 sh = ld_mod<Tag>(a.shift, a.shs, row, e);
@@ -166,12 +183,48 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
       if (has_beta) t = t + elem<Tag>(bt, j);
       o[j] = t * (1.f + elem<Tag>(sc, j)) + elem<Tag>(sh, j);
     }
-    st_row<Tag>(a.y, row * a.ys, e, pack<Tag>(o));
+    if constexpr (QNT) {
+      const u32x4 yr = pack<Tag>(o);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        yq[i][j] = elem<Tag>(yr, j);
+        ymax = nan_max_abs(ymax, yq[i][j]);
+      }
+    } else {
+      st_row<Tag>(a.y, row * a.ys, e, pack<Tag>(o));
+    }
+  }
+  if constexpr (QNT) {
+    // As quant_rows_kernel: a finite NaN-propagating maximum is the
+    // reference's amax and lets the clamp go; workgroups with a non-finite
+    // row take the NaN-skipping maximum and clamp.
+    float amax = row_reduce<LPR, OpAmax>(ymax, red_c);
+    const bool finite_row = finite_bits(amax);
+    if (__syncthreads_or(!finite_row)) {
+      float m = 0.f;
+#pragma unroll
+      for (int i = 0; i < CH; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(yq[i][j]));
+      amax = row_reduce<LPR, OpAmax>(m, red_d);
+    }
+    const float scale = amax / kFp8Max;
+    if (row_ok && lane == 0) a.s[row] = scale;
+    const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;
+    const bool fast = finite_row && finite_bits(inv);
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int e = (i * LPR + lane) * V;
+      if (row_ok && e < N)
+        st8_nt(a.q + row * a.qs + e, fast ? quant8<false>(yq[i], inv) : quant8<true>(yq[i], inv));
+    }
   }
 }
 
 // One row per workgroup with element-wise accesses (any N, any alignment).
-template <class Tag, int NT, bool ADD>
+// With QNT, y is evaluated twice (for the row maximum, then to quantize):
+// both evaluations are the same operations on the same values.
+template <class Tag, int NT, bool ADD, bool QNT>
 __global__ __launch_bounds__(kBlock) void norm_mod_generic_kernel(const NormArgs a) {
   __shared__ float red[kBlock / kWave];
   const int64_t row = blockIdx.x;
@@ -211,23 +264,35 @@ __global__ __launch_bounds__(kBlock) void norm_mod_generic_kernel(const NormArgs
   }
   const bool affine = a.gamma != nullptr;
   const bool has_beta = affine && a.beta != nullptr && NT == kLayer;
-  for (int i = threadIdx.x; i < N; i += kBlock) {
+  auto y_at = [&](int i) {
     const float v = load_elem<Tag>(src, so_src + i);
     float t = (NT == kLayer) ? (v - mean) * r : v * r;
     if (affine) t = t * load_elem<Tag>(a.gamma, i);
     if (has_beta) t = t + load_elem<Tag>(a.beta, i);
-    store_elem<Tag>(a.y, yo + i,
-                    t * (1.f + load_elem<Tag>(a.scale, so + i)) + load_elem<Tag>(a.shift, ho + i));
+    return t * (1.f + load_elem<Tag>(a.scale, so + i)) + load_elem<Tag>(a.shift, ho + i);
+  };
+  if constexpr (QNT) {
+    float amax = 0.f;
+    for (int i = threadIdx.x; i < N; i += kBlock) amax = fmaxf(amax, fabsf(round_to<Tag>(y_at(i))));
+    amax = block_reduce<OpAmax>(amax, red);
+    const float scale = amax / kFp8Max;
+    if (threadIdx.x == 0) a.s[row] = scale;
+    const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;
+    for (int i = threadIdx.x; i < N; i += kBlock)
+      a.q[row * a.qs + i] = fp8_byte(round_to<Tag>(y_at(i)) * inv);
+  } else {
+    for (int i = threadIdx.x; i < N; i += kBlock) store_elem<Tag>(a.y, yo + i, y_at(i));
   }
 }
 
-template <class Tag, int NT, bool ADD>
+template <class Tag, int NT, bool ADD, bool QNT>
 int launch_norm_mod(const NormArgs& a, hipStream_t stream, const char* op) {
   const int b = Tag::kBytes;
-  bool vec_ok = (a.N % Tag::kVec == 0) && aligned(a.x, 16) && (a.xs * b) % 16 == 0 &&
-                aligned(a.y, 16) && (a.ys * b) % 16 == 0 && aligned(a.scale, 16) &&
-                (a.scs * b) % 16 == 0 && aligned(a.shift, 16) && (a.shs * b) % 16 == 0 &&
-                aligned(a.gamma, 16) && aligned(a.beta, 16);
+  const bool out_ok = QNT ? (aligned(a.q, 8) && a.qs % 8 == 0)
+                          : (aligned(a.y, 16) && (a.ys * b) % 16 == 0);
+  bool vec_ok = (a.N % Tag::kVec == 0) && aligned(a.x, 16) && (a.xs * b) % 16 == 0 && out_ok &&
+                aligned(a.scale, 16) && (a.scs * b) % 16 == 0 && aligned(a.shift, 16) &&
+                (a.shs * b) % 16 == 0 && aligned(a.gamma, 16) && aligned(a.beta, 16);
   if (ADD)
     vec_ok = vec_ok && aligned(a.res, 16) && (a.rs * b) % 16 == 0 && aligned(a.gate, 16) &&
              (a.gs * b) % 16 == 0;
@@ -236,12 +301,12 @@ int launch_norm_mod(const NormArgs& a, hipStream_t stream, const char* op) {
     launched = dispatch_row_shape<Tag::kVec, true>(a.N, [&](auto lpr, auto ch) {
       constexpr int LPR = decltype(lpr)::value;
       constexpr int CH = decltype(ch)::value;
-      hipLaunchKernelGGL((norm_mod_kernel<Tag, LPR, CH, NT, ADD>), dim3(row_blocks(a.M, LPR)),
-                         dim3(kBlock), 0, stream, a);
+      hipLaunchKernelGGL((norm_mod_kernel<Tag, LPR, CH, NT, ADD, QNT>),
+                         dim3(row_blocks(a.M, LPR)), dim3(kBlock), 0, stream, a);
     });
   }
   if (!launched)
-    hipLaunchKernelGGL((norm_mod_generic_kernel<Tag, NT, ADD>), dim3(a.M), dim3(kBlock), 0,
+    hipLaunchKernelGGL((norm_mod_generic_kernel<Tag, NT, ADD, QNT>), dim3(a.M), dim3(kBlock), 0,
                        stream, a);
   return launch_status(op);
 }
@@ -249,10 +314,16 @@ int launch_norm_mod(const NormArgs& a, hipStream_t stream, const char* op) {
 template <int NT, bool ADD>
 int launch_norm_mod_dt(int dtype, const NormArgs& a, hipStream_t stream, const char* op) {
   switch (dtype) {
-    case JO_DTYPE_BF16: return launch_norm_mod<BF16, NT, ADD>(a, stream, op);
-    case JO_DTYPE_F16: return launch_norm_mod<F16, NT, ADD>(a, stream, op);
-    default: return launch_norm_mod<F32, NT, ADD>(a, stream, op);
+    case JO_DTYPE_BF16: return launch_norm_mod<BF16, NT, ADD, false>(a, stream, op);
+    case JO_DTYPE_F16: return launch_norm_mod<F16, NT, ADD, false>(a, stream, op);
+    default: return launch_norm_mod<F32, NT, ADD, false>(a, stream, op);
   }
+}
+
+template <int NT, bool ADD>
+int launch_norm_mod_quant_dt(int dtype, const NormArgs& a, hipStream_t stream, const char* op) {
+  if (dtype == JO_DTYPE_BF16) return launch_norm_mod<BF16, NT, ADD, true>(a, stream, op);
+  return launch_norm_mod<F16, NT, ADD, true>(a, stream, op);
 }
 
 // ---------------------------------------------------------------------------
@@ -402,4 +473,34 @@ extern "C" int jo_fused_add_layernorm_scale_shift(
              scale_stride, shift, shift_stride, y, y_stride, M, static_cast<int>(N), eps};
   return launch_norm_mod_dt<kLayer, true>(dtype, a, static_cast<hipStream_t>(stream),
                                           "fused_add_layernorm_scale_shift");
+}
+
+extern "C" int jo_norm_scale_shift_quant_fp8(
+    const void* x, int64_t x_stride, void* residual, int64_t res_stride, const void* gate,
+    int64_t gate_stride, const void* gamma, const void* beta, const void* scale,
+    int64_t scale_stride, const void* shift, int64_t shift_stride, void* out_q, int64_t q_stride,
+    float* out_s, int64_t M, int64_t N, int dtype, int norm_type, float eps, void* stream) {
+  const char* op = "norm_scale_shift_quant_fp8";
+  JO_REQUIRE(dtype == JO_DTYPE_BF16 || dtype == JO_DTYPE_F16,
+             "%s: input must be bf16 or fp16 (the quantized row is the 16-bit y)", op);
+  JO_REQUIRE(norm_type == JO_NORM_LAYER || norm_type == JO_NORM_RMS,
+             "norm_type must be 0 (layer) or 1 (rms)");
+  JO_REQUIRE(M >= 0 && N >= 0 && N <= INT32_MAX, "%s: bad shape", op);
+  JO_REQUIRE(N % 4 == 0, "N must be divisible by 4");
+  JO_REQUIRE(x_stride >= N && q_stride >= N && scale_stride >= 0 && shift_stride >= 0 &&
+                 gate_stride >= 0 && (residual == nullptr || res_stride >= N),
+             "%s: bad row stride", op);
+  JO_REQUIRE(residual != nullptr || gate == nullptr, "%s: a gate needs a residual", op);
+  if (M == 0 || N == 0) return JO_OK;
+  JO_REQUIRE(x && out_q && out_s && scale && shift, "%s: null pointer", op);
+  NormArgs a{x, x_stride, residual, res_stride, gate, gate_stride, gamma, beta, scale,
+             scale_stride, shift, shift_stride, nullptr, 0, M, static_cast<int>(N), eps,
+             static_cast<uint8_t*>(out_q), q_stride, out_s};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (residual) {
+    if (norm_type == JO_NORM_LAYER) return launch_norm_mod_quant_dt<kLayer, true>(dtype, a, st, op);
+    return launch_norm_mod_quant_dt<kRms, true>(dtype, a, st, op);
+  }
+  if (norm_type == JO_NORM_LAYER) return launch_norm_mod_quant_dt<kLayer, false>(dtype, a, st, op);
+  return launch_norm_mod_quant_dt<kRms, false>(dtype, a, st, op);
 }

@@ -11,14 +11,6 @@
 namespace jo {
 namespace {
 
-// Quantizes 8 fp32 values with the reference's rule and returns 8 bytes.
-// CLAMP = false only where the inputs are finite and inv is finite (see fp8x4).
-template <bool CLAMP = true>
-__device__ __forceinline__ u32x2 quant8(const float (&v)[8], float inv) {
-  return u32x2{fp8x4<CLAMP>(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv),
-               fp8x4<CLAMP>(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv)};
-}
-
 // ---------------------------------------------------------------------------
 // Per-token quantization: follows per_token_quant_fp8.cu:56-82.
 //   amax = max |x| (NaN ignored: fmaxf), scale = amax / 448 (IEEE division),
@@ -100,10 +92,7 @@ __global__ __launch_bounds__(kBlock) void quant_generic_kernel(const void* __res
   if (threadIdx.x == 0) s[row] = scale;
   const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;
   uint8_t* qr = q + row * qs;
-  for (int i = threadIdx.x; i < N; i += kBlock) {
-    const float v = fp8_clamp(load_elem<Tag>(x, xo + i) * inv);
-    qr[i] = static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.f, 0, false) & 0xff);
-  }
+  for (int i = threadIdx.x; i < N; i += kBlock) qr[i] = fp8_byte(load_elem<Tag>(x, xo + i) * inv);
 }
 
 template <class Tag>

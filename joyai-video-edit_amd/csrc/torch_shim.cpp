@@ -5,8 +5,9 @@
 // (fused_qknorm_rope_3d_kernel.cu:183-200, fused_norm_scale_shift.cu:176-196,
 // rmsnorm.cu:77-81, per_token_quant_fp8.cu:149-156), so
 // torch.ops.joyomni_ops.* behaves as the reference does for callers. The new
-// ops (grid RoPE, K ring-cache write, add+LayerNorm, RMSNorm->FP8) have their
-// own names. Tensors on ROCm carry the CUDA device type, so the impls are
+// ops (grid RoPE, K ring-cache write, add+LayerNorm, RMSNorm->FP8,
+// norm+AdaLN->FP8) have their own names. Tensors on ROCm carry the CUDA
+// device type, so the impls are
 // registered on the CUDA dispatch key like the reference's. Every op runs
 // on the current stream of the tensor's device and never synchronizes.
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
@@ -389,6 +390,71 @@ void rmsnorm_quant_fp8(const torch::Tensor& x, const torch::Tensor& weight, doub
                "rmsnorm_quant_fp8");
 }
 
+void norm_scale_shift_quant_fp8(const torch::Tensor& x,
+                                const c10::optional<torch::Tensor>& residual_opt,
+                                const c10::optional<torch::Tensor>& gate_opt,
+                                const c10::optional<torch::Tensor>& gamma_opt,
+                                const c10::optional<torch::Tensor>& beta_opt,
+                                const torch::Tensor& scale, const torch::Tensor& shift,
+                                int64_t norm_type, double eps, torch::Tensor output_q,
+                                torch::Tensor output_s) {
+  JO_CHECK_CUDA(x);
+  JO_CHECK_CUDA(output_q);
+  JO_CHECK_CUDA(output_s);
+  TORCH_CHECK(x.dim() == 2 && x.stride(-1) == 1, "x must be 2D [M, N] with contiguous rows");
+  TORCH_CHECK(x.scalar_type() == torch::kBFloat16 || x.scalar_type() == torch::kFloat16,
+              "x must be bf16 or fp16");
+  TORCH_CHECK(norm_type == 0 || norm_type == 1, "norm_type must be 0 (layer) or 1 (rms)");
+  const int64_t M = x.size(0), N = x.size(1);
+  TORCH_CHECK(N % 4 == 0, "N must be divisible by 4");
+  TORCH_CHECK(scale.dtype() == x.dtype() && shift.dtype() == x.dtype(),
+              "x/scale/shift dtype must match");
+  const int64_t sc_stride = mod_stride(scale, M, N, "scale");
+  const int64_t sh_stride = mod_stride(shift, M, N, "shift");
+  const bool has_res = residual_opt.has_value() && residual_opt->defined();
+  if (has_res) {
+    JO_CHECK_CUDA(*residual_opt);
+    TORCH_CHECK(residual_opt->sizes() == x.sizes() && residual_opt->stride(-1) == 1 &&
+                    residual_opt->dtype() == x.dtype(),
+                "residual must match x");
+  }
+  const bool has_gate = gate_opt.has_value() && gate_opt->defined();
+  TORCH_CHECK(!has_gate || has_res, "a gate needs a residual");
+  int64_t g_stride = 0;
+  if (has_gate) {
+    TORCH_CHECK(gate_opt->dtype() == x.dtype(), "gate dtype must match x");
+    g_stride = mod_stride(*gate_opt, M, N, "gate");
+  }
+  const bool has_gamma = gamma_opt.has_value() && gamma_opt->defined();
+  const bool has_beta = beta_opt.has_value() && beta_opt->defined();
+  if (has_gamma)
+    TORCH_CHECK(gamma_opt->numel() == N && gamma_opt->is_contiguous() &&
+                    gamma_opt->dtype() == x.dtype(),
+                "gamma must be [N] contiguous of x's dtype");
+  if (has_beta)
+    TORCH_CHECK(beta_opt->numel() == N && beta_opt->is_contiguous() &&
+                    beta_opt->dtype() == x.dtype(),
+                "beta must be [N] contiguous of x's dtype");
+  TORCH_CHECK(output_q.scalar_type() == at::kFloat8_e4m3fn && output_q.is_contiguous() &&
+                  output_q.numel() == M * N,
+              "output_q must be a contiguous float8_e4m3fn tensor with M*N elements");
+  TORCH_CHECK(output_s.scalar_type() == torch::kFloat32 && output_s.is_contiguous() &&
+                  output_s.numel() == M,
+              "output_s must be contiguous float32 with M elements");
+  if (M == 0) return;
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  check_status(jo_norm_scale_shift_quant_fp8(
+                   x.data_ptr(), row_stride(x), has_res ? residual_opt->data_ptr() : nullptr,
+                   has_res ? row_stride(*residual_opt) : 0,
+                   has_gate ? gate_opt->data_ptr() : nullptr, g_stride,
+                   has_gamma ? gamma_opt->data_ptr() : nullptr,
+                   has_beta ? beta_opt->data_ptr() : nullptr, scale.data_ptr(), sc_stride,
+                   shift.data_ptr(), sh_stride, output_q.data_ptr(), N,
+                   output_s.data_ptr<float>(), M, N, dtype_code(x),
+                   static_cast<int>(norm_type), static_cast<float>(eps), current_stream(x)),
+               "norm_scale_shift_quant_fp8");
+}
+
 }  // namespace joyomni_ops
 
 TORCH_LIBRARY(joyomni_ops, m) {
@@ -416,6 +482,10 @@ TORCH_LIBRARY(joyomni_ops, m) {
   m.def(
       "rmsnorm_quant_fp8(Tensor x, Tensor weight, float eps, Tensor! output_q, "
       "Tensor! output_s, int group_size) -> ()");
+  m.def(
+      "norm_scale_shift_quant_fp8(Tensor x, Tensor(a!)? residual, Tensor? gate, "
+      "Tensor? gamma_opt, Tensor? beta_opt, Tensor scale, Tensor shift, int norm_type, "
+      "float eps, Tensor! output_q, Tensor! output_s) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(joyomni_ops, CUDA, m) {
@@ -427,4 +497,5 @@ TORCH_LIBRARY_IMPL(joyomni_ops, CUDA, m) {
   m.impl("fused_qk_norm_rope_3d_kvcache", &joyomni_ops::fused_qk_norm_rope_3d_kvcache);
   m.impl("fused_add_layernorm_scale_shift", &joyomni_ops::fused_add_layernorm_scale_shift);
   m.impl("rmsnorm_quant_fp8", &joyomni_ops::rmsnorm_quant_fp8);
+  m.impl("norm_scale_shift_quant_fp8", &joyomni_ops::norm_scale_shift_quant_fp8);
 }

@@ -179,3 +179,16 @@ def fused_add_layernorm_scale_shift(x, residual, scale, shift, gate=None, gamma=
 def rmsnorm_quant_fp8(x, weight, eps, output_q, output_s, group_size=0):
     """FP8 e4m3 quantization of RMSNorm(x) * weight (fp32), per token or per 1x128 block."""
     _ops.rmsnorm_quant_fp8(x, weight, eps, output_q, output_s, group_size)
+
+
+def norm_scale_shift_quant_fp8(x, scale, shift, output_q, output_s, residual=None, gate=None,
+                               gamma=None, beta=None, norm_type="layer", eps=1e-6):
+    """Per-token FP8 e4m3 quantization of the bf16/fp16 y that
+    fused_norm_scale_shift (residual None) or fused_add_layernorm_scale_shift
+    (residual given, updated in place with residual + x (* gate)) would return;
+    y itself is never written. output_q: float8_e4m3fn [M, N]; output_s:
+    float32 [M] or [M, 1]. norm_type "layer" or "rms".
+    """
+    nt = 0 if norm_type == "layer" else 1 if norm_type == "rms" else -1
+    _ops.norm_scale_shift_quant_fp8(x, residual, gate, gamma, beta, scale, shift, nt, eps,
+                                    output_q, output_s)

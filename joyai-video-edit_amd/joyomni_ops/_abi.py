@@ -48,6 +48,9 @@ SIGNATURES: dict[str, list] = {
         _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, c_int,
         _F, _P],
     "jo_rmsnorm_quant_fp8": [_P, _I64, _P, _P, _I64, _P, _I64, _I64, c_int, _F, _I64, _P],
+    "jo_norm_scale_shift_quant_fp8": [
+        _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64,
+        c_int, c_int, _F, _P],
 }
 
 _lib = None

@@ -19,6 +19,9 @@ Additional entry points for callers that can use the new fused ops:
   fused_add_gate_layernorm_modulate residual + x * gate and the following
                             fused_layernorm_modulate in one pass (dit.py:447-457).
   quantize_activation_fp8   x_q, x_scale of Fp8Linear.forward (fp8_linear.py:140-166).
+  layernorm_modulate_fp8    fused_layernorm_modulate followed by that quantization,
+                            in one pass (the bf16 output is never written).
+  fused_add_gate_layernorm_modulate_fp8  the same after residual + x * gate.
 """
 from __future__ import annotations
 
@@ -27,8 +30,8 @@ from typing import Optional, Sequence, Tuple
 import torch
 
 from . import (fused_add_layernorm_scale_shift, fused_norm_scale_shift,
-               fused_qk_norm_rope_3d_grid, fused_qk_norm_rope_3d_paired, rmsnorm, rope_freqs,
-               sgl_per_token_quant_fp8)
+               fused_qk_norm_rope_3d_grid, fused_qk_norm_rope_3d_paired,
+               norm_scale_shift_quant_fp8, rmsnorm, rope_freqs, sgl_per_token_quant_fp8)
 
 
 def available() -> bool:
@@ -197,3 +200,64 @@ def quantize_activation_fp8(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor
     x_scale = torch.empty((M, 1), device=x_2d.device, dtype=torch.float32)
     sgl_per_token_quant_fp8(x_2d, x_q, x_scale)
     return x_q, x_scale
+
+
+def _mod_of(t: torch.Tensor, B: int, L: int, D: int, b: int) -> torch.Tensor:
+    """Sample b's modulation: [D] from [B, D] / [B, 1, D], or [L, D] from [B, L, D]."""
+    if t.numel() == B * D:
+        return t.reshape(B, D)[b]
+    return t.reshape(B, L, D)[b]
+
+
+def _fp8_outputs(M: int, D: int, device) -> Tuple[torch.Tensor, torch.Tensor]:
+    """x_q fp8 e4m3fn [M, D] and x_scale fp32 [M, 1], as Fp8Linear.forward allocates them."""
+    return (torch.empty((M, D), device=device, dtype=torch.float8_e4m3fn),
+            torch.empty((M, 1), device=device, dtype=torch.float32))
+
+
+def layernorm_modulate_fp8(
+    x: torch.Tensor,
+    shift: torch.Tensor,
+    scale: torch.Tensor,
+    *,
+    weight: Optional[torch.Tensor] = None,
+    bias: Optional[torch.Tensor] = None,
+    eps: float = 1e-6,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """quantize_activation_fp8(fused_layernorm_modulate(x, shift, scale)) in one
+    pass: x [B, L, D], shift/scale [B, D], [B, 1, D] or [B, L, D] ->
+    (x_q [B*L, D], x_scale [B*L, 1]), byte-identical to the two calls."""
+    B, L, D = x.shape
+    x_q, x_scale = _fp8_outputs(B * L, D, x.device)
+    for b in range(B):
+        rows = slice(b * L, (b + 1) * L)
+        norm_scale_shift_quant_fp8(x[b], _mod_of(scale, B, L, D, b), _mod_of(shift, B, L, D, b),
+                                   x_q[rows], x_scale[rows], gamma=weight, beta=bias, eps=eps)
+    return x_q, x_scale
+
+
+def fused_add_gate_layernorm_modulate_fp8(
+    residual: torch.Tensor,
+    x: torch.Tensor,
+    gate: torch.Tensor,
+    shift: torch.Tensor,
+    scale: torch.Tensor,
+    *,
+    weight: Optional[torch.Tensor] = None,
+    bias: Optional[torch.Tensor] = None,
+    eps: float = 1e-6,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """fused_add_gate_layernorm_modulate followed by quantize_activation_fp8 of
+    its modulated output, in one pass: returns (residual', x_q [B*L, D],
+    x_scale [B*L, 1]); residual [B, L, D] is updated in place."""
+    B, L, D = x.shape
+    if not residual.is_contiguous():
+        raise RuntimeError("residual must be contiguous (it is updated in place)")
+    x_q, x_scale = _fp8_outputs(B * L, D, x.device)
+    for b in range(B):
+        rows = slice(b * L, (b + 1) * L)
+        norm_scale_shift_quant_fp8(x[b], _mod_of(scale, B, L, D, b), _mod_of(shift, B, L, D, b),
+                                   x_q[rows], x_scale[rows], residual=residual[b],
+                                   gate=_mod_of(gate, B, L, D, b), gamma=weight, beta=bias,
+                                   eps=eps)
+    return residual, x_q, x_scale

@@ -8,6 +8,11 @@ Configs (720p 3-latent-frame chunk shapes, hidden 3072, 24 heads x 128):
   C3   QK RMSNorm + RoPE with K into a 7-slot ring cache: q,k [1, 10530, 24, 128]
   C4*  RMSNorm -> FP8, T in {4725, 10530}, per-token or per-1x128-block scales
 
+Next-row workloads (not BASELINE configs; same shapes):
+  N3   gated residual add + LayerNorm + AdaLN with the per-token FP8 epilogue
+       (the y of C2 quantized for the next Fp8Linear instead of written):
+       x, residual bf16 [10530, 3072], gate/scale/shift bf16 [3072]
+
 Inputs are generated on the CPU with torch.Generator().manual_seed(s)
 (s = config index) in fp32, cast to bf16, and copied to the device, so the
 CPU oracle and the GPU see identical tensors. Outliers: exactly
@@ -42,6 +47,7 @@ CONFIGS: dict[str, Config] = {
     "C4_4725_blk": Config("C4_4725_blk", "rms_quant", 4, dict(M=4725, N=3072, group=128, eps=1e-6)),
     "C4_10530_tok": Config("C4_10530_tok", "rms_quant", 4, dict(M=10530, N=3072, group=0, eps=1e-6)),
     "C4_10530_blk": Config("C4_10530_blk", "rms_quant", 4, dict(M=10530, N=3072, group=128, eps=1e-6)),
+    "N3": Config("N3", "add_ln_quant", 5, dict(M=10530, N=3072, eps=1e-6)),
 }
 
 
@@ -70,11 +76,13 @@ def make_inputs(cfg: Config, device="cpu") -> dict:
                                          dtype=torch.bfloat16)
     elif cfg.op == "quant":
         out["x"] = with_outliers(torch.randn(d["M"], d["K"], generator=g), g).to(torch.bfloat16)
-    elif cfg.op == "add_ln":
+    elif cfg.op in ("add_ln", "add_ln_quant"):
         out["x"] = torch.randn(d["M"], d["N"], generator=g).to(torch.bfloat16)
         out["residual"] = torch.randn(d["M"], d["N"], generator=g).to(torch.bfloat16)
         out["shift"] = (0.2 * torch.randn(d["N"], generator=g)).to(torch.bfloat16)
         out["scale"] = (0.2 * torch.randn(d["N"], generator=g)).to(torch.bfloat16)
+        if cfg.op == "add_ln_quant":
+            out["gate"] = torch.randn(d["N"], generator=g).to(torch.bfloat16)
     elif cfg.op == "rms_quant":
         out["x"] = with_outliers(torch.randn(d["M"], d["N"], generator=g), g).to(torch.bfloat16)
         out["weight"] = (1 + 0.1 * torch.randn(d["N"], generator=g)).to(torch.bfloat16)
@@ -99,6 +107,9 @@ def algorithmic_bytes(cfg: Config) -> int:
     if cfg.op == "rms_quant":
         ns = d["M"] if d["group"] == 0 else d["M"] * (d["N"] // d["group"])
         return d["M"] * d["N"] * 3 + ns * 4 + d["N"] * 2   # bf16 in, fp8 out, scales, gamma
+    if cfg.op == "add_ln_quant":
+        # x, res in; res out (bf16); fp8 out; scales; gate/scale/shift rows
+        return 7 * d["M"] * d["N"] + 4 * d["M"] + 3 * d["N"] * 2
     raise ValueError(cfg.op)
 
 
@@ -114,6 +125,9 @@ def alloc_outputs(cfg: Config, inputs: dict) -> dict:
                 "s": torch.empty(ns, dtype=torch.float32, device=dev)}
     if cfg.op == "add_ln":
         return {"y": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev)}
+    if cfg.op == "add_ln_quant":
+        return {"q": torch.empty(d["M"], d["N"], dtype=torch.float8_e4m3fn, device=dev),
+                "s": torch.empty(d["M"], dtype=torch.float32, device=dev)}
     return {}
 
 
@@ -136,6 +150,11 @@ def launch(cfg: Config, t: dict, stream_handle: int, freqs: torch.Tensor | None 
         _abi.call("jo_fused_add_layernorm_scale_shift", p(t["x"]), d["N"], p(t["residual"]),
                   d["N"], None, 0, None, None, p(t["scale"]), 0, p(t["shift"]), 0, p(t["y"]),
                   d["N"], d["M"], d["N"], _abi.JO_DTYPE_BF16, d["eps"], stream_handle)
+    elif cfg.op == "add_ln_quant":
+        _abi.call("jo_norm_scale_shift_quant_fp8", p(t["x"]), d["N"], p(t["residual"]), d["N"],
+                  p(t["gate"]), 0, None, None, p(t["scale"]), 0, p(t["shift"]), 0, p(t["q"]),
+                  d["N"], p(t["s"]), d["M"], d["N"], _abi.JO_DTYPE_BF16, _abi.JO_NORM_LAYER,
+                  d["eps"], stream_handle)
     elif cfg.op in ("qk_grid", "qk_kvcache"):
         B, L, H, D = d["B"], d["L"], d["H"], d["D"]
         gh, gw = d["grid"]

@@ -29,4 +29,6 @@ its tests only print fp32-formula diffs):
   add_layernorm_*       composition of torch.addcmul and F.layer_norm.
   rmsnorm_quant_fp8     composition of the rmsnorm restatement and the C
                         per-token / per-block quantizer.
+  norm_scale_shift_quant_fp8  composition of residual_add / norm_scale_shift
+                        and per_token_quant_fp8 (each pinned above).
 """

@@ -127,13 +127,38 @@ def norm_scale_shift(x, gamma, beta, scale, shift, norm_type: int, eps: float):
 # deploy/xvideo/models/dit/sgl_fused_ops.py:114-117 (torch.addcmul, one
 # rounding) and the LayerNorm path above, on the rounded residual.
 # ---------------------------------------------------------------------------
-def add_layernorm_scale_shift(x, residual, gate, gamma, beta, scale, shift, eps: float):
+def residual_add(x, residual, gate):
+    """round(residual + x * gate) (gate None: residual + x), fp32 then one rounding."""
     xf = x.float()
     rf = residual.float()
     upd = rf + (xf * gate.float() if gate is not None else xf)
-    new_res = upd.to(residual.dtype)
+    return upd.to(residual.dtype)
+
+
+def add_layernorm_scale_shift(x, residual, gate, gamma, beta, scale, shift, eps: float):
+    new_res = residual_add(x, residual, gate)
     y = norm_scale_shift_f32(new_res, gamma, beta, scale, shift, 0, eps)
     return new_res, y
+
+
+# ---------------------------------------------------------------------------
+# (Gated residual add +) norm + AdaLN with the per-token FP8 epilogue: the
+# calls the DiT makes back to back — the residual update and modulated norm
+# above (dit.py:447-476), the 16-bit y as that op returns it, then
+# per_token_quant_fp8 (per_token_quant_fp8.cu:56-82) as Fp8Linear.forward
+# runs it on y (fp8_linear.py:138-169).
+# ---------------------------------------------------------------------------
+def norm_scale_shift_quant_fp8(x, residual, gate, gamma, beta, scale, shift, norm_type: int,
+                               eps: float, y=None):
+    """Returns (new residual or None, q uint8 [M, N], s fp32 [M], y [M, N] 16-bit).
+    y, when given, is the 16-bit output to quantize (e.g. a device op's own y,
+    whose summation order the fp32 restatement does not follow)."""
+    new_res = residual_add(x, residual, gate) if residual is not None else None
+    src = new_res if residual is not None else x
+    if y is None:
+        y = norm_scale_shift_f32(src, gamma, beta, scale, shift, norm_type, eps).to(x.dtype)
+    q, s = per_token_quant_fp8(y)
+    return new_res, q, s, y
 
 
 # ---------------------------------------------------------------------------

@@ -269,3 +269,26 @@ def test_source_id_composition_is_angle_addition():
 def test_ring_slots():
     assert ops.ring_slots(3, 7, 0) == [0, 1, 2]
     assert ops.ring_slots(3, 7, 6) == [6, 0, 1]
+
+
+def test_norm_quant_oracle_quantizes_the_rounded_y():
+    """The FP8 epilogue quantizes the 16-bit y the unfused op returns: its
+    scale is amax|bf16 y| / 448 (checked against torch's max and the C
+    encoder's bytes), and a planted slip (quantizing the fp32 y instead)
+    changes scales on random rows."""
+    g = torch.Generator().manual_seed(3)
+    M, N = 16, 256
+    x = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    gate = torch.randn(N, generator=g).to(torch.bfloat16)
+    sc = (0.2 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    sh = (0.2 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    new_res, q, s, y = ops.norm_scale_shift_quant_fp8(x, res, gate, None, None, sc, sh, 0, 1e-6)
+    assert torch.equal(new_res, torch.addcmul(res.float(), x.float(), gate.float()).to(torch.bfloat16))
+    assert y.dtype == torch.bfloat16
+    assert torch.equal(s, (y.float().abs().amax(-1) / 448.0))
+    qc, sc_c = fp8ref.per_token_quant(y.float().numpy())
+    assert np.array_equal(q.numpy(), qc) and np.array_equal(s.numpy(), sc_c)
+    y32 = ops.norm_scale_shift_f32(new_res, None, None, sc, sh, 0, 1e-6)
+    _, s_slip = ops.per_token_quant_fp8(y32)
+    assert not torch.equal(s_slip, s)
