@@ -5,8 +5,9 @@
 A "step" is one call of an op over one batch of synthetic input. The headline
 workload (`value`) is BASELINE config 1: per-token FP8 e4m3 quantization of a
 bf16 [10530, 3072] activation. Every other BASELINE config is timed the same
-way and reported under "ops", as is N3 (the gated residual + LayerNorm +
-AdaLN with the per-token FP8 epilogue, a next-row workload at the C2 shape).
+way and reported under "ops", as are the next-row workloads N3 (the gated
+residual + LayerNorm + AdaLN with the per-token FP8 epilogue, C2 shape) and
+N4 (the graph runner's 40-layer KV-pool commit at the deployment shape).
 
 Timing: W eager warmup calls, then K calls captured into one HIP graph and
 replayed once untimed and once timed between HIP events recorded on the
@@ -147,6 +148,9 @@ def cpu_fn(cfg):
     if cfg.op == "add_ln":
         return lambda t: ops.add_layernorm_scale_shift(t["x"], t["residual"], None, None, None,
                                                        t["scale"], t["shift"], d["eps"])
+    if cfg.op == "kv_commit":
+        return lambda t: ops.commit_kv(t["pool_k"], t["pool_v"], t["stage_k"], t["stage_v"],
+                                       d["off"], t["cos"], t["sin"])
     if cfg.op == "add_ln_quant":
         return lambda t: ops.norm_scale_shift_quant_fp8(t["x"], t["residual"], t["gate"], None,
                                                         None, t["scale"], t["shift"], 0, d["eps"])

@@ -236,6 +236,36 @@ int jo_norm_scale_shift_quant_fp8(const void* x, int64_t x_stride, void* residua
                                   void* out_q, int64_t q_stride, float* out_s, int64_t M,
                                   int64_t N, int dtype, int norm_type, float eps, void* stream);
 
+/* ------------------------------------------------------------------------
+ * RoPE'd K and copied V into a KV pool, every layer in one launch:
+ *   dst_k[l, b, off + n, :] = apply_rotary_emb(src_k[l, b, n, :], cos[b, n], sin[b, n])
+ *   dst_v[l, b, off + n, :] = src_v[l, b, n, :]           (when src_v != NULL)
+ * with torch's evaluation of apply_rotary_emb (rope.py:21-28): per pair
+ * (x0, x1) at columns (2i, 2i+1), out0 = fl(fl(x0*cos[2i]) - fl(x1*sin[2i])),
+ * out1 = fl(fl(x1*cos[2i+1]) + fl(x0*sin[2i+1])) in fp32, then one rounding
+ * to dtype — bit-identical to the reference for the same fp32 tables.
+ * Replaces the per-layer loop of StreamingGraphRunner.run_commit
+ * (deploy/xvideo/serving/graph_runner.py:137-142: 40 apply_rotary_emb + 80
+ * copy kernels), its _seed_segment (:204-215) and, with layers = 1 and a
+ * fresh destination, apply_rotary_emb itself (rope.py:21-28, used by
+ * dit.py:211-217 and dit.py:384-385).
+ * src: [layers, batch, tokens, num_heads * head_dim], dst: [layers, batch,
+ * dst_tokens, num_heads * head_dim], with element strides (token rows
+ * contiguous); dst_token_offset + tokens <= dst_tokens;
+ * cos, sin: fp32 [batch?, tokens, head_dim] with token stride table_stride
+ * and batch stride table_batch_stride (0 = one table for all batch rows).
+ * dtype bf16 or fp16; head_dim even.
+ * ------------------------------------------------------------------------ */
+int jo_kv_commit_rope(const void* src_k, const void* src_v, void* dst_k, void* dst_v,
+                      int64_t layers, int64_t batch, int64_t tokens, int64_t num_heads,
+                      int64_t head_dim, int64_t src_layer_stride, int64_t src_batch_stride,
+                      int64_t src_token_stride, int64_t dst_layer_stride,
+                      int64_t dst_batch_stride, int64_t dst_token_stride,
+                      int64_t dst_tokens, int64_t dst_token_offset, const float* cos,
+                      const float* sin,
+                      int64_t table_stride, int64_t table_batch_stride, int dtype,
+                      void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

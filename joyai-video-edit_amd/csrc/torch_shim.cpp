@@ -6,7 +6,7 @@
 // rmsnorm.cu:77-81, per_token_quant_fp8.cu:149-156), so
 // torch.ops.joyomni_ops.* behaves as the reference does for callers. The new
 // ops (grid RoPE, K ring-cache write, add+LayerNorm, RMSNorm->FP8,
-// norm+AdaLN->FP8) have their own names. Tensors on ROCm carry the CUDA
+// norm+AdaLN->FP8, KV-pool commit, apply_rotary_emb) have their own names. Tensors on ROCm carry the CUDA
 // device type, so the impls are
 // registered on the CUDA dispatch key like the reference's. Every op runs
 // on the current stream of the tensor's device and never synchronizes.
@@ -455,6 +455,87 @@ void norm_scale_shift_quant_fp8(const torch::Tensor& x,
                "norm_scale_shift_quant_fp8");
 }
 
+namespace {
+// Strides of a [B, T, H, D] (L = 1) or [L, B, T, H, D] K/V tensor whose
+// heads are contiguous per token: {layer, batch, token} in elements.
+struct KVLayout {
+  int64_t L, B, T, H, D, ls, bs, ts;
+};
+KVLayout kv_layout(const torch::Tensor& t, const char* name) {
+  JO_CHECK_CUDA(t);
+  TORCH_CHECK(t.dim() == 4 || t.dim() == 5, name, " must be [B, T, H, D] or [L, B, T, H, D]");
+  TORCH_CHECK(t.scalar_type() == torch::kBFloat16 || t.scalar_type() == torch::kFloat16, name,
+              " must be bf16 or fp16");
+  const int64_t o = t.dim() - 4;
+  KVLayout k{o ? t.size(0) : 1, t.size(o), t.size(o + 1), t.size(o + 2), t.size(o + 3),
+             o ? t.stride(0) : 0, t.stride(o), t.stride(o + 1)};
+  TORCH_CHECK(t.stride(-1) == 1 && (k.H <= 1 || t.stride(-2) == k.D), name,
+              " must have contiguous heads per token");
+  return k;
+}
+// Table batch stride for fp32 [T, D] / [1, T, D] (shared) or [B, T, D] tables.
+int64_t table_batch_stride(const torch::Tensor& c, int64_t B, int64_t T, int64_t D,
+                           const char* name) {
+  JO_CHECK_CUDA(c);
+  TORCH_CHECK(c.scalar_type() == torch::kFloat32 && c.is_contiguous(), name,
+              " must be a contiguous float32 table");
+  if (c.numel() == T * D) return 0;
+  TORCH_CHECK(c.numel() == B * T * D, name, " must hold [T, D] or [B, T, D] values");
+  return T * D;
+}
+}  // namespace
+
+void kv_commit_rope(const torch::Tensor& src_k, const c10::optional<torch::Tensor>& src_v_opt,
+                    torch::Tensor dst_k, const c10::optional<torch::Tensor>& dst_v_opt,
+                    int64_t dst_offset, const torch::Tensor& cos, const torch::Tensor& sin) {
+  const KVLayout s = kv_layout(src_k, "src_k");
+  const KVLayout d = kv_layout(dst_k, "dst_k");
+  TORCH_CHECK(src_k.dim() == dst_k.dim() && s.L == d.L && s.B == d.B && s.H == d.H && s.D == d.D,
+              "src_k and dst_k must agree in layers, batch and heads");
+  TORCH_CHECK(dst_k.scalar_type() == src_k.scalar_type(), "dst_k dtype must match src_k");
+  TORCH_CHECK(dst_offset >= 0 && dst_offset + s.T <= d.T,
+              "dst_offset + tokens must fit in dst_k's token dim");
+  const bool has_v = src_v_opt.has_value() && src_v_opt->defined();
+  TORCH_CHECK(has_v == (dst_v_opt.has_value() && dst_v_opt->defined()),
+              "src_v and dst_v go together");
+  if (has_v) {
+    const KVLayout sv = kv_layout(*src_v_opt, "src_v");
+    const KVLayout dv = kv_layout(*dst_v_opt, "dst_v");
+    TORCH_CHECK(src_v_opt->sizes() == src_k.sizes() && dst_v_opt->sizes() == dst_k.sizes() &&
+                    sv.ls == s.ls && sv.bs == s.bs && sv.ts == s.ts && dv.ls == d.ls &&
+                    dv.bs == d.bs && dv.ts == d.ts &&
+                    src_v_opt->scalar_type() == src_k.scalar_type() &&
+                    dst_v_opt->scalar_type() == src_k.scalar_type(),
+                "V tensors must have the shapes, strides and dtype of the K tensors");
+  }
+  const int64_t tbs = table_batch_stride(cos, s.B, s.T, s.D, "cos");
+  TORCH_CHECK(table_batch_stride(sin, s.B, s.T, s.D, "sin") == tbs, "cos and sin must match");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(src_k.device());
+  check_status(jo_kv_commit_rope(src_k.data_ptr(), has_v ? src_v_opt->data_ptr() : nullptr,
+                                 dst_k.data_ptr(), has_v ? dst_v_opt->data_ptr() : nullptr, s.L,
+                                 s.B, s.T, s.H, s.D, s.ls, s.bs, s.ts, d.ls, d.bs, d.ts, d.T,
+                                 dst_offset, cos.data_ptr<float>(), sin.data_ptr<float>(), s.D,
+                                 tbs, dtype_code(src_k), current_stream(src_k)),
+               "kv_commit_rope");
+}
+
+torch::Tensor apply_rotary_emb(const torch::Tensor& x, const torch::Tensor& cos,
+                               const torch::Tensor& sin) {
+  TORCH_CHECK(x.dim() == 4, "x must be [B, T, H, D]");
+  const KVLayout s = kv_layout(x, "x");
+  auto out = torch::empty({s.B, s.T, s.H, s.D}, x.options());
+  const int64_t tbs = table_batch_stride(cos, s.B, s.T, s.D, "cos");
+  TORCH_CHECK(table_batch_stride(sin, s.B, s.T, s.D, "sin") == tbs, "cos and sin must match");
+  if (out.numel() == 0) return out;
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  check_status(jo_kv_commit_rope(x.data_ptr(), nullptr, out.data_ptr(), nullptr, 1, s.B, s.T,
+                                 s.H, s.D, 0, s.bs, s.ts, 0, s.T * s.H * s.D, s.H * s.D, s.T, 0,
+                                 cos.data_ptr<float>(), sin.data_ptr<float>(), s.D, tbs,
+                                 dtype_code(x), current_stream(x)),
+               "apply_rotary_emb");
+  return out;
+}
+
 }  // namespace joyomni_ops
 
 TORCH_LIBRARY(joyomni_ops, m) {
@@ -486,6 +567,10 @@ TORCH_LIBRARY(joyomni_ops, m) {
       "norm_scale_shift_quant_fp8(Tensor x, Tensor(a!)? residual, Tensor? gate, "
       "Tensor? gamma_opt, Tensor? beta_opt, Tensor scale, Tensor shift, int norm_type, "
       "float eps, Tensor! output_q, Tensor! output_s) -> ()");
+  m.def(
+      "kv_commit_rope(Tensor src_k, Tensor? src_v, Tensor(a!) dst_k, Tensor(b!)? dst_v, "
+      "int dst_offset, Tensor cos, Tensor sin) -> ()");
+  m.def("apply_rotary_emb(Tensor x, Tensor cos, Tensor sin) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(joyomni_ops, CUDA, m) {
@@ -498,4 +583,6 @@ TORCH_LIBRARY_IMPL(joyomni_ops, CUDA, m) {
   m.impl("fused_add_layernorm_scale_shift", &joyomni_ops::fused_add_layernorm_scale_shift);
   m.impl("rmsnorm_quant_fp8", &joyomni_ops::rmsnorm_quant_fp8);
   m.impl("norm_scale_shift_quant_fp8", &joyomni_ops::norm_scale_shift_quant_fp8);
+  m.impl("kv_commit_rope", &joyomni_ops::kv_commit_rope);
+  m.impl("apply_rotary_emb", &joyomni_ops::apply_rotary_emb);
 }

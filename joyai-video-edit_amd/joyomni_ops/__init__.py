@@ -192,3 +192,23 @@ def norm_scale_shift_quant_fp8(x, scale, shift, output_q, output_s, residual=Non
     nt = 0 if norm_type == "layer" else 1 if norm_type == "rms" else -1
     _ops.norm_scale_shift_quant_fp8(x, residual, gate, gamma, beta, scale, shift, nt, eps,
                                     output_q, output_s)
+
+
+def kv_commit_rope(src_k, dst_k, dst_offset, cos, sin, src_v=None, dst_v=None):
+    """dst_k[..., dst_offset + n, :, :] = apply_rotary_emb(src_k[..., n, :, :]) and
+    dst_v[..., dst_offset + n, :, :] = src_v[..., n, :, :] for every layer and
+    batch row in one launch. src/dst: [B, T, H, D] or [L, B, T, H, D] (dst's T
+    may be longer); cos, sin: fp32 [T, D], [1, T, D] or [B, T, D]."""
+    _ops.kv_commit_rope(src_k, src_v, dst_k, dst_v, dst_offset, _table(cos), _table(sin))
+
+
+def _table(t):
+    return t.float().contiguous()
+
+
+def apply_rotary_emb(x, freqs_cis):
+    """The reference's apply_rotary_emb (rope.py:21-28) for x [B, T, H, D] and
+    freqs_cis = (cos, sin) of [T, D] (or [1, T, D] / [B, T, D]) values, bit for
+    bit: (x.float() * cos + rotate_half(x.float()) * sin).type_as(x)."""
+    cos, sin = freqs_cis
+    return _ops.apply_rotary_emb(x, _table(cos), _table(sin))

@@ -22,6 +22,8 @@ Additional entry points for callers that can use the new fused ops:
   layernorm_modulate_fp8    fused_layernorm_modulate followed by that quantization,
                             in one pass (the bf16 output is never written).
   fused_add_gate_layernorm_modulate_fp8  the same after residual + x * gate.
+  commit_kv_pool            StreamingGraphRunner.run_commit (graph_runner.py:137-142)
+                            for all layers in one launch.
 """
 from __future__ import annotations
 
@@ -31,7 +33,8 @@ import torch
 
 from . import (fused_add_layernorm_scale_shift, fused_norm_scale_shift,
                fused_qk_norm_rope_3d_grid, fused_qk_norm_rope_3d_paired,
-               norm_scale_shift_quant_fp8, rmsnorm, rope_freqs, sgl_per_token_quant_fp8)
+               kv_commit_rope, norm_scale_shift_quant_fp8, rmsnorm, rope_freqs,
+               sgl_per_token_quant_fp8)
 
 
 def available() -> bool:
@@ -261,3 +264,14 @@ def fused_add_gate_layernorm_modulate_fp8(
                                    gate=_mod_of(gate, B, L, D, b), gamma=weight, beta=bias,
                                    eps=eps)
     return residual, x_q, x_scale
+
+
+def commit_kv_pool(pool_k: torch.Tensor, pool_v: torch.Tensor, stage_k: torch.Tensor,
+                   stage_v: torch.Tensor, offset: int, commit_cos: torch.Tensor,
+                   commit_sin: torch.Tensor) -> None:
+    """The graph runner's commit (graph_runner.py:137-142): for every layer li,
+    pool_k[li, :, offset:offset+T] = apply_rotary_emb(stage_k[li], (cos, sin)) and
+    pool_v[li, :, offset:offset+T] = stage_v[li], as one launch instead of one
+    RoPE and two copies per layer. pool_*: [L, B, P, H, D]; stage_*: [L, B, T, H, D];
+    commit_cos/sin: fp32 [1, T, D]. Bit-identical to the loop."""
+    kv_commit_rope(stage_k, pool_k, offset, commit_cos, commit_sin, src_v=stage_v, dst_v=pool_v)

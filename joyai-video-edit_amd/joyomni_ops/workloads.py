@@ -12,6 +12,9 @@ Next-row workloads (not BASELINE configs; same shapes):
   N3   gated residual add + LayerNorm + AdaLN with the per-token FP8 epilogue
        (the y of C2 quantized for the next Fp8Linear instead of written):
        x, residual bf16 [10530, 3072], gate/scale/shift bf16 [3072]
+  N4   KV-pool commit of the graph runner at the deployment shape: RoPE'd K and
+       V of 40 layers x 1560 tokens x 32 heads x 128 into a [40, 1, 3120, 32, 128]
+       pool at token offset 1560, fp32 [1560, 128] tables
 
 Inputs are generated on the CPU with torch.Generator().manual_seed(s)
 (s = config index) in fp32, cast to bf16, and copied to the device, so the
@@ -48,6 +51,7 @@ CONFIGS: dict[str, Config] = {
     "C4_10530_tok": Config("C4_10530_tok", "rms_quant", 4, dict(M=10530, N=3072, group=0, eps=1e-6)),
     "C4_10530_blk": Config("C4_10530_blk", "rms_quant", 4, dict(M=10530, N=3072, group=128, eps=1e-6)),
     "N3": Config("N3", "add_ln_quant", 5, dict(M=10530, N=3072, eps=1e-6)),
+    "N4": Config("N4", "kv_commit", 6, dict(L=40, T=1560, P=3120, off=1560, H=32, D=128)),
 }
 
 
@@ -83,6 +87,15 @@ def make_inputs(cfg: Config, device="cpu") -> dict:
         out["scale"] = (0.2 * torch.randn(d["N"], generator=g)).to(torch.bfloat16)
         if cfg.op == "add_ln_quant":
             out["gate"] = torch.randn(d["N"], generator=g).to(torch.bfloat16)
+    elif cfg.op == "kv_commit":
+        shape = (d["L"], 1, d["T"], d["H"], d["D"])
+        out["stage_k"] = torch.randn(shape, generator=g).to(torch.bfloat16)
+        out["stage_v"] = torch.randn(shape, generator=g).to(torch.bfloat16)
+        out["pool_k"] = torch.zeros((d["L"], 1, d["P"], d["H"], d["D"]), dtype=torch.bfloat16)
+        out["pool_v"] = torch.zeros((d["L"], 1, d["P"], d["H"], d["D"]), dtype=torch.bfloat16)
+        ang = torch.rand(d["T"], d["D"] // 2, generator=g) * 100
+        out["cos"] = ang.cos().repeat_interleave(2, 1).contiguous()
+        out["sin"] = ang.sin().repeat_interleave(2, 1).contiguous()
     elif cfg.op == "rms_quant":
         out["x"] = with_outliers(torch.randn(d["M"], d["N"], generator=g), g).to(torch.bfloat16)
         out["weight"] = (1 + 0.1 * torch.randn(d["N"], generator=g)).to(torch.bfloat16)
@@ -110,6 +123,9 @@ def algorithmic_bytes(cfg: Config) -> int:
     if cfg.op == "add_ln_quant":
         # x, res in; res out (bf16); fp8 out; scales; gate/scale/shift rows
         return 7 * d["M"] * d["N"] + 4 * d["M"] + 3 * d["N"] * 2
+    if cfg.op == "kv_commit":
+        # stage K, V read; pool K, V segment written; cos/sin tables
+        return 4 * d["L"] * d["T"] * d["H"] * d["D"] * 2 + 2 * d["T"] * d["D"] * 4
     raise ValueError(cfg.op)
 
 
@@ -155,6 +171,12 @@ def launch(cfg: Config, t: dict, stream_handle: int, freqs: torch.Tensor | None 
                   p(t["gate"]), 0, None, None, p(t["scale"]), 0, p(t["shift"]), 0, p(t["q"]),
                   d["N"], p(t["s"]), d["M"], d["N"], _abi.JO_DTYPE_BF16, _abi.JO_NORM_LAYER,
                   d["eps"], stream_handle)
+    elif cfg.op == "kv_commit":
+        L, T, P, H, D = d["L"], d["T"], d["P"], d["H"], d["D"]
+        hd = H * D
+        _abi.call("jo_kv_commit_rope", p(t["stage_k"]), p(t["stage_v"]), p(t["pool_k"]),
+                  p(t["pool_v"]), L, 1, T, H, D, T * hd, T * hd, hd, P * hd, P * hd, hd, P, d["off"],
+                  p(t["cos"]), p(t["sin"]), D, 0, _abi.JO_DTYPE_BF16, stream_handle)
     elif cfg.op in ("qk_grid", "qk_kvcache"):
         B, L, H, D = d["B"], d["L"], d["H"], d["D"]
         gh, gw = d["grid"]

@@ -31,4 +31,8 @@ its tests only print fp32-formula diffs):
                         per-token / per-block quantizer.
   norm_scale_shift_quant_fp8  composition of residual_add / norm_scale_shift
                         and per_token_quant_fp8 (each pinned above).
+  apply_rotary_emb      identity and quarter-turn tables (exact), complex
+                        multiplication in float64, a planted sign slip.
+  commit_kv             apply_rotary_emb per layer + copies (pool regions
+                        outside the segment unchanged).
 """

@@ -275,3 +275,38 @@ def rmsnorm_quant_fp8(x, w, eps: float, group_size: int = 0, v: torch.Tensor | N
     g = v.reshape(M, N // group_size, group_size)
     scale, inv = scale_and_inv(nan_ignoring_amax(g))
     return fp8_quant_with_inv(g, inv[..., None]).reshape(M, N), scale, v
+
+
+# ---------------------------------------------------------------------------
+# apply_rotary_emb — deploy/xvideo/models/dit/rope.py:14-28: rotate_half of the
+# fp32 input, then x*cos + rotate_half(x)*sin as three separately rounded fp32
+# tensor operations, then type_as(x). The tables broadcast over heads
+# (reshape_for_broadcast, rope.py:5-11). The graph runner's commit loop
+# (deploy/xvideo/serving/graph_runner.py:137-142) applies it per layer and
+# copies the result and V into the pool.
+# ---------------------------------------------------------------------------
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    xr, xi = x.float().reshape(*x.shape[:-1], -1, 2).unbind(-1)
+    return torch.stack([-xi, xr], dim=-1).flatten(-2)
+
+
+def apply_rotary_emb(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x [B, T, H, D]; cos, sin [T, D] / [1, T, D] / [B, T, D] (float32)."""
+    B, T, H, D = x.shape
+    c = cos.float().reshape(-1, T, 1, D)
+    s = sin.float().reshape(-1, T, 1, D)
+    return (x.float() * c + rotate_half(x.float()) * s).to(x.dtype)
+
+
+def commit_kv(pool_k, pool_v, stage_k, stage_v, offset: int, cos, sin):
+    """New (pool_k, pool_v) after run_commit: per layer, the RoPE'd stage_k and
+    the stage_v at tokens offset .. offset+T of the pool. pool_*: [L, B, P, H, D];
+    stage_*: [L, B, T, H, D]; pool_v / stage_v may be None."""
+    pk = pool_k.clone()
+    pv = pool_v.clone() if pool_v is not None else None
+    T = stage_k.shape[2]
+    for li in range(stage_k.shape[0]):
+        pk[li, :, offset:offset + T] = apply_rotary_emb(stage_k[li], cos, sin)
+        if pv is not None:
+            pv[li, :, offset:offset + T] = stage_v[li]
+    return pk, pv

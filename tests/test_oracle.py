@@ -292,3 +292,47 @@ def test_norm_quant_oracle_quantizes_the_rounded_y():
     y32 = ops.norm_scale_shift_f32(new_res, None, None, sc, sh, 0, 1e-6)
     _, s_slip = ops.per_token_quant_fp8(y32)
     assert not torch.equal(s_slip, s)
+
+
+def test_apply_rotary_emb_oracle_pins():
+    """Identity and quarter-turn tables give exact results; a general table
+    matches complex multiplication (x0 + i x1)(c + i s) in float64 to the
+    fp32 rounding; a planted sign slip in sin is caught."""
+    g = torch.Generator().manual_seed(11)
+    B, T, H, D = 2, 5, 3, 16
+    x = torch.randn(B, T, H, D, generator=g).to(torch.bfloat16)
+    one, zero = torch.ones(T, D), torch.zeros(T, D)
+    assert torch.equal(ops.apply_rotary_emb(x, one, zero), x)
+    quarter = ops.apply_rotary_emb(x, zero, one).float()
+    x0, x1 = x.float()[..., 0::2], x.float()[..., 1::2]
+    assert torch.equal(quarter[..., 0::2], (-x1).to(torch.bfloat16).float())
+    assert torch.equal(quarter[..., 1::2], x0)
+    ang = torch.rand(T, D // 2, generator=g, dtype=torch.float64) * 40
+    cos = ang.cos().float().repeat_interleave(2, 1)
+    sin = ang.sin().float().repeat_interleave(2, 1)
+    got = ops.apply_rotary_emb(x, cos, sin).float()
+    z = torch.complex(x0.double(), x1.double()) * torch.complex(
+        cos[:, 0::2].double(), sin[:, 0::2].double())[None, :, None, :]
+    ref = torch.stack([z.real, z.imag], -1).flatten(-2)
+    ulp = 2.0 ** (torch.floor(torch.log2(ref.abs().clamp_min(1e-30))) - 7)
+    assert ((got.double() - ref).abs() <= ulp * 1.01 + 1e-6).all()
+
+    def slipped(x, c, s):
+        return (x.float() * c.reshape(1, T, 1, D) - ops.rotate_half(x) * s.reshape(1, T, 1, D)
+                ).to(x.dtype)
+    bad = slipped(x, cos, sin).float()
+    assert not ((bad.double() - ref).abs() <= ulp * 1.01 + 1e-6).all()
+
+
+def test_commit_kv_oracle_touches_only_its_segment():
+    g = torch.Generator().manual_seed(12)
+    L, B, T, P, H, D = 2, 1, 4, 12, 2, 8
+    pool_k = torch.randn(L, B, P, H, D, generator=g).to(torch.bfloat16)
+    pool_v = torch.randn(L, B, P, H, D, generator=g).to(torch.bfloat16)
+    sk = torch.randn(L, B, T, H, D, generator=g).to(torch.bfloat16)
+    sv = torch.randn(L, B, T, H, D, generator=g).to(torch.bfloat16)
+    cos, sin = torch.ones(T, D), torch.zeros(T, D)
+    pk, pv = ops.commit_kv(pool_k, pool_v, sk, sv, 4, cos, sin)
+    assert torch.equal(pk[:, :, 4:8], sk) and torch.equal(pv[:, :, 4:8], sv)
+    assert torch.equal(pk[:, :, :4], pool_k[:, :, :4]) and torch.equal(pk[:, :, 8:], pool_k[:, :, 8:])
+    assert torch.equal(pv[:, :, :4], pool_v[:, :, :4]) and torch.equal(pv[:, :, 8:], pool_v[:, :, 8:])
