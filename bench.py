@@ -137,6 +137,50 @@ def time_gpu(cfg, steps: int, warmup: int, dev, use_graph: bool = True) -> dict:
             "rotated_mb": round(n_sets * set_bytes / 1e6, 1), "timing": "hip-graph"}
 
 
+def torch_reference_us(cfg, dev, iters: int = 10):
+    """Per-call time of the reference's own code path where that path is plain
+    torch, run eagerly on the same GPU: N4 is StreamingGraphRunner.run_commit
+    (graph_runner.py:137-142) over apply_rotary_emb (rope.py:14-28). None for
+    configs whose reference is a CUDA kernel (not runnable here)."""
+    if cfg.op != "kv_commit":
+        return None
+    import torch
+    from joyomni_ops import workloads as W
+
+    def rotate_half(x):
+        x_real, x_imag = x.float().reshape(*x.shape[:-1], -1, 2).unbind(-1)
+        return torch.stack([-x_imag, x_real], dim=-1).flatten(-2)
+
+    def apply_rotary_emb(x, cos, sin):
+        c = cos.view(1, x.shape[1], 1, x.shape[-1])
+        s = sin.view(1, x.shape[1], 1, x.shape[-1])
+        return (x.float() * c + rotate_half(x.float()) * s).type_as(x)
+
+    d = cfg.dims
+    t = {k: v.to(dev) for k, v in W.make_inputs(cfg).items()}
+    seg = slice(d["off"], d["off"] + d["T"])
+
+    def run_commit():
+        for li in range(d["L"]):
+            roped = apply_rotary_emb(t["stage_k"][li], t["cos"], t["sin"])
+            t["pool_k"][li, :, seg].copy_(roped)
+            t["pool_v"][li, :, seg].copy_(t["stage_v"][li])
+
+    for _ in range(2):
+        run_commit()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        run_commit()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / iters
+    del t
+    torch.cuda.empty_cache()
+    return round(us, 1)
+
+
 def cpu_fn(cfg):
     """The oracle's restatement of the reference formula for a config (CPU tensors)."""
     from oracle import ops
@@ -242,6 +286,9 @@ def main() -> int:
         cfg = W.CONFIGS[n]
         log(f"{n}: timing {args.steps} {'eager' if args.no_graph else 'graph-replayed'} calls")
         results[n] = time_gpu(cfg, args.steps, args.warmup, dev, use_graph=not args.no_graph)
+        ref_us = torch_reference_us(cfg, dev)
+        if ref_us is not None:
+            results[n]["torch_reference_us_per_call"] = ref_us
         log(f"{n}: {results[n]}")
     copy = None
     if args.copy_mb:
