@@ -7,7 +7,10 @@ workload (`value`) is BASELINE config 1: per-token FP8 e4m3 quantization of a
 bf16 [10530, 3072] activation. Every other BASELINE config is timed the same
 way and reported under "ops", as are the next-row workloads N3 (the gated
 residual + LayerNorm + AdaLN with the per-token FP8 epilogue, C2 shape) and
-N4 (the graph runner's 40-layer KV-pool commit at the deployment shape).
+N4 (the graph runner's 40-layer KV-pool commit at the deployment shape), and
+the FP8 GEMMs G1-G3 (fp8_scaled_mm at Fp8Linear's deployment shapes), whose
+lines add TFLOP/s against the 5.0 PFLOP/s dense fp8 matrix-core peak and the
+time of torch._scaled_mm (hipBLASLt) on the same operands.
 
 Timing: W eager warmup calls, then K calls captured into one HIP graph and
 replayed once untimed and once timed between HIP events recorded on the
@@ -40,6 +43,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "µs/call + achieved HBM GB/s (% of ~8 TB/s) per op at 720p 3-frame chunk"
 PEAK_GBPS = 8000.0
+PEAK_FP8_TFLOPS = 5000.0
 HEADLINE = "C1"
 HEADLINE_KERNEL = "quant_rows_kernel<BF16, 64, 6>"
 ROT_BYTES = 640e6
@@ -135,6 +139,36 @@ def time_gpu(cfg, steps: int, warmup: int, dev, use_graph: bool = True) -> dict:
             "gbps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_GBPS, 4),
             "algorithmic_bytes": alg, "buffer_sets": n_sets,
             "rotated_mb": round(n_sets * set_bytes / 1e6, 1), "timing": "hip-graph"}
+
+
+def hipblaslt_us(cfg, dev, iters: int = 20):
+    """torch._scaled_mm (hipBLASLt) on a GEMM config's operands, row-wise scales
+    and bias — the vendor library's time for the same problem. None if this
+    torch build cannot run it."""
+    if cfg.op != "gemm":
+        return None
+    import torch
+    from joyomni_ops import workloads as W
+    d = cfg.dims
+    t = {k: v.to(dev) for k, v in W.make_inputs(cfg).items()}
+    a = t["a"].view(torch.float8_e4m3fn)
+    b = t["w"].view(torch.float8_e4m3fn).t()
+    sa, sb = t["sa"].view(d["M"], 1), t["sb"].view(1, d["N"])
+    try:
+        for _ in range(3):
+            torch._scaled_mm(a, b, scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16, bias=t["bias"])
+        torch.cuda.synchronize()
+    except Exception as ex:  # noqa: BLE001 - report, do not fail the bench
+        log(f"torch._scaled_mm unavailable: {str(ex)[:120]}")
+        return None
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        torch._scaled_mm(a, b, scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16, bias=t["bias"])
+    e1.record()
+    torch.cuda.synchronize()
+    del t
+    return round(e0.elapsed_time(e1) * 1000.0 / iters, 2)
 
 
 def torch_reference_us(cfg, dev, iters: int = 10):
@@ -289,6 +323,15 @@ def main() -> int:
         ref_us = torch_reference_us(cfg, dev)
         if ref_us is not None:
             results[n]["torch_reference_us_per_call"] = ref_us
+        flops = W.algorithmic_flops(cfg)
+        if flops is not None:
+            tf = flops / (results[n]["us_per_call"] * 1e-6) / 1e12
+            results[n].update(algorithmic_flops=flops, tflops=round(tf, 1),
+                              frac_of_fp8_peak=round(tf / PEAK_FP8_TFLOPS, 4))
+            lib_us = hipblaslt_us(cfg, dev)
+            if lib_us is not None:
+                results[n]["hipblaslt_us_per_call"] = lib_us
+                results[n]["hipblaslt_tflops"] = round(flops / (lib_us * 1e-6) / 1e12, 1)
         log(f"{n}: {results[n]}")
     copy = None
     if args.copy_mb:

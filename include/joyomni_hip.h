@@ -237,6 +237,23 @@ int jo_norm_scale_shift_quant_fp8(const void* x, int64_t x_stride, void* residua
                                   int64_t N, int dtype, int norm_type, float eps, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Row-wise scaled FP8 GEMM with optional bias.
+ * Replaces joyomni_ops::fp8_scaled_mm
+ *   (deploy/joyomni_ops/csrc/fp8_gemm.cu:1450-1546; epilogue :99-136).
+ *   acc[m, n] = sum_k A[m, k] * B[k, n]   (e4m3fn operands, fp32 accumulation)
+ *   out[m, n] = round( scales_a[m] * (acc[m, n] * scales_b[n]) + bias[n] )
+ * mat_a: fp8 [M, K] row-major, row stride lda bytes; mat_b: fp8 [K, N]
+ * column-major (column n's K bytes contiguous), column stride ldb bytes;
+ * scales_a fp32 [M]; scales_b fp32 [N]; bias [N] of out_dtype or NULL;
+ * out: [M, N] row-major, row stride ldo elements, out_dtype BF16 or F16.
+ * K % 16 == 0, N % 8 == 0, lda and ldb multiples of 16, operands 16-byte
+ * aligned (the reference's alignment rules).
+ * ------------------------------------------------------------------------ */
+int jo_fp8_scaled_mm(const void* mat_a, int64_t lda, const void* mat_b, int64_t ldb,
+                     const float* scales_a, const float* scales_b, const void* bias, void* out,
+                     int64_t ldo, int64_t M, int64_t N, int64_t K, int out_dtype, void* stream);
+
+/* ------------------------------------------------------------------------
  * RoPE'd K and copied V into a KV pool, every layer in one launch:
  *   dst_k[l, b, off + n, :] = apply_rotary_emb(src_k[l, b, n, :], cos[b, n], sin[b, n])
  *   dst_v[l, b, off + n, :] = src_v[l, b, n, :]           (when src_v != NULL)

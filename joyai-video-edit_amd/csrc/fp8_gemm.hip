@@ -1,0 +1,202 @@
+// Row-wise scaled FP8 GEMM with bias (drop-in for the reference's
+// fp8_scaled_mm, deploy/joyomni_ops/csrc/fp8_gemm.cu:1450-1546):
+//   out[m, n] = round_out( scale_a[m] * (acc[m, n] * scale_b[n]) + bias[n] ),
+//   acc[m, n] = sum_k A[m, k] * B[k, n]   (fp8 e4m3fn operands, fp32 accumulate)
+// with A [M, K] row-major and B [K, N] column-major (each column's K bytes
+// contiguous, i.e. B^T [N, K] row-major) — the epilogue order of the
+// reference's visitor tree (fp8_gemm.cu:99-136: acc * scale_b, then
+// scale_a * that + bias, round to nearest).
+//
+// gfx950 design: one 256-thread workgroup per 256x256 output tile; the four
+// waves own 128x128 quadrants computed with v_mfma_f32_32x32x64_f8f6f4
+// (4x4 MFMA tiles, 256 fp32 accumulators per lane). K advances in 128-byte
+// stages: every thread loads 8 sixteen-byte chunks of A and 8 of B^T from
+// HBM into registers for the next stage while the MFMAs run on the current
+// one, then writes them to the other half of a double-buffered LDS tile
+// (2 x 64 KB). LDS rows are 128 bytes; chunk c of row r is stored at chunk
+// position c ^ (r % 8) ^ ((r / 8) % 2), so the 16 rows a 16-lane group
+// reads with one ds_read_b128 fall in 16 distinct 16-byte bank groups.
+#include "jo_device.hpp"
+#include "jo_host.hpp"
+
+namespace jo {
+namespace {
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBM = 256;
+constexpr int kBN = 256;
+constexpr int kBK = 128;                      // bytes of K per stage
+constexpr int kStageBytes = (kBM + kBN) * kBK;  // A tile then B tile
+constexpr int kChunksPerThread = kBM * kBK / 16 / kBlock;  // 8 (same for B)
+
+struct GemmArgs {
+  const uint8_t* a;  // [M, K], row stride lda (bytes)
+  const uint8_t* b;  // B^T [N, K], row stride ldb (bytes)
+  const float* sa;   // [M]
+  const float* sb;   // [N]
+  const void* bias;  // [N] out dtype, optional
+  void* out;         // [M, N] out dtype, row stride ldo (elements)
+  int64_t lda, ldb, ldo;
+  int M, N, K;
+};
+
+__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// One 32x32x64 fp8 MFMA with unit block scales (lowered to the unscaled
+// v_mfma_f32_32x32x64_f8f6f4).
+__device__ __forceinline__ f32x16 mfma32(const i32x8& a, const i32x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+template <class OutTag>
+__global__ __launch_bounds__(kBlock, 1) void fp8_gemm_kernel(const GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kStageBytes];  // 2 stages
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+
+  // Global chunk q = tid + 256 j of a 256 x 128-byte tile: row q / 8, chunk q % 8.
+  // Rows beyond M (N) read row M-1 (N-1): their results are never stored.
+  // Chunks beyond K read as zero so they add nothing.
+  const uint8_t* ga[kChunksPerThread];
+  const uint8_t* gb[kChunksPerThread];
+  int lds_off[kChunksPerThread];
+#pragma unroll
+  for (int j = 0; j < kChunksPerThread; ++j) {
+    const int q = tid + kBlock * j;
+    const int r = q >> 3, c = q & 7;
+    const int ra = min(m0 + r, g.M - 1), rb = min(n0 + r, g.N - 1);
+    ga[j] = g.a + static_cast<int64_t>(ra) * g.lda + c * 16;
+    gb[j] = g.b + static_cast<int64_t>(rb) * g.ldb + c * 16;
+    lds_off[j] = r * kBK + ((c ^ swz(r)) << 4);
+  }
+  const int stages = (g.K + kBK - 1) / kBK;
+  u32x4 ra[kChunksPerThread], rb[kChunksPerThread];
+  auto load_stage = [&](int s) {
+    const int kb = s * kBK;
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
+      const int c = (tid + kBlock * j) & 7;
+      const bool in_k = kb + c * 16 < g.K;
+      ra[j] = in_k ? ld16(ga[j] + kb) : u32x4{0u, 0u, 0u, 0u};
+      rb[j] = in_k ? ld16(gb[j] + kb) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_stage = [&](int buf) {
+    uint8_t* base = smem + buf * kStageBytes;
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
+      *reinterpret_cast<u32x4*>(base + lds_off[j]) = ra[j];
+      *reinterpret_cast<u32x4*>(base + kBM * kBK + lds_off[j]) = rb[j];
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Fragment read offsets: tile row (l % 32) of subtile i, chunk pair
+  // (l / 32) * 2 + {0, 1} of k-slice s (4 chunks per 64-byte slice).
+  const int fr = lane & 31, fh = lane >> 5;
+
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+  for (int s = 0; s < stages; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < stages) load_stage(s + 1);
+    const uint8_t* As = smem + buf * kStageBytes;
+    const uint8_t* Bs = As + kBM * kBK;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      i32x8 af[4], bf[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = wm * 128 + i * 32 + fr;
+        const int c = ks * 4 + fh * 2;
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(As + r * kBK + ((c ^ swz(r)) << 4));
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(As + r * kBK + (((c + 1) ^ swz(r)) << 4));
+        af[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = wn * 128 + j * 32 + fr;
+        const int c = ks * 4 + fh * 2;
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(Bs + r * kBK + ((c ^ swz(r)) << 4));
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(Bs + r * kBK + (((c + 1) ^ swz(r)) << 4));
+        bf[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(af[i], bf[j], acc[i][j]);
+    }
+    if (s + 1 < stages) store_stage(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds column n = n0 + wn*128 + j*32 + (l % 32) of subtile
+  // (i, j), rows m = m0 + wm*128 + i*32 + (e / 4)*8 + (l / 32)*4 + e % 4.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + wn * 128 + j * 32 + fr;
+    if (n >= g.N) continue;
+    const float sbn = g.sb[n];
+    const float bn = g.bias ? load_elem<OutTag>(g.bias, n) : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm * 128 + i * 32 + (e >> 2) * 8 + fh * 4 + (e & 3);
+        if (m < g.M) {
+          const float t = acc[i][j][e] * sbn;
+          store_elem<OutTag>(g.out, static_cast<int64_t>(m) * g.ldo + n, __builtin_fmaf(g.sa[m], t, bn));
+        }
+      }
+    }
+  }
+}
+
+template <class OutTag>
+int launch_gemm(const GemmArgs& g, hipStream_t stream) {
+  const dim3 grid((g.N + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
+  hipLaunchKernelGGL((fp8_gemm_kernel<OutTag>), grid, dim3(kBlock), 0, stream, g);
+  return launch_status("fp8_scaled_mm");
+}
+
+}  // namespace
+}  // namespace jo
+
+using namespace jo;
+
+extern "C" int jo_fp8_scaled_mm(const void* mat_a, int64_t lda, const void* mat_b, int64_t ldb,
+                                const float* scales_a, const float* scales_b, const void* bias,
+                                void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                                int out_dtype, void* stream) {
+  const char* op = "fp8_scaled_mm";
+  JO_REQUIRE(out_dtype == JO_DTYPE_BF16 || out_dtype == JO_DTYPE_F16,
+             "out_dtype must be Half or BFloat16");
+  JO_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
+             "%s: bad shape", op);
+  JO_REQUIRE(K % 16 == 0, "mat_a must be multiple of 16 bytes for memory alignment");
+  JO_REQUIRE(N % 8 == 0, "out must be multiple of 16 bytes for memory alignment");
+  JO_REQUIRE(lda >= K && ldb >= K && ldo >= N && lda % 16 == 0 && ldb % 16 == 0 && ldo % 8 == 0,
+             "%s: row strides must cover the rows and keep 16-byte alignment", op);
+  if (M == 0 || N == 0) return JO_OK;
+  JO_REQUIRE(mat_a && mat_b && scales_a && scales_b && out, "%s: null pointer", op);
+  JO_REQUIRE(aligned(mat_a, 16) && aligned(mat_b, 16) && aligned(out, 16),
+             "%s: operands must be 16-byte aligned", op);
+  GemmArgs g{static_cast<const uint8_t*>(mat_a), static_cast<const uint8_t*>(mat_b), scales_a,
+             scales_b, bias, out, lda, ldb, ldo, static_cast<int>(M), static_cast<int>(N),
+             static_cast<int>(K)};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return out_dtype == JO_DTYPE_BF16 ? launch_gemm<BF16>(g, st) : launch_gemm<F16>(g, st);
+}

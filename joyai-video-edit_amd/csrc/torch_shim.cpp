@@ -1,9 +1,9 @@
 // TORCH_LIBRARY(joyomni_ops) registration over the C ABI of libjoyomni_hip.so.
 //
-// The four reference ops keep their schema strings byte-for-byte
-// (deploy/joyomni_ops/csrc/pybind.cpp:35-43) and their TORCH_CHECKs
+// The five reference ops keep their schema strings byte-for-byte
+// (deploy/joyomni_ops/csrc/pybind.cpp:35-46) and their TORCH_CHECKs
 // (fused_qknorm_rope_3d_kernel.cu:183-200, fused_norm_scale_shift.cu:176-196,
-// rmsnorm.cu:77-81, per_token_quant_fp8.cu:149-156), so
+// rmsnorm.cu:77-81, per_token_quant_fp8.cu:149-156, fp8_gemm.cu:1457-1485), so
 // torch.ops.joyomni_ops.* behaves as the reference does for callers. The new
 // ops (grid RoPE, K ring-cache write, add+LayerNorm, RMSNorm->FP8,
 // norm+AdaLN->FP8, KV-pool commit, apply_rotary_emb) have their own names. Tensors on ROCm carry the CUDA
@@ -536,6 +536,57 @@ torch::Tensor apply_rotary_emb(const torch::Tensor& x, const torch::Tensor& cos,
   return out;
 }
 
+// Checks of fp8_gemm.cu:1457-1485 (messages verbatim), plus the leading
+// dimensions the kernel needs (multiples of 16 bytes).
+torch::Tensor fp8_scaled_mm(const torch::Tensor& mat_a, const torch::Tensor& mat_b,
+                            const torch::Tensor& scales_a, const torch::Tensor& scales_b,
+                            c10::ScalarType out_dtype, const c10::optional<torch::Tensor>& bias) {
+  TORCH_CHECK(mat_a.is_cuda(), "mat_a must be a CUDA tensor");
+  TORCH_CHECK(mat_b.is_cuda(), "mat_b must be a CUDA tensor");
+  TORCH_CHECK(mat_a.dim() == 2, "mat_a must be a 2D tensor");
+  TORCH_CHECK(mat_b.dim() == 2, "mat_b must be a 2D tensor");
+  TORCH_CHECK(mat_a.stride(1) == 1, "mat_a must be a row major tensor");
+  TORCH_CHECK(mat_b.stride(0) == 1, "mat_b must be a column major tensor");
+  TORCH_CHECK(mat_a.size(1) == mat_b.size(0), "mat_a and mat_b shapes cannot be multiplied");
+  TORCH_CHECK((mat_a.size(1) * mat_a.element_size()) % 16 == 0,
+              "mat_a must be multiple of 16 bytes for memory alignment");
+  TORCH_CHECK((mat_b.size(0) * mat_b.element_size()) % 16 == 0,
+              "mat_b must be multiple of 16 bytes for memory alignment");
+  TORCH_CHECK(mat_a.scalar_type() == torch::kFloat8_e4m3fn, "mat_a must be Float8_e4m3fn");
+  TORCH_CHECK(mat_b.scalar_type() == torch::kFloat8_e4m3fn, "mat_b must be Float8_e4m3fn");
+  TORCH_CHECK(out_dtype == torch::kHalf || out_dtype == torch::kBFloat16,
+              "out_dtype must be Half or BFloat16");
+  TORCH_CHECK(scales_a.numel() == mat_a.size(0), "size of scales_a is not matched");
+  TORCH_CHECK(scales_b.numel() == mat_b.size(1), "size of scales_b is not matched");
+  TORCH_CHECK(scales_a.is_contiguous(), "scales_a must be contiguous");
+  TORCH_CHECK(scales_b.is_contiguous(), "scales_b msut be contiguous");
+  TORCH_CHECK(scales_a.scalar_type() == torch::kFloat32, "scales_a must be Float32");
+  TORCH_CHECK(scales_b.scalar_type() == torch::kFloat32, "scales_b must be Float32");
+  const bool has_bias = bias.has_value() && bias->defined();
+  if (has_bias) {
+    TORCH_CHECK(bias->numel() == mat_b.size(1), "size of bias is not matched");
+    TORCH_CHECK(bias->is_contiguous(), "bias must be contiguous");
+    TORCH_CHECK(bias->dtype() == out_dtype, "bias dtype must match output dtype");
+  }
+  const int64_t M = mat_a.size(0), K = mat_a.size(1), N = mat_b.size(1);
+  const int64_t lda = M <= 1 ? K : mat_a.stride(0);
+  const int64_t ldb = N <= 1 ? K : mat_b.stride(1);
+  TORCH_CHECK(lda % 16 == 0 && ldb % 16 == 0,
+              "mat_a / mat_b leading dimensions must be multiples of 16 bytes");
+  torch::Tensor out = torch::empty({M, N}, mat_a.options().dtype(out_dtype));
+  TORCH_CHECK((out.size(1) * out.element_size()) % 16 == 0,
+              "out must be multiple of 16 bytes for memory alignment");
+  if (M == 0 || N == 0) return out;
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(mat_a.device());
+  check_status(jo_fp8_scaled_mm(mat_a.data_ptr(), lda, mat_b.data_ptr(), ldb,
+                                scales_a.data_ptr<float>(), scales_b.data_ptr<float>(),
+                                has_bias ? bias->data_ptr() : nullptr, out.data_ptr(), N, M, N, K,
+                                out_dtype == torch::kBFloat16 ? JO_DTYPE_BF16 : JO_DTYPE_F16,
+                                current_stream(mat_a)),
+               "fp8_scaled_mm");
+  return out;
+}
+
 }  // namespace joyomni_ops
 
 TORCH_LIBRARY(joyomni_ops, m) {
@@ -548,6 +599,9 @@ TORCH_LIBRARY(joyomni_ops, m) {
       "Tensor scale, Tensor shift, int norm_type, float eps) -> Tensor");
   m.def("rmsnorm(Tensor x, Tensor weight, float eps) -> Tensor");
   m.def("sgl_per_token_quant_fp8(Tensor input, Tensor! output_q, Tensor! output_s) -> ()");
+  m.def(
+      "fp8_scaled_mm(Tensor mat_a, Tensor mat_b, Tensor scales_a, Tensor scales_b, "
+      "ScalarType out_dtype, Tensor? bias) -> Tensor");
   // New ops.
   m.def(
       "fused_qk_norm_rope_3d_grid(Tensor! q, Tensor! k, int seq_len, int num_heads, float eps, "
@@ -578,6 +632,7 @@ TORCH_LIBRARY_IMPL(joyomni_ops, CUDA, m) {
   m.impl("fused_norm_scale_shift", &joyomni_ops::fused_norm_scale_shift);
   m.impl("rmsnorm", &joyomni_ops::rmsnorm);
   m.impl("sgl_per_token_quant_fp8", &joyomni_ops::sgl_per_token_quant_fp8);
+  m.impl("fp8_scaled_mm", &joyomni_ops::fp8_scaled_mm);
   m.impl("fused_qk_norm_rope_3d_grid", &joyomni_ops::fused_qk_norm_rope_3d_grid);
   m.impl("fused_qk_norm_rope_3d_kvcache", &joyomni_ops::fused_qk_norm_rope_3d_kvcache);
   m.impl("fused_add_layernorm_scale_shift", &joyomni_ops::fused_add_layernorm_scale_shift);

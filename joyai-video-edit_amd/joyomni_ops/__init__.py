@@ -73,12 +73,7 @@ def rmsnorm(x, weight, eps=1e-6):
 
 
 def has_fp8() -> bool:
-    """True when the FP8 GEMM op is registered (the reference's test, __init__.py:49-50).
-
-    This library provides the FP8 quantization ops but not fp8_scaled_mm, so
-    callers take the reference's bf16 GEMM path, as with a reference build
-    made with JOYOMNI_OPS_NO_FP8.
-    """
+    """True when the FP8 GEMM op is registered (the reference's test, __init__.py:49-50)."""
     return hasattr(_ops, "fp8_scaled_mm")
 
 
@@ -87,9 +82,8 @@ def sgl_per_token_quant_fp8(input, output_q, output_s):
 
 
 def fp8_scaled_mm(mat_a, mat_b, scales_a, scales_b, out_dtype, bias: Optional[torch.Tensor] = None):
-    """Rowwise-scaled FP8 GEMM: not implemented by this library (has_fp8() is False)."""
-    if not has_fp8():
-        raise NotImplementedError("fp8_scaled_mm is not provided by this build (has_fp8() is False)")
+    """Row-wise scaled FP8 GEMM: scales_a[m] * (mat_a @ mat_b * scales_b[n]) + bias[n].
+    mat_a fp8 [M, K] row-major, mat_b fp8 [K, N] column-major; out_dtype bf16/fp16."""
     return _ops.fp8_scaled_mm(mat_a, mat_b, scales_a, scales_b, out_dtype, bias)
 
 

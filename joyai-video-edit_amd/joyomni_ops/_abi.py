@@ -51,6 +51,7 @@ SIGNATURES: dict[str, list] = {
     "jo_norm_scale_shift_quant_fp8": [
         _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64,
         c_int, c_int, _F, _P],
+    "jo_fp8_scaled_mm": [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, c_int, _P],
     "jo_kv_commit_rope": [
         _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
         _I64, _P, _P, _I64, _I64, c_int, _P],

@@ -24,6 +24,9 @@ Additional entry points for callers that can use the new fused ops:
   fused_add_gate_layernorm_modulate_fp8  the same after residual + x * gate.
   commit_kv_pool            StreamingGraphRunner.run_commit (graph_runner.py:137-142)
                             for all layers in one launch.
+  fp8_linear                Fp8Linear.forward (fp8_linear.py:155-169): per-token
+                            quantization + fp8_scaled_mm; quantize_weight_per_channel
+                            is its weight preparation (fp8_linear.py:100-110).
 """
 from __future__ import annotations
 
@@ -31,7 +34,7 @@ from typing import Optional, Sequence, Tuple
 
 import torch
 
-from . import (fused_add_layernorm_scale_shift, fused_norm_scale_shift,
+from . import (fp8_scaled_mm, fused_add_layernorm_scale_shift, fused_norm_scale_shift,
                fused_qk_norm_rope_3d_grid, fused_qk_norm_rope_3d_paired,
                kv_commit_rope, norm_scale_shift_quant_fp8, rmsnorm, rope_freqs,
                sgl_per_token_quant_fp8)
@@ -275,3 +278,34 @@ def commit_kv_pool(pool_k: torch.Tensor, pool_v: torch.Tensor, stage_k: torch.Te
     RoPE and two copies per layer. pool_*: [L, B, P, H, D]; stage_*: [L, B, T, H, D];
     commit_cos/sin: fp32 [1, T, D]. Bit-identical to the loop."""
     kv_commit_rope(stage_k, pool_k, offset, commit_cos, commit_sin, src_v=stage_v, dst_v=pool_v)
+
+
+FP8_MAX = 448.0
+
+
+def quantize_weight_per_channel(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Fp8Linear's weight preparation (fp8_linear.py:100-110, the path without
+    fast accumulation): w [N, K] -> (w_q fp8 [K, N] column-major, scale fp32 [N])
+    with scale = max|w[n, :]| / 448 (floored at 1e-8 / 448)."""
+    w_kn = w.to(torch.bfloat16).t().contiguous()
+    absmax = w_kn.abs().amax(dim=0).to(torch.float32).clamp_min(1e-8)
+    scale = absmax / FP8_MAX
+    w_q_rm = (w_kn.float() / scale.unsqueeze(0)).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return w_q_rm.t().contiguous().t(), scale
+
+
+def fp8_linear(x: torch.Tensor, weight_fp8: torch.Tensor, weight_scale: torch.Tensor,
+               bias: Optional[torch.Tensor] = None, out_dtype=torch.bfloat16) -> torch.Tensor:
+    """Fp8Linear.forward (fp8_linear.py:155-169): x [..., K] bf16 -> per-token
+    fp8 + scales -> fp8_scaled_mm with the per-channel weight scales and bias."""
+    x_q, x_scale = quantize_activation_fp8(x)
+    y = fp8_scaled_mm(x_q, weight_fp8, x_scale, weight_scale, out_dtype, bias)
+    return y.reshape(*x.shape[:-1], weight_fp8.shape[1])
+
+
+def fp8_linear_quantized(x_q: torch.Tensor, x_scale: torch.Tensor, weight_fp8: torch.Tensor,
+                         weight_scale: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                         out_dtype=torch.bfloat16) -> torch.Tensor:
+    """The GEMM half of fp8_linear for activations already quantized in a norm's
+    epilogue (layernorm_modulate_fp8 / fused_add_gate_layernorm_modulate_fp8)."""
+    return fp8_scaled_mm(x_q, weight_fp8, x_scale, weight_scale, out_dtype, bias)

@@ -12,6 +12,9 @@ Next-row workloads (not BASELINE configs; same shapes):
   N3   gated residual add + LayerNorm + AdaLN with the per-token FP8 epilogue
        (the y of C2 quantized for the next Fp8Linear instead of written):
        x, residual bf16 [10530, 3072], gate/scale/shift bf16 [3072]
+  G1   FP8 GEMMs of Fp8Linear at the deployment shape (M = 3120 tokens, hidden
+  G2   4096): G1 qkv [3120 x 4096] x [4096 x 12288], G2 MLP up x [4096 x 16384],
+  G3   G3 MLP down [3120 x 16384] x [16384 x 4096]; bf16 output with bias
   N4   KV-pool commit of the graph runner at the deployment shape: RoPE'd K and
        V of 40 layers x 1560 tokens x 32 heads x 128 into a [40, 1, 3120, 32, 128]
        pool at token offset 1560, fp32 [1560, 128] tables
@@ -52,6 +55,9 @@ CONFIGS: dict[str, Config] = {
     "C4_10530_blk": Config("C4_10530_blk", "rms_quant", 4, dict(M=10530, N=3072, group=128, eps=1e-6)),
     "N3": Config("N3", "add_ln_quant", 5, dict(M=10530, N=3072, eps=1e-6)),
     "N4": Config("N4", "kv_commit", 6, dict(L=40, T=1560, P=3120, off=1560, H=32, D=128)),
+    "G1": Config("G1", "gemm", 7, dict(M=3120, N=12288, K=4096)),
+    "G2": Config("G2", "gemm", 8, dict(M=3120, N=16384, K=4096)),
+    "G3": Config("G3", "gemm", 9, dict(M=3120, N=4096, K=16384)),
 }
 
 
@@ -87,6 +93,14 @@ def make_inputs(cfg: Config, device="cpu") -> dict:
         out["scale"] = (0.2 * torch.randn(d["N"], generator=g)).to(torch.bfloat16)
         if cfg.op == "add_ln_quant":
             out["gate"] = torch.randn(d["N"], generator=g).to(torch.bfloat16)
+    elif cfg.op == "gemm":
+        M, N, K = d["M"], d["N"], d["K"]
+        # fp8 codes of N(0, 4) values (no NaN), per-row / per-column scales, bias
+        out["a"] = (torch.randn(M, K, generator=g) * 4).to(torch.float8_e4m3fn).view(torch.uint8)
+        out["w"] = (torch.randn(N, K, generator=g) * 4).to(torch.float8_e4m3fn).view(torch.uint8)
+        out["sa"] = torch.rand(M, generator=g) * 0.02 + 1e-3
+        out["sb"] = torch.rand(N, generator=g) * 0.02 + 1e-3
+        out["bias"] = torch.randn(N, generator=g).to(torch.bfloat16)
     elif cfg.op == "kv_commit":
         shape = (d["L"], 1, d["T"], d["H"], d["D"])
         out["stage_k"] = torch.randn(shape, generator=g).to(torch.bfloat16)
@@ -123,10 +137,19 @@ def algorithmic_bytes(cfg: Config) -> int:
     if cfg.op == "add_ln_quant":
         # x, res in; res out (bf16); fp8 out; scales; gate/scale/shift rows
         return 7 * d["M"] * d["N"] + 4 * d["M"] + 3 * d["N"] * 2
+    if cfg.op == "gemm":
+        # A, B^T read once, out written once, scales and bias
+        return d["M"] * d["K"] + d["N"] * d["K"] + d["M"] * d["N"] * 2 + d["M"] * 4 + d["N"] * 6
     if cfg.op == "kv_commit":
         # stage K, V read; pool K, V segment written; cos/sin tables
         return 4 * d["L"] * d["T"] * d["H"] * d["D"] * 2 + 2 * d["T"] * d["D"] * 4
     raise ValueError(cfg.op)
+
+
+def algorithmic_flops(cfg: Config) -> int | None:
+    """Matrix-core flops of one call (GEMM configs), else None."""
+    d = cfg.dims
+    return 2 * d["M"] * d["N"] * d["K"] if cfg.op == "gemm" else None
 
 
 def alloc_outputs(cfg: Config, inputs: dict) -> dict:
@@ -141,6 +164,8 @@ def alloc_outputs(cfg: Config, inputs: dict) -> dict:
                 "s": torch.empty(ns, dtype=torch.float32, device=dev)}
     if cfg.op == "add_ln":
         return {"y": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev)}
+    if cfg.op == "gemm":
+        return {"out": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev)}
     if cfg.op == "add_ln_quant":
         return {"q": torch.empty(d["M"], d["N"], dtype=torch.float8_e4m3fn, device=dev),
                 "s": torch.empty(d["M"], dtype=torch.float32, device=dev)}
@@ -171,6 +196,10 @@ def launch(cfg: Config, t: dict, stream_handle: int, freqs: torch.Tensor | None 
                   p(t["gate"]), 0, None, None, p(t["scale"]), 0, p(t["shift"]), 0, p(t["q"]),
                   d["N"], p(t["s"]), d["M"], d["N"], _abi.JO_DTYPE_BF16, _abi.JO_NORM_LAYER,
                   d["eps"], stream_handle)
+    elif cfg.op == "gemm":
+        M, N, K = d["M"], d["N"], d["K"]
+        _abi.call("jo_fp8_scaled_mm", p(t["a"]), K, p(t["w"]), K, p(t["sa"]), p(t["sb"]),
+                  p(t["bias"]), p(t["out"]), N, M, N, K, _abi.JO_DTYPE_BF16, stream_handle)
     elif cfg.op == "kv_commit":
         L, T, P, H, D = d["L"], d["T"], d["P"], d["H"], d["D"]
         hd = H * D

@@ -35,4 +35,8 @@ its tests only print fp32-formula diffs):
                         multiplication in float64, a planted sign slip.
   commit_kv             apply_rotary_emb per layer + copies (pool regions
                         outside the segment unchanged).
+  fp8_scaled_mm         exact integer matmul (int64 on the fp8 values times
+                        2^9) equals the float64 accumulation; decoding of all
+                        256 codes against the C encoder's table; the
+                        epilogue order against a hand-checked row.
 """

@@ -310,3 +310,30 @@ def commit_kv(pool_k, pool_v, stage_k, stage_v, offset: int, cos, sin):
         if pv is not None:
             pv[li, :, offset:offset + T] = stage_v[li]
     return pk, pv
+
+
+# ---------------------------------------------------------------------------
+# Row-wise scaled FP8 GEMM — deploy/joyomni_ops/csrc/fp8_gemm.cu:1450-1546, the
+# epilogue of its visitor tree (:99-136): t = acc * scale_b (fp32), then
+# scale_a * t + bias (multiply-add), rounded to the output dtype.
+# The float64 product of e4m3fn operands is exact: every product is a
+# multiple of 2^-18 below 2^18, so any sum of up to 2^16 of them fits in a
+# double's 53 bits, whatever the order.
+# ---------------------------------------------------------------------------
+def fp8_scaled_mm(a_q: torch.Tensor, b_q: torch.Tensor, scale_a: torch.Tensor,
+                  scale_b: torch.Tensor, out_dtype, bias: torch.Tensor | None = None):
+    """a_q fp8 [M, K], b_q fp8 [K, N] (any strides). Returns (out [M, N] of
+    out_dtype, acc float64 [M, N] exact, mag float64 [M, N] = sum |a||b| scaled
+    by the row and column scales — the size of the terms, for tolerances)."""
+    a = a_q.float().double()
+    b = b_q.float().double()
+    acc = a @ b
+    sa = scale_a.reshape(-1, 1).float()
+    sb = scale_b.reshape(1, -1).float()
+    t = acc.float() * sb
+    out = sa.double() * t.double()
+    if bias is not None:
+        out = out + bias.float().double().reshape(1, -1)
+    out32 = out.float()  # one rounding of the multiply-add
+    mag = (a.abs() @ b.abs()) * sa.double() * sb.double()
+    return out32.to(out_dtype), acc, mag

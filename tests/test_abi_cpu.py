@@ -127,6 +127,10 @@ REFERENCE_SCHEMAS = {
     "rmsnorm": "rmsnorm(Tensor x, Tensor weight, float eps) -> Tensor",
     "sgl_per_token_quant_fp8":
         "sgl_per_token_quant_fp8(Tensor input, Tensor! output_q, Tensor! output_s) -> ()",
+    # pybind.cpp:44-46
+    "fp8_scaled_mm":
+        "fp8_scaled_mm(Tensor mat_a, Tensor mat_b, Tensor scales_a, Tensor scales_b, "
+        "ScalarType out_dtype, Tensor? bias) -> Tensor",
 }
 
 
@@ -136,9 +140,10 @@ def test_torch_ops_register_reference_schemas():
         expected = torch._C.parse_schema("joyomni_ops::" + schema)
         assert getattr(torch.ops.joyomni_ops, name).default._schema == expected, name
     for name in ("fused_qk_norm_rope_3d_grid", "fused_qk_norm_rope_3d_kvcache",
-                 "fused_add_layernorm_scale_shift", "rmsnorm_quant_fp8"):
+                 "fused_add_layernorm_scale_shift", "rmsnorm_quant_fp8",
+                 "norm_scale_shift_quant_fp8", "kv_commit_rope", "apply_rotary_emb"):
         assert hasattr(torch.ops.joyomni_ops, name)
-    assert not jo.has_fp8()
+    assert jo.has_fp8()
 
 
 def test_ops_have_no_cpu_kernel():

@@ -1,0 +1,129 @@
+"""GPU parity of the row-wise scaled FP8 GEMM (jo_fp8_scaled_mm, torch op
+fp8_scaled_mm, dit_ops.fp8_linear).
+
+Bar: every output within 1 ulp of the output dtype of the exact result
+scale_a[m] * scale_b[n] * sum_k a*b + bias[n] (float64 from the oracle, whose
+accumulation is exact for fp8 operands), plus 2^-13 of the scaled sum of |a*b|
+terms for the fp32 accumulation inside the matrix cores (a dropped 16-byte K
+chunk or a wrong scale is far outside it). The full deployment shapes are
+checked on sampled rows (the last, ragged row tile included).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def ulp(x, dtype):
+    frac = 7 if dtype == torch.bfloat16 else 10
+    e = torch.floor(torch.log2(x.abs().clamp_min(2.0 ** -14)))
+    return 2.0 ** (e - frac)
+
+
+def check(out, a, b, sa, sb, bias, what, rows=None):
+    """out [M', N] device result (rows `rows` of the full result if given)."""
+    a_r = a if rows is None else a[rows]
+    sa_r = sa if rows is None else sa[rows]
+    _, acc, mag = ops.fp8_scaled_mm(a_r, b, sa_r, sb, out.dtype, bias)
+    ref = acc * sa_r.double().reshape(-1, 1) * sb.double().reshape(1, -1)
+    if bias is not None:
+        ref = ref + bias.double().reshape(1, -1)
+    got = out.cpu().double()
+    tol = ulp(ref, out.dtype) + mag * 2.0 ** -13
+    err = (got - ref).abs()
+    bad = (err > tol).nonzero()
+    assert bad.numel() == 0, (f"{what}: {bad.shape[0]} outputs off, first {bad[0].tolist()}: "
+                              f"{got[tuple(bad[0])].item()} vs {ref[tuple(bad[0])].item()}")
+
+
+def operands(M, N, K, seed, dtype=torch.bfloat16, with_bias=True):
+    g = torch.Generator().manual_seed(seed)
+    a = (torch.randn(M, K, generator=g) * 4).to(torch.float8_e4m3fn)
+    w = (torch.randn(N, K, generator=g) * 4).to(torch.float8_e4m3fn)   # weight [N, K]
+    sa = torch.rand(M, generator=g) * 0.02 + 1e-3
+    sb = torch.rand(N, generator=g) * 0.02 + 1e-3
+    bias = torch.randn(N, generator=g).to(dtype) if with_bias else None
+    return a, w, sa, sb, bias
+
+
+SHAPES = [(1, 8, 16), (17, 8, 16), (256, 256, 128), (300, 264, 208), (257, 520, 400),
+          (3120, 512, 4096), (129, 1024, 16384), (64, 2048, 4096)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_fp8_scaled_mm_matches_oracle(dev, M, N, K, dtype, with_bias):
+    import joyomni_ops as jo
+    a, w, sa, sb, bias = operands(M, N, K, M + N + K, dtype, with_bias)
+    mat_b = w.to(dev).t()                      # [K, N] column-major, as Fp8Linear stores it
+    out = jo.fp8_scaled_mm(a.to(dev), mat_b, sa.to(dev), sb.to(dev), dtype,
+                           bias.to(dev) if with_bias else None)
+    torch.cuda.synchronize()
+    assert out.shape == (M, N) and out.dtype == dtype
+    check(out, a, w.t(), sa, sb, bias, f"[{M},{N},{K}] {dtype} bias={with_bias}")
+
+
+def test_fp8_scaled_mm_strided_operands(abi, dev, stream_handle):
+    """A and B^T rows padded (lda, ldb > K), an output row stride > N, scales
+    given as [M, 1] (Fp8Linear's x_scale)."""
+    M, N, K = 200, 136, 320
+    a, w, sa, sb, bias = operands(M, N, K, 5)
+    ap = torch.zeros(M, K + 48, dtype=torch.uint8)
+    ap[:, :K] = a.view(torch.uint8)
+    wp = torch.zeros(N, K + 32, dtype=torch.uint8)
+    wp[:, :K] = w.view(torch.uint8)
+    apd, wpd = ap.to(dev), wp.to(dev)
+    out = torch.full((M, N + 24), 7.0, dtype=torch.bfloat16, device=dev)
+    sad, sbd, bd = sa.reshape(M, 1).to(dev), sb.to(dev), bias.to(dev)
+    abi.call("jo_fp8_scaled_mm", apd.data_ptr(), K + 48, wpd.data_ptr(), K + 32, sad.data_ptr(),
+             sbd.data_ptr(), bd.data_ptr(), out.data_ptr(), N + 24, M, N, K,
+             abi.dtype_code(torch.bfloat16), stream_handle)
+    torch.cuda.synchronize()
+    assert (out.cpu()[:, N:] == 7.0).all(), "columns beyond N written"
+    check(out[:, :N], a, w.t(), sa, sb, bias, "strided")
+
+
+@pytest.mark.parametrize("N,K", [(12288, 4096), (16384, 4096), (4096, 16384)])
+def test_fp8_scaled_mm_deployment_shapes_sampled_rows(dev, N, K):
+    """M = 3120 tokens (720x1248 image stream); 40 sampled rows, the ragged
+    last row tile included, against the exact oracle."""
+    import joyomni_ops as jo
+    M = 3120
+    a, w, sa, sb, bias = operands(M, N, K, N + K)
+    out = jo.fp8_scaled_mm(a.to(dev), w.to(dev).t(), sa.to(dev), sb.to(dev), torch.bfloat16,
+                           bias.to(dev))
+    torch.cuda.synchronize()
+    g = torch.Generator().manual_seed(1)
+    rows = torch.cat([torch.randperm(3072, generator=g)[:24], torch.arange(3104, 3120)])
+    check(out.cpu()[rows], a, w.t(), sa, sb, bias, f"[{M},{N},{K}] sampled", rows=rows)
+
+
+def test_fp8_linear_shim_and_rejects(dev):
+    """dit_ops.fp8_linear == per-token quantization + GEMM (Fp8Linear.forward),
+    with the weight prepared like Fp8Linear.from_linear; reference errors."""
+    import joyomni_ops as jo
+    from joyomni_ops import dit_ops
+    g = torch.Generator().manual_seed(3)
+    B, L, K, N = 2, 96, 512, 384
+    x = torch.randn(B, L, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16)
+    wq, ws = dit_ops.quantize_weight_per_channel(w.to(dev))
+    assert wq.shape == (K, N) and wq.stride() == (1, K)
+    y = dit_ops.fp8_linear(x.to(dev), wq, ws, bias.to(dev))
+    torch.cuda.synchronize()
+    xq, xs = ops.per_token_quant_fp8(x.reshape(-1, K))
+    check(y.reshape(-1, N), xq.view(torch.float8_e4m3fn), wq.cpu(), xs, ws.cpu(), bias, "fp8_linear")
+    a = torch.zeros(4, 32, dtype=torch.float8_e4m3fn, device=dev)
+    s4, s8 = torch.ones(4, device=dev), torch.ones(8, device=dev)
+    with pytest.raises(RuntimeError, match="column major"):
+        jo.fp8_scaled_mm(a, torch.zeros(32, 8, dtype=torch.float8_e4m3fn, device=dev), s4, s8,
+                         torch.bfloat16)
+    with pytest.raises(RuntimeError, match="out_dtype must be Half or BFloat16"):
+        jo.fp8_scaled_mm(a, torch.zeros(8, 32, dtype=torch.float8_e4m3fn, device=dev).t(), s4, s8,
+                         torch.float32)

@@ -336,3 +336,47 @@ def test_commit_kv_oracle_touches_only_its_segment():
     assert torch.equal(pk[:, :, 4:8], sk) and torch.equal(pv[:, :, 4:8], sv)
     assert torch.equal(pk[:, :, :4], pool_k[:, :, :4]) and torch.equal(pk[:, :, 8:], pool_k[:, :, 8:])
     assert torch.equal(pv[:, :, :4], pool_v[:, :, :4]) and torch.equal(pv[:, :, 8:], pool_v[:, :, 8:])
+
+
+def test_fp8_gemm_oracle_accumulation_is_exact():
+    """The float64 accumulation of e4m3fn products equals an exact int64
+    matmul of the same values scaled by 2^9 (each code is a multiple of
+    2^-9), on random codes spanning the whole range, NaN excluded."""
+    g = torch.Generator().manual_seed(2)
+    M, K, N = 9, 512, 7
+    codes_a = torch.randint(0, 256, (M, K), generator=g, dtype=torch.uint8)
+    codes_b = torch.randint(0, 256, (K, N), generator=g, dtype=torch.uint8)
+    codes_a[(codes_a & 0x7F) == 0x7F] = 0x7E
+    codes_b[(codes_b & 0x7F) == 0x7F] = 0x7E
+    a = codes_a.view(torch.float8_e4m3fn)
+    b = codes_b.view(torch.float8_e4m3fn)
+    ai = (a.float().double() * 512).round().long()
+    bi = (b.float().double() * 512).round().long()
+    assert torch.equal(ai.double() / 512, a.float().double())
+    exact = (ai @ bi).double() / 2.0 ** 18
+    _, acc, _ = ops.fp8_scaled_mm(a, b, torch.ones(M), torch.ones(N), torch.bfloat16)
+    assert torch.equal(acc, exact)
+
+
+def test_fp8_decode_matches_c_encoder_table():
+    codes = torch.arange(256, dtype=torch.uint8)
+    vals = codes.view(torch.float8_e4m3fn).float()
+    for c in range(256):
+        ref = fp8ref.decode(c)
+        if math.isnan(ref):
+            assert math.isnan(vals[c].item())
+        else:
+            assert vals[c].item() == ref, c
+
+
+def test_fp8_gemm_oracle_epilogue_order():
+    """scale_a * (acc * scale_b) + bias with fp32 roundings between, not
+    (scale_a * scale_b) * acc: a row where the two orders differ in fp32."""
+    a = torch.tensor([[12.0, 0.0]]).to(torch.float8_e4m3fn)
+    b = torch.tensor([[1.0], [0.0]]).to(torch.float8_e4m3fn)
+    sa = torch.tensor([1032143960], dtype=torch.int32).view(torch.float32)   # 0.0650717616...
+    sb = torch.tensor([1031643931], dtype=torch.int32).view(torch.float32)   # 0.0619231276...
+    out, acc, _ = ops.fp8_scaled_mm(a, b, sa, sb, torch.float32)
+    t = torch.tensor(12.0, dtype=torch.float32) * sb[0]
+    assert out.item() == (sa[0] * t).item()
+    assert out.item() != ((sa[0] * sb[0]) * torch.tensor(12.0)).item()
