@@ -16,6 +16,8 @@
 // (2 x 64 KB). LDS rows are 128 bytes; chunk c of row r is stored at chunk
 // position c ^ (r % 8) ^ ((r / 8) % 2), so the 16 rows a 16-lane group
 // reads with one ds_read_b128 fall in 16 distinct 16-byte bank groups.
+#include <stdlib.h>
+
 #include "jo_device.hpp"
 #include "jo_host.hpp"
 
@@ -165,10 +167,215 @@ __global__ __launch_bounds__(kBlock, 1) void fp8_gemm_kernel(const GemmArgs g) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined kernel (K % 64 == 0): NW waves on a 256x256 tile, in a 2 x NW/2
+// grid of 128 x (512/NW) wave tiles (NW = 8: two waves per SIMD, so one
+// wave's barrier and LDS waits overlap the other's MFMAs; NW = 4: one wave
+// per SIMD with 128x128 tiles and half the LDS reads per MFMA). K advances in
+// 64-byte stages through a ring of four LDS stages (4 x 32 KB) filled by
+// direct global->LDS loads issued four stages ahead, and each wave holds the
+// next stage's fragments in a second register set while the current stage's
+// MFMAs run. LDS rows are 64 bytes; chunk c of row r sits at chunk position
+// c ^ ((r >> 2) & 3). gfx950's LDS serves a ds_read_b128 sixteen lanes per
+// cycle from 64 four-byte banks: the sixteen consecutive rows a 16-lane group
+// reads then fall in sixteen distinct 16-byte bank groups (rocprofv3
+// SQ_LDS_BANK_CONFLICT reads 0 for this layout, 2.0e7 for an XOR with
+// ((r >> 1) ^ (r >> 3)) & 3, 6.1e7 unswizzled, on the 3120x16384x4096 GEMM).
+// ---------------------------------------------------------------------------
+constexpr int kPBK = 64;                          // bytes of K per stage
+constexpr int kPStages = 4;                       // LDS ring depth
+constexpr int kPStageBytes = (kBM + kBN) * kPBK;  // 32 KB
+
+__device__ __forceinline__ int pswz(int r) { return (r >> 2) & 3; }
+
+// s_waitcnt with only the vector-memory counter limited to n (n < 64).
+#define JO_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
+
+template <class OutTag, int NW>
+__device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
+  constexpr int J = NW == 8 ? 2 : 4;             // n-subtiles of 32 per wave
+  constexpr int WCOLS = J * 32;                  // wave tile columns
+  constexpr int LPW = kBM * kPBK / 1024 / NW;    // 1 KB direct loads per wave per stage (each of A, B)
+  static_assert(NW == 4 || NW == 8, "wave count");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kPStages * kPStageBytes];
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+
+  // Direct loads: wave instruction i covers tile rows (wave*LPW + i)*16 .. +16;
+  // lane p fills row +p/4, chunk position p%4 with the global chunk that
+  // belongs there. Rows beyond M (N) read row M-1 (N-1); they are never stored.
+  const uint8_t* ga[LPW];
+  const uint8_t* gb[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int r = (wave * LPW + i) * 16 + lane / 4;
+    const int c = (lane & 3) ^ pswz(r);
+    ga[i] = g.a + static_cast<int64_t>(min(m0 + r, g.M - 1)) * g.lda + c * 16;
+    gb[i] = g.b + static_cast<int64_t>(min(n0 + r, g.N - 1)) * g.ldb + c * 16;
+  }
+  const int stages = g.K / kPBK;
+  auto issue = [&](int s) {
+    uint8_t* base = smem + (s % kPStages) * kPStageBytes;
+    const int kb = s * kPBK;
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int row_blk = (wave * LPW + i) * 1024;
+      __builtin_amdgcn_global_load_lds(ga[i] + kb, (__attribute__((address_space(3))) void*)(base + row_blk), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(gb[i] + kb, (__attribute__((address_space(3))) void*)(base + kBM * kPBK + row_blk), 16, 0, 0);
+    }
+  };
+
+  f32x16 acc[4][J];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int fr = lane & 31, fh = lane >> 5;
+  // LDS byte offsets of this lane's fragment chunks (same in every stage).
+  int offa[4][2], offb[J][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = wm * 128 + i * 32 + fr;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) offa[i][h] = r * kPBK + (((fh * 2 + h) ^ pswz(r)) << 4);
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int r = wn * WCOLS + j * 32 + fr;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) offb[j][h] = kBM * kPBK + r * kPBK + (((fh * 2 + h) ^ pswz(r)) << 4);
+  }
+
+  auto read_frags = [&](int s, i32x8 (&af)[4], i32x8 (&bf)[J]) {
+    const uint8_t* st = smem + (s % kPStages) * kPStageBytes;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(st + offb[j][0]);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(st + offb[j][1]);
+      bf[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(st + offa[i][0]);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(st + offa[i][1]);
+      af[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    }
+  };
+  // Wait for this wave's loads of the stage being synced (with `later`
+  // younger stages still allowed in flight), then meet the other waves: that
+  // stage is complete in LDS, and every wave has finished reading the stage
+  // before it. A bare s_barrier: a fenced barrier would also wait for the
+  // loads of the later stages.
+  auto sync_stage = [&](int later) {
+    if (later >= 3)
+      JO_WAIT_VM(3 * 2 * LPW);
+    else if (later == 2)
+      JO_WAIT_VM(2 * 2 * LPW);
+    else if (later == 1)
+      JO_WAIT_VM(2 * LPW);
+    else
+      JO_WAIT_VM(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // Software pipeline: the fragments of stage s are in registers while its
+  // MFMAs run; halfway through, the wave syncs on stage s+1, refills the
+  // ring slot of stage s (read by every wave by then) with stage s+4, and
+  // reads stage s+1's fragments into the other register set, so LDS and
+  // HBM latency overlap the second half of the MFMAs.
+  for (int s = 0; s < kPStages && s < stages; ++s) issue(s);
+  sync_stage(min(stages - 1, kPStages - 1));
+  i32x8 af0[4], bf0[J], af1[4], bf1[J];
+  read_frags(0, af0, bf0);
+  // B first: the accumulator is the transposed tile, so a lane holds one
+  // output row (m = lane % 32 of the subtile) and, per group of four
+  // registers, four consecutive columns — stored as one 8-byte chunk.
+  auto stage = [&](int s, i32x8 (&af)[4], i32x8 (&bf)[J], i32x8 (&an)[4], i32x8 (&bn)[J]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < J; ++j) acc[i][j] = mfma32(bf[j], af[i], acc[i][j]);
+    if (s + 1 < stages) {
+      sync_stage(min(stages - 2 - s, kPStages - 2));
+      if (s + kPStages < stages) issue(s + kPStages);
+      read_frags(s + 1, an, bn);
+    }
+#pragma unroll
+    for (int i = 2; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < J; ++j) acc[i][j] = mfma32(bf[j], af[i], acc[i][j]);
+  };
+  for (int s = 0; s < stages; s += 2) {
+    stage(s, af0, bf0, af1, bf1);
+    if (s + 1 < stages) stage(s + 1, af1, bf1, af0, bf0);
+  }
+
+  // Epilogue: subtile (i, j) element e of a lane is row
+  // m = m0 + wm*128 + i*32 + lane%32, column n = n0 + wn*WCOLS + j*32 +
+  // (e/4)*8 + (lane/32)*4 + e%4.
+  float sam[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sam[i] = g.sa[min(m0 + wm * 128 + i * 32 + fr, g.M - 1)];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n0 + wn * WCOLS + j * 32 + q * 8 + fh * 4;  // N % 8 == 0: n < N covers n..n+3
+      if (n >= g.N) continue;
+      const u32x4 sbv = ld16(g.sb + n);
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (g.bias) {
+        const u32x2 braw = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(g.bias) + n);
+        const u32x4 b4{braw.x, braw.y, 0u, 0u};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bv[t] = elem<OutTag>(b4, t);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = m0 + wm * 128 + i * 32 + fr;
+        if (m >= g.M) continue;
+        float o[8];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float tt = acc[i][j][q * 4 + t] * elem<F32>(sbv, t);
+          o[t] = __builtin_fmaf(sam[i], tt, bv[t]);
+          o[t + 4] = 0.f;
+        }
+        const u32x4 pk = pack<OutTag>(o);
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(g.out) + static_cast<int64_t>(m) * g.ldo + n) =
+            u32x2{pk.x, pk.y};
+      }
+    }
+  }
+}
+
+// The body lives in a device function: with the lambdas above directly in a
+// kernel template over NW, the host compiler emits no launch stub for it.
+template <class OutTag, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void fp8_gemm_pipe_kernel(const GemmArgs g) {
+  fp8_gemm_pipe_body<OutTag, NW>(g);
+}
+
 template <class OutTag>
 int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   const dim3 grid((g.N + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
-  hipLaunchKernelGGL((fp8_gemm_kernel<OutTag>), grid, dim3(kBlock), 0, stream, g);
+  const bool pipe_ok = g.K % kPBK == 0 && aligned(g.sb, 16) && (g.bias == nullptr || aligned(g.bias, 8));
+  const char* w = getenv("JO_GEMM_WAVES");
+  const int waves = w ? atoi(w) : 8;
+  if (pipe_ok && waves == 4)
+    hipLaunchKernelGGL((fp8_gemm_pipe_kernel<OutTag, 4>), grid, dim3(256), 0, stream, g);
+  else if (pipe_ok && waves == 8)
+    hipLaunchKernelGGL((fp8_gemm_pipe_kernel<OutTag, 8>), grid, dim3(512), 0, stream, g);
+  else
+    hipLaunchKernelGGL((fp8_gemm_kernel<OutTag>), grid, dim3(kBlock), 0, stream, g);
   return launch_status("fp8_scaled_mm");
 }
 
