@@ -182,50 +182,54 @@ __global__ __launch_bounds__(kBlock, 1) void fp8_gemm_kernel(const GemmArgs g) {
 // SQ_LDS_BANK_CONFLICT reads 0 for this layout, 2.0e7 for an XOR with
 // ((r >> 1) ^ (r >> 3)) & 3, 6.1e7 unswizzled, on the 3120x16384x4096 GEMM).
 // ---------------------------------------------------------------------------
-constexpr int kPBK = 64;                          // bytes of K per stage
-constexpr int kPStages = 4;                       // LDS ring depth
-constexpr int kPStageBytes = (kBM + kBN) * kPBK;  // 32 KB
+constexpr int kPBK = 64;  // bytes of K per stage
 
 __device__ __forceinline__ int pswz(int r) { return (r >> 2) & 3; }
 
 // s_waitcnt with only the vector-memory counter limited to n (n < 64).
 #define JO_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
 
-template <class OutTag, int NW>
+template <class OutTag, int BN, int NW, int NST>
 __device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
-  constexpr int J = NW == 8 ? 2 : 4;             // n-subtiles of 32 per wave
-  constexpr int WCOLS = J * 32;                  // wave tile columns
-  constexpr int LPW = kBM * kPBK / 1024 / NW;    // 1 KB direct loads per wave per stage (each of A, B)
-  static_assert(NW == 4 || NW == 8, "wave count");
+  constexpr int WCOLS = BN / (NW / 2);            // wave tile columns (2 x NW/2 waves)
+  constexpr int J = WCOLS / 32;                   // n-subtiles of 32 per wave
+  constexpr int LPA = kBM * kPBK / 1024 / NW;     // 1 KB direct loads per wave per stage: A
+  constexpr int LPB = BN * kPBK / 1024 / NW;      //                                       B
+  constexpr int kPStages = NST;                   // LDS ring depth
+  constexpr int kPStageBytes = (kBM + BN) * kPBK;
+  static_assert(J >= 1 && LPA >= 1 && LPB >= 1, "tile shape");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kPStages * kPStageBytes];
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wave = tid / kWave;
   const int wm = wave & 1, wn = wave >> 1;
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * BN;
 
-  // Direct loads: wave instruction i covers tile rows (wave*LPW + i)*16 .. +16;
+  // Direct loads: wave instruction i covers tile rows (wave*LP + i)*16 .. +16;
   // lane p fills row +p/4, chunk position p%4 with the global chunk that
   // belongs there. Rows beyond M (N) read row M-1 (N-1); they are never stored.
-  const uint8_t* ga[LPW];
-  const uint8_t* gb[LPW];
+  const uint8_t* ga[LPA];
+  const uint8_t* gb[LPB];
 #pragma unroll
-  for (int i = 0; i < LPW; ++i) {
-    const int r = (wave * LPW + i) * 16 + lane / 4;
-    const int c = (lane & 3) ^ pswz(r);
-    ga[i] = g.a + static_cast<int64_t>(min(m0 + r, g.M - 1)) * g.lda + c * 16;
-    gb[i] = g.b + static_cast<int64_t>(min(n0 + r, g.N - 1)) * g.ldb + c * 16;
+  for (int i = 0; i < LPA; ++i) {
+    const int r = (wave * LPA + i) * 16 + lane / 4;
+    ga[i] = g.a + static_cast<int64_t>(min(m0 + r, g.M - 1)) * g.lda + (((lane & 3) ^ pswz(r)) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < LPB; ++i) {
+    const int r = (wave * LPB + i) * 16 + lane / 4;
+    gb[i] = g.b + static_cast<int64_t>(min(n0 + r, g.N - 1)) * g.ldb + (((lane & 3) ^ pswz(r)) * 16);
   }
   const int stages = g.K / kPBK;
   auto issue = [&](int s) {
     uint8_t* base = smem + (s % kPStages) * kPStageBytes;
     const int kb = s * kPBK;
 #pragma unroll
-    for (int i = 0; i < LPW; ++i) {
-      const int row_blk = (wave * LPW + i) * 1024;
-      __builtin_amdgcn_global_load_lds(ga[i] + kb, (__attribute__((address_space(3))) void*)(base + row_blk), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(gb[i] + kb, (__attribute__((address_space(3))) void*)(base + kBM * kPBK + row_blk), 16, 0, 0);
-    }
+    for (int i = 0; i < LPA; ++i)
+      __builtin_amdgcn_global_load_lds(ga[i] + kb, (__attribute__((address_space(3))) void*)(base + (wave * LPA + i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < LPB; ++i)
+      __builtin_amdgcn_global_load_lds(gb[i] + kb, (__attribute__((address_space(3))) void*)(base + kBM * kPBK + (wave * LPB + i) * 1024), 16, 0, 0);
   };
 
   f32x16 acc[4][J];
@@ -273,12 +277,13 @@ __device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
   // before it. A bare s_barrier: a fenced barrier would also wait for the
   // loads of the later stages.
   auto sync_stage = [&](int later) {
+    constexpr int per = LPA + LPB;  // loads per wave per stage
     if (later >= 3)
-      JO_WAIT_VM(3 * 2 * LPW);
+      JO_WAIT_VM(3 * per);
     else if (later == 2)
-      JO_WAIT_VM(2 * 2 * LPW);
+      JO_WAIT_VM(2 * per);
     else if (later == 1)
-      JO_WAIT_VM(2 * LPW);
+      JO_WAIT_VM(per);
     else
       JO_WAIT_VM(0);
     asm volatile("" ::: "memory");
@@ -359,21 +364,28 @@ __device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
 
 // The body lives in a device function: with the lambdas above directly in a
 // kernel template over NW, the host compiler emits no launch stub for it.
-template <class OutTag, int NW>
-__global__ __launch_bounds__(NW * 64, 1) void fp8_gemm_pipe_kernel(const GemmArgs g) {
-  fp8_gemm_pipe_body<OutTag, NW>(g);
+template <class OutTag, int BN, int NW, int NST>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void fp8_gemm_pipe_kernel(const GemmArgs g) {
+  fp8_gemm_pipe_body<OutTag, BN, NW, NST>(g);
 }
 
 template <class OutTag>
 int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   const dim3 grid((g.N + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
   const bool pipe_ok = g.K % kPBK == 0 && aligned(g.sb, 16) && (g.bias == nullptr || aligned(g.bias, 8));
-  const char* w = getenv("JO_GEMM_WAVES");
-  const int waves = w ? atoi(w) : 8;
-  if (pipe_ok && waves == 4)
-    hipLaunchKernelGGL((fp8_gemm_pipe_kernel<OutTag, 4>), grid, dim3(256), 0, stream, g);
-  else if (pipe_ok && waves == 8)
-    hipLaunchKernelGGL((fp8_gemm_pipe_kernel<OutTag, 8>), grid, dim3(512), 0, stream, g);
+  // 256x128 tiles (two 4-wave workgroups per CU, whose barriers do not stall
+  // each other) measured faster at K = 4096 (3120x16384: 295 -> 284 us;
+  // 3120x12288: 241 -> 228 us); 256x256 tiles (8 waves, half the A re-reads)
+  // at K = 16384 (3120x4096: 250 -> 219 us). JO_GEMM_SHAPE=0|1|2 forces
+  // 256x256, 256x128 or the register-staged kernel (results are the same up
+  // to the fp32 accumulation order inside the matrix cores).
+  const char* w = getenv("JO_GEMM_SHAPE");
+  const int shape = w ? atoi(w) : (g.K <= 8192 ? 1 : 0);
+  if (pipe_ok && shape == 1)
+    hipLaunchKernelGGL((fp8_gemm_pipe_kernel<OutTag, 128, 4, 3>), dim3((g.N + 127) / 128, grid.y),
+                       dim3(256), 0, stream, g);
+  else if (pipe_ok && shape == 0)
+    hipLaunchKernelGGL((fp8_gemm_pipe_kernel<OutTag, 256, 8, 4>), grid, dim3(512), 0, stream, g);
   else
     hipLaunchKernelGGL((fp8_gemm_kernel<OutTag>), grid, dim3(kBlock), 0, stream, g);
   return launch_status("fp8_scaled_mm");

@@ -18,6 +18,15 @@ from oracle import ops
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(params=["auto", "0", "1", "2"], autouse=True)
+def gemm_shape(request, monkeypatch):
+    """Every kernel variant: the default choice, 256x256 (8 waves), 256x128
+    (4 waves) and the register-staged kernel (also the K % 64 != 0 path)."""
+    if request.param != "auto":
+        monkeypatch.setenv("JO_GEMM_SHAPE", request.param)
+    return request.param
+
+
 def ulp(x, dtype):
     frac = 7 if dtype == torch.bfloat16 else 10
     e = torch.floor(torch.log2(x.abs().clamp_min(2.0 ** -14)))
