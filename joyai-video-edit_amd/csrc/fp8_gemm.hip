@@ -325,39 +325,64 @@ __device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
 
   // Epilogue: subtile (i, j) element e of a lane is row
   // m = m0 + wm*128 + i*32 + lane%32, column n = n0 + wn*WCOLS + j*32 +
-  // (e/4)*8 + (lane/32)*4 + e%4.
+  // (e/4)*8 + (lane/32)*4 + e%4. The finished values go through LDS (free
+  // after the K loop) one 128-row half at a time, so that every row leaves
+  // as whole lines of 16-byte lane stores: stored straight from the MFMA
+  // layout (8 bytes per lane, 32 rows per wave store) the lines were written
+  // back part-filled, measured 2.4-4.5x the output bytes in WRITE_SIZE.
+  constexpr int kRowBytes = BN * 2 + 16;  // padded LDS row: 8-byte writes of 32 rows spread over the banks
+  static_assert(128 * kRowBytes <= kPStages * kPStageBytes, "epilogue staging fits the ring");
   float sam[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) sam[i] = g.sa[min(m0 + wm * 128 + i * 32 + fr, g.M - 1)];
+  float sbq[J][4][4], bq[J][4][4];
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
+  for (int j = 0; j < J; ++j)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int n = n0 + wn * WCOLS + j * 32 + q * 8 + fh * 4;  // N % 8 == 0: n < N covers n..n+3
-      if (n >= g.N) continue;
+      const int n = min(n0 + wn * WCOLS + j * 32 + q * 8 + fh * 4, g.N - 4);  // N % 8 == 0
       const u32x4 sbv = ld16(g.sb + n);
-      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      u32x4 b4{0u, 0u, 0u, 0u};
       if (g.bias) {
         const u32x2 braw = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(g.bias) + n);
-        const u32x4 b4{braw.x, braw.y, 0u, 0u};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) bv[t] = elem<OutTag>(b4, t);
+        b4 = u32x4{braw.x, braw.y, 0u, 0u};
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = m0 + wm * 128 + i * 32 + fr;
-        if (m >= g.M) continue;
-        float o[8];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float tt = acc[i][j][q * 4 + t] * elem<F32>(sbv, t);
-          o[t] = __builtin_fmaf(sam[i], tt, bv[t]);
-          o[t + 4] = 0.f;
-        }
-        const u32x4 pk = pack<OutTag>(o);
-        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(g.out) + static_cast<int64_t>(m) * g.ldo + n) =
-            u32x2{pk.x, pk.y};
+      for (int t = 0; t < 4; ++t) {
+        sbq[j][q][t] = elem<F32>(sbv, t);
+        bq[j][q][t] = g.bias ? elem<OutTag>(b4, t) : 0.f;
       }
+    }
+  constexpr int kT = NW * 64;
+  constexpr int kChunksPerRow = BN * 2 / 16;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    __syncthreads();  // the ring (or the previous half) is no longer read
+    if (wm == half) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float o[8];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              o[t] = __builtin_fmaf(sam[i], acc[i][j][q * 4 + t] * sbq[j][q][t], bq[j][q][t]);
+              o[t + 4] = 0.f;
+            }
+            const u32x4 pk = pack<OutTag>(o);
+            const int rl = i * 32 + fr, cl = wn * WCOLS + j * 32 + q * 8 + fh * 4;
+            *reinterpret_cast<u32x2*>(smem + rl * kRowBytes + cl * 2) = u32x2{pk.x, pk.y};
+          }
+    }
+    __syncthreads();
+    for (int c = tid; c < 128 * kChunksPerRow; c += kT) {
+      const int rl = c / kChunksPerRow, ch = c % kChunksPerRow;
+      const int m = m0 + half * 128 + rl, n = n0 + ch * 8;
+      if (m < g.M && n < g.N)
+        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(g.out) + static_cast<int64_t>(m) * g.ldo + n) =
+            *reinterpret_cast<const u32x4*>(smem + rl * kRowBytes + ch * 16);
     }
   }
 }
