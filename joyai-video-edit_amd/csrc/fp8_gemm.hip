@@ -168,12 +168,12 @@ __global__ __launch_bounds__(kBlock, 1) void fp8_gemm_kernel(const GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
-// Pipelined kernel (K % 64 == 0): NW waves on a 256x256 tile, in a 2 x NW/2
-// grid of 128 x (512/NW) wave tiles (NW = 8: two waves per SIMD, so one
-// wave's barrier and LDS waits overlap the other's MFMAs; NW = 4: one wave
-// per SIMD with 128x128 tiles and half the LDS reads per MFMA). K advances in
-// 64-byte stages through a ring of four LDS stages (4 x 32 KB) filled by
-// direct global->LDS loads issued four stages ahead, and each wave holds the
+// Pipelined kernel (K % 64 == 0): NW waves on a BM x BN tile (BM 256 or 224),
+// in a 2 x NW/2 grid of wave tiles 128 (or 96, the second row of a 224-row
+// tile) x 2*BN/NW (NW = 8: two waves per SIMD, so one wave's barrier and LDS
+// waits overlap the other's MFMAs). K advances in 64-byte stages through a
+// ring of NST LDS stages of (BM + BN) x 64 bytes filled by direct
+// global->LDS loads issued NST stages ahead, and each wave holds the
 // next stage's fragments in a second register set while the current stage's
 // MFMAs run. LDS rows are 64 bytes; chunk c of row r sits at chunk position
 // c ^ ((r >> 2) & 3). gfx950's LDS serves a ds_read_b128 sixteen lanes per
@@ -189,52 +189,56 @@ __device__ __forceinline__ int pswz(int r) { return (r >> 2) & 3; }
 // s_waitcnt with only the vector-memory counter limited to n (n < 64).
 #define JO_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
 
-template <class OutTag, int BN, int NW, int NST>
-__device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
-  constexpr int WCOLS = BN / (NW / 2);            // wave tile columns (2 x NW/2 waves)
-  constexpr int J = WCOLS / 32;                   // n-subtiles of 32 per wave
-  constexpr int LPA = kBM * kPBK / 1024 / NW;     // 1 KB direct loads per wave per stage: A
-  constexpr int LPB = BN * kPBK / 1024 / NW;      //                                       B
-  constexpr int kPStages = NST;                   // LDS ring depth
-  constexpr int kPStageBytes = (kBM + BN) * kPBK;
-  static_assert(J >= 1 && LPA >= 1 && LPB >= 1, "tile shape");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kPStages * kPStageBytes];
+template <int PER>
+__device__ __forceinline__ void wait_loads(int later) {
+  if (later >= 3)
+    JO_WAIT_VM(3 * PER);
+  else if (later == 2)
+    JO_WAIT_VM(2 * PER);
+  else if (later == 1)
+    JO_WAIT_VM(PER);
+  else
+    JO_WAIT_VM(0);
+}
+
+// Direct loads of one stage: BM rows of A then BN rows of B^T, 64 bytes each,
+// written by (BM + BN) / 16 wave instructions of 1 KB (16 rows, four lanes per
+// row); slot L fills stage bytes L * 1024 .. +1024 and belongs to wave L % NW.
+template <int BM, int BN, int NW>
+struct PipeLoads {
+  static constexpr int kSlots = (BM + BN) / 16;
+  static constexpr int kPerWave = (kSlots + NW - 1) / NW;
+  static constexpr bool kEven = kSlots % NW == 0;
+  const uint8_t* src[kPerWave];  // this lane's 16-byte chunk of each slot at K offset 0
+  bool last;                     // the wave owns a slot kPerWave - 1 (always when kEven)
+};
+
+// One output tile's K loop and epilogue for a wave holding MI row blocks of 32
+// (rows wm*128 .. wm*128 + 32*MI - 1 of the tile) and WCOLS columns.
+template <class OutTag, int BM, int BN, int NW, int NST, int MI>
+__device__ __forceinline__ void fp8_gemm_pipe_tile(const GemmArgs& g, uint8_t* smem,
+                                                   const PipeLoads<BM, BN, NW>& ld, int wave,
+                                                   int wm, int wn, int m0, int n0) {
+  using Loads = PipeLoads<BM, BN, NW>;
+  constexpr int WCOLS = BN / (NW / 2);  // wave tile columns
+  constexpr int J = WCOLS / 32;         // n-subtiles of 32 per wave
+  constexpr int kStage = (BM + BN) * kPBK;
+  static_assert(J >= 1 && MI >= 2 && MI <= 4, "tile shape");
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
-  const int wave = tid / kWave;
-  const int wm = wave & 1, wn = wave >> 1;
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * BN;
-
-  // Direct loads: wave instruction i covers tile rows (wave*LP + i)*16 .. +16;
-  // lane p fills row +p/4, chunk position p%4 with the global chunk that
-  // belongs there. Rows beyond M (N) read row M-1 (N-1); they are never stored.
-  const uint8_t* ga[LPA];
-  const uint8_t* gb[LPB];
-#pragma unroll
-  for (int i = 0; i < LPA; ++i) {
-    const int r = (wave * LPA + i) * 16 + lane / 4;
-    ga[i] = g.a + static_cast<int64_t>(min(m0 + r, g.M - 1)) * g.lda + (((lane & 3) ^ pswz(r)) * 16);
-  }
-#pragma unroll
-  for (int i = 0; i < LPB; ++i) {
-    const int r = (wave * LPB + i) * 16 + lane / 4;
-    gb[i] = g.b + static_cast<int64_t>(min(n0 + r, g.N - 1)) * g.ldb + (((lane & 3) ^ pswz(r)) * 16);
-  }
   const int stages = g.K / kPBK;
   auto issue = [&](int s) {
-    uint8_t* base = smem + (s % kPStages) * kPStageBytes;
+    uint8_t* base = smem + (s % NST) * kStage;
     const int kb = s * kPBK;
 #pragma unroll
-    for (int i = 0; i < LPA; ++i)
-      __builtin_amdgcn_global_load_lds(ga[i] + kb, (__attribute__((address_space(3))) void*)(base + (wave * LPA + i) * 1024), 16, 0, 0);
-#pragma unroll
-    for (int i = 0; i < LPB; ++i)
-      __builtin_amdgcn_global_load_lds(gb[i] + kb, (__attribute__((address_space(3))) void*)(base + kBM * kPBK + (wave * LPB + i) * 1024), 16, 0, 0);
+    for (int i = 0; i < Loads::kPerWave; ++i)
+      if (Loads::kEven || i + 1 < Loads::kPerWave || ld.last)
+        __builtin_amdgcn_global_load_lds(ld.src[i] + kb, (__attribute__((address_space(3))) void*)(base + (wave + i * NW) * 1024), 16, 0, 0);
   };
 
-  f32x16 acc[4][J];
+  f32x16 acc[MI][J];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < J; ++j)
 #pragma unroll
@@ -242,9 +246,9 @@ __device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
 
   const int fr = lane & 31, fh = lane >> 5;
   // LDS byte offsets of this lane's fragment chunks (same in every stage).
-  int offa[4][2], offb[J][2];
+  int offa[MI][2], offb[J][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < MI; ++i) {
     const int r = wm * 128 + i * 32 + fr;
 #pragma unroll
     for (int h = 0; h < 2; ++h) offa[i][h] = r * kPBK + (((fh * 2 + h) ^ pswz(r)) << 4);
@@ -253,11 +257,11 @@ __device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
   for (int j = 0; j < J; ++j) {
     const int r = wn * WCOLS + j * 32 + fr;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) offb[j][h] = kBM * kPBK + r * kPBK + (((fh * 2 + h) ^ pswz(r)) << 4);
+    for (int h = 0; h < 2; ++h) offb[j][h] = BM * kPBK + r * kPBK + (((fh * 2 + h) ^ pswz(r)) << 4);
   }
 
-  auto read_frags = [&](int s, i32x8 (&af)[4], i32x8 (&bf)[J]) {
-    const uint8_t* st = smem + (s % kPStages) * kPStageBytes;
+  auto read_frags = [&](int s, i32x8 (&af)[MI], i32x8 (&bf)[J]) {
+    const uint8_t* st = smem + (s % NST) * kStage;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const u32x4 lo = *reinterpret_cast<const u32x4*>(st + offb[j][0]);
@@ -265,7 +269,7 @@ __device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
       bf[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < MI; ++i) {
       const u32x4 lo = *reinterpret_cast<const u32x4*>(st + offa[i][0]);
       const u32x4 hi = *reinterpret_cast<const u32x4*>(st + offa[i][1]);
       af[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
@@ -277,44 +281,39 @@ __device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
   // before it. A bare s_barrier: a fenced barrier would also wait for the
   // loads of the later stages.
   auto sync_stage = [&](int later) {
-    constexpr int per = LPA + LPB;  // loads per wave per stage
-    if (later >= 3)
-      JO_WAIT_VM(3 * per);
-    else if (later == 2)
-      JO_WAIT_VM(2 * per);
-    else if (later == 1)
-      JO_WAIT_VM(per);
+    if (Loads::kEven || ld.last)
+      wait_loads<Loads::kPerWave>(later);
     else
-      JO_WAIT_VM(0);
+      wait_loads<Loads::kPerWave - 1>(later);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
 
   // Software pipeline: the fragments of stage s are in registers while its
-  // MFMAs run; halfway through, the wave syncs on stage s+1, refills the
-  // ring slot of stage s (read by every wave by then) with stage s+4, and
-  // reads stage s+1's fragments into the other register set, so LDS and
-  // HBM latency overlap the second half of the MFMAs.
-  for (int s = 0; s < kPStages && s < stages; ++s) issue(s);
-  sync_stage(min(stages - 1, kPStages - 1));
-  i32x8 af0[4], bf0[J], af1[4], bf1[J];
+  // MFMAs run; after the first two row blocks, the wave syncs on stage s+1,
+  // refills the ring slot of stage s (read by every wave by then) with stage
+  // s+NST, and reads stage s+1's fragments into the other register set, so
+  // LDS and HBM latency overlap the remaining MFMAs.
+  for (int s = 0; s < NST && s < stages; ++s) issue(s);
+  sync_stage(min(stages - 1, NST - 1));
+  i32x8 af0[MI], bf0[J], af1[MI], bf1[J];
   read_frags(0, af0, bf0);
   // B first: the accumulator is the transposed tile, so a lane holds one
   // output row (m = lane % 32 of the subtile) and, per group of four
   // registers, four consecutive columns — stored as one 8-byte chunk.
-  auto stage = [&](int s, i32x8 (&af)[4], i32x8 (&bf)[J], i32x8 (&an)[4], i32x8 (&bn)[J]) {
+  auto stage = [&](int s, i32x8 (&af)[MI], i32x8 (&bf)[J], i32x8 (&an)[MI], i32x8 (&bn)[J]) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < J; ++j) acc[i][j] = mfma32(bf[j], af[i], acc[i][j]);
     if (s + 1 < stages) {
-      sync_stage(min(stages - 2 - s, kPStages - 2));
-      if (s + kPStages < stages) issue(s + kPStages);
+      sync_stage(min(stages - 2 - s, NST - 2));
+      if (s + NST < stages) issue(s + NST);
       read_frags(s + 1, an, bn);
     }
 #pragma unroll
-    for (int i = 2; i < 4; ++i)
+    for (int i = 2; i < MI; ++i)
 #pragma unroll
       for (int j = 0; j < J; ++j) acc[i][j] = mfma32(bf[j], af[i], acc[i][j]);
   };
@@ -331,10 +330,10 @@ __device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
   // layout (8 bytes per lane, 32 rows per wave store) the lines were written
   // back part-filled, measured 2.4-4.5x the output bytes in WRITE_SIZE.
   constexpr int kRowBytes = BN * 2 + 16;  // padded LDS row: 8-byte writes of 32 rows spread over the banks
-  static_assert(128 * kRowBytes <= kPStages * kPStageBytes, "epilogue staging fits the ring");
-  float sam[4];
+  static_assert(128 * kRowBytes <= NST * kStage, "epilogue staging fits the ring");
+  float sam[MI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sam[i] = g.sa[min(m0 + wm * 128 + i * 32 + fr, g.M - 1)];
+  for (int i = 0; i < MI; ++i) sam[i] = g.sa[min(m0 + wm * 128 + i * 32 + fr, g.M - 1)];
   float sbq[J][4][4], bq[J][4][4];
 #pragma unroll
   for (int j = 0; j < J; ++j)
@@ -360,7 +359,7 @@ __device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
     __syncthreads();  // the ring (or the previous half) is no longer read
     if (wm == half) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < J; ++j)
 #pragma unroll
@@ -377,7 +376,8 @@ __device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
           }
     }
     __syncthreads();
-    for (int c = tid; c < 128 * kChunksPerRow; c += kT) {
+    const int rows = half == 0 ? 128 : BM - 128;
+    for (int c = tid; c < rows * kChunksPerRow; c += kT) {
       const int rl = c / kChunksPerRow, ch = c % kChunksPerRow;
       const int m = m0 + half * 128 + rl, n = n0 + ch * 8;
       if (m < g.M && n < g.N)
@@ -387,30 +387,103 @@ __device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
   }
 }
 
+template <class OutTag, int BM, int BN, int NW, int NST>
+__device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
+  using Loads = PipeLoads<BM, BN, NW>;
+  static_assert(BM == 256 || BM == 224, "tile rows");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * (BM + BN) * kPBK];
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  // BM = 256: a 2 x NW/2 grid of 128 x WCOLS wave tiles (even waves rows
+  // 0-127, odd waves rows 128-255). BM = 224: waves 0 .. NW/2-1 take rows
+  // 0-127 (four row blocks), the others rows 128-223 (three): a workgroup's
+  // waves are spread round-robin over the CU's four SIMDs, so with NW = 8
+  // each SIMD runs one wave of each kind, 7 row blocks where a 256-row tile
+  // gives it 8.
+  const int wm = BM == 256 ? (wave & 1) : wave / (NW / 2);
+  const int wn = BM == 256 ? (wave >> 1) : wave % (NW / 2);
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+  // Lane p of a slot fills row +p/4, chunk position p%4 with the global chunk
+  // that belongs there. Rows beyond M (N) read row M-1 (N-1); they are never
+  // stored.
+  Loads ld;
+#pragma unroll
+  for (int i = 0; i < Loads::kPerWave; ++i) {
+    const int slot = wave + i * NW;
+    const bool is_a = slot < BM / 16;
+    const int r = (is_a ? slot : slot - BM / 16) * 16 + lane / 4;
+    const uint8_t* row = is_a ? g.a + static_cast<int64_t>(min(m0 + r, g.M - 1)) * g.lda
+                              : g.b + static_cast<int64_t>(min(n0 + r, g.N - 1)) * g.ldb;
+    ld.src[i] = row + (((lane & 3) ^ pswz(r)) * 16);
+  }
+  ld.last = Loads::kEven || wave + (Loads::kPerWave - 1) * NW < Loads::kSlots;
+  if constexpr (BM == 256) {
+    fp8_gemm_pipe_tile<OutTag, BM, BN, NW, NST, 4>(g, smem, ld, wave, wm, wn, m0, n0);
+  } else {
+    if (wm == 0)
+      fp8_gemm_pipe_tile<OutTag, BM, BN, NW, NST, 4>(g, smem, ld, wave, wm, wn, m0, n0);
+    else
+      fp8_gemm_pipe_tile<OutTag, BM, BN, NW, NST, 3>(g, smem, ld, wave, wm, wn, m0, n0);
+  }
+}
+
 // The body lives in a device function: with the lambdas above directly in a
 // kernel template over NW, the host compiler emits no launch stub for it.
-template <class OutTag, int BN, int NW, int NST>
+template <class OutTag, int BM, int BN, int NW, int NST>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void fp8_gemm_pipe_kernel(const GemmArgs g) {
-  fp8_gemm_pipe_body<OutTag, BN, NW, NST>(g);
+  fp8_gemm_pipe_body<OutTag, BM, BN, NW, NST>(g);
+}
+
+template <class OutTag, int BM, int BN, int NW, int NST>
+void launch_pipe(const GemmArgs& g, hipStream_t stream) {
+  hipLaunchKernelGGL((fp8_gemm_pipe_kernel<OutTag, BM, BN, NW, NST>),
+                     dim3((g.N + BN - 1) / BN, (g.M + BM - 1) / BM), dim3(NW * 64), 0, stream, g);
+}
+
+int cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cached[dev];
+}
+
+// Tile rows for the 8-wave x 256-column kernel: one workgroup per CU, so the
+// time is about (rounds of workgroups over the CUs) x (row blocks per SIMD),
+// 8 for a 256-row tile and 7 for a 224-row one. At M = 3120 (13 tiles of 256,
+// 14 of 224) every deployment shape needs the same number of rounds with
+// either height, and 224-row tiles measured 3120x12288x4096 185 -> 180 us,
+// 3120x16384x4096 233 -> 224 us, 3120x4096x16384 198 -> 193 us.
+int pick_tile_rows(int M, int N) {
+  const int64_t cus = cu_count(), cols = (N + 255) / 256;
+  auto cost = [&](int64_t bm) { return ((M + bm - 1) / bm * cols + cus - 1) / cus * (bm / 32); };
+  return cost(224) < cost(256) ? 224 : 256;
 }
 
 template <class OutTag>
 int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   const dim3 grid((g.N + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
   const bool pipe_ok = g.K % kPBK == 0 && aligned(g.sb, 16) && (g.bias == nullptr || aligned(g.bias, 8));
-  // 256x128 tiles (two 4-wave workgroups per CU, whose barriers do not stall
-  // each other) measured faster at K = 4096 (3120x16384: 295 -> 284 us;
-  // 3120x12288: 241 -> 228 us); 256x256 tiles (8 waves, half the A re-reads)
-  // at K = 16384 (3120x4096: 250 -> 219 us). JO_GEMM_SHAPE=0|1|2 forces
-  // 256x256, 256x128 or the register-staged kernel (results are the same up
-  // to the fp32 accumulation order inside the matrix cores).
+  // 8-wave 256-column tiles measured faster than two 4-wave 128-column
+  // workgroups per CU at every deployment shape (3120x12288x4096: 199 -> 185
+  // us, 3120x16384x4096: 257 -> 233 us). JO_GEMM_SHAPE=0|1|2|3|4 forces
+  // 256x256, 256x128, the register-staged kernel, 224x256 or 224x128 (results
+  // are the same up to the fp32 accumulation order inside the matrix cores).
   const char* w = getenv("JO_GEMM_SHAPE");
-  const int shape = w ? atoi(w) : (g.K <= 8192 ? 1 : 0);
+  const int shape = w ? atoi(w) : (pick_tile_rows(g.M, g.N) == 224 ? 3 : 0);
   if (pipe_ok && shape == 1)
-    hipLaunchKernelGGL((fp8_gemm_pipe_kernel<OutTag, 128, 4, 3>), dim3((g.N + 127) / 128, grid.y),
-                       dim3(256), 0, stream, g);
+    launch_pipe<OutTag, 256, 128, 4, 3>(g, stream);
   else if (pipe_ok && shape == 0)
-    hipLaunchKernelGGL((fp8_gemm_pipe_kernel<OutTag, 256, 8, 4>), grid, dim3(512), 0, stream, g);
+    launch_pipe<OutTag, 256, 256, 8, 4>(g, stream);
+  else if (pipe_ok && shape == 3)
+    launch_pipe<OutTag, 224, 256, 8, 4>(g, stream);
+  else if (pipe_ok && shape == 4)
+    launch_pipe<OutTag, 224, 128, 4, 3>(g, stream);
   else
     hipLaunchKernelGGL((fp8_gemm_kernel<OutTag>), grid, dim3(kBlock), 0, stream, g);
   return launch_status("fp8_scaled_mm");

@@ -18,10 +18,11 @@ from oracle import ops
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["auto", "0", "1", "2"], autouse=True)
+@pytest.fixture(params=["auto", "0", "1", "2", "3", "4"], autouse=True)
 def gemm_shape(request, monkeypatch):
     """Every kernel variant: the default choice, 256x256 (8 waves), 256x128
-    (4 waves) and the register-staged kernel (also the K % 64 != 0 path)."""
+    (4 waves), the register-staged kernel (also the K % 64 != 0 path), 224x256
+    (8 waves, 4 and 3 row blocks) and 224x128 (4 waves)."""
     if request.param != "auto":
         monkeypatch.setenv("JO_GEMM_SHAPE", request.param)
     return request.param
