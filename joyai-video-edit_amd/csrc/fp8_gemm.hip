@@ -186,19 +186,20 @@ constexpr int kPBK = 64;  // bytes of K per stage
 
 __device__ __forceinline__ int pswz(int r) { return (r >> 2) & 3; }
 
-// s_waitcnt with only the vector-memory counter limited to n (n < 64).
-#define JO_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
+// s_waitcnt limiting the vector-memory counter to n (n < 64) and the LDS
+// counter to 0.
+#define JO_WAIT_VM_LDS0(n) __builtin_amdgcn_s_waitcnt(0x0070 | ((n) & 15) | (((n) >> 4) << 14))
 
 template <int PER>
 __device__ __forceinline__ void wait_loads(int later) {
   if (later >= 3)
-    JO_WAIT_VM(3 * PER);
+    JO_WAIT_VM_LDS0(3 * PER);
   else if (later == 2)
-    JO_WAIT_VM(2 * PER);
+    JO_WAIT_VM_LDS0(2 * PER);
   else if (later == 1)
-    JO_WAIT_VM(PER);
+    JO_WAIT_VM_LDS0(PER);
   else
-    JO_WAIT_VM(0);
+    JO_WAIT_VM_LDS0(0);
 }
 
 // Direct loads of one stage: BM rows of A then BN rows of B^T, 64 bytes each,
@@ -276,10 +277,10 @@ __device__ __forceinline__ void fp8_gemm_pipe_tile(const GemmArgs& g, uint8_t* s
     }
   };
   // Wait for this wave's loads of the stage being synced (with `later`
-  // younger stages still allowed in flight), then meet the other waves: that
-  // stage is complete in LDS, and every wave has finished reading the stage
-  // before it. A bare s_barrier: a fenced barrier would also wait for the
-  // loads of the later stages.
+  // younger stages still allowed in flight) and its LDS reads, then meet the
+  // other waves: that stage is complete in LDS, and every wave has finished
+  // reading the stage before it. A bare s_barrier: a fenced barrier would
+  // also wait for the loads of the later stages.
   auto sync_stage = [&](int later) {
     if (Loads::kEven || ld.last)
       wait_loads<Loads::kPerWave>(later);
@@ -290,11 +291,12 @@ __device__ __forceinline__ void fp8_gemm_pipe_tile(const GemmArgs& g, uint8_t* s
     asm volatile("" ::: "memory");
   };
 
-  // Software pipeline: the fragments of stage s are in registers while its
-  // MFMAs run; after the first two row blocks, the wave syncs on stage s+1,
-  // refills the ring slot of stage s (read by every wave by then) with stage
-  // s+NST, and reads stage s+1's fragments into the other register set, so
-  // LDS and HBM latency overlap the remaining MFMAs.
+  // Software pipeline: at the start of stage s the wave waits for its LDS
+  // reads (stage s's fragments) and for its own loads of stage s+1, then meets
+  // the other waves: stage s+1 is complete in LDS, and every wave holds its
+  // stage-s fragments, so the ring slot of stage s is free. It refills that
+  // slot with stage s+NST, starts reading stage s+1's fragments into the
+  // other register set and runs all of stage s's MFMAs while they arrive.
   for (int s = 0; s < NST && s < stages; ++s) issue(s);
   sync_stage(min(stages - 1, NST - 1));
   i32x8 af0[MI], bf0[J], af1[MI], bf1[J];
@@ -302,24 +304,36 @@ __device__ __forceinline__ void fp8_gemm_pipe_tile(const GemmArgs& g, uint8_t* s
   // B first: the accumulator is the transposed tile, so a lane holds one
   // output row (m = lane % 32 of the subtile) and, per group of four
   // registers, four consecutive columns — stored as one 8-byte chunk.
-  auto stage = [&](int s, i32x8 (&af)[MI], i32x8 (&bf)[J], i32x8 (&an)[MI], i32x8 (&bn)[J]) {
+  auto mfmas = [&](i32x8 (&af)[MI], i32x8 (&bf)[J]) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int j = 0; j < J; ++j) acc[i][j] = mfma32(bf[j], af[i], acc[i][j]);
+  };
+  // While stage s+NST exists, NST-2 younger stages stay in flight at the
+  // sync: a constant wait.
+  auto steady = [&](int s, i32x8 (&af)[MI], i32x8 (&bf)[J], i32x8 (&an)[MI], i32x8 (&bn)[J]) {
+    sync_stage(NST - 2);
+    issue(s + NST);
+    read_frags(s + 1, an, bn);
+    mfmas(af, bf);
+  };
+  auto drain = [&](int s, i32x8 (&af)[MI], i32x8 (&bf)[J], i32x8 (&an)[MI], i32x8 (&bn)[J]) {
     if (s + 1 < stages) {
       sync_stage(min(stages - 2 - s, NST - 2));
       if (s + NST < stages) issue(s + NST);
       read_frags(s + 1, an, bn);
     }
-#pragma unroll
-    for (int i = 2; i < MI; ++i)
-#pragma unroll
-      for (int j = 0; j < J; ++j) acc[i][j] = mfma32(bf[j], af[i], acc[i][j]);
+    mfmas(af, bf);
   };
-  for (int s = 0; s < stages; s += 2) {
-    stage(s, af0, bf0, af1, bf1);
-    if (s + 1 < stages) stage(s + 1, af1, bf1, af0, bf0);
+  int s = 0;
+  for (; s + 1 + NST < stages; s += 2) {
+    steady(s, af0, bf0, af1, bf1);
+    steady(s + 1, af1, bf1, af0, bf0);
+  }
+  for (; s < stages; s += 2) {
+    drain(s, af0, bf0, af1, bf1);
+    if (s + 1 < stages) drain(s + 1, af1, bf1, af0, bf0);
   }
 
   // Epilogue: subtile (i, j) element e of a lane is row
