@@ -186,20 +186,21 @@ constexpr int kPBK = 64;  // bytes of K per stage
 
 __device__ __forceinline__ int pswz(int r) { return (r >> 2) & 3; }
 
-// s_waitcnt limiting the vector-memory counter to n (n < 64) and the LDS
-// counter to 0.
-#define JO_WAIT_VM_LDS0(n) __builtin_amdgcn_s_waitcnt(0x0070 | ((n) & 15) | (((n) >> 4) << 14))
+// s_waitcnt limiting only the vector-memory counter to n (n < 64); s_waitcnt
+// limiting only the LDS counter to 0.
+#define JO_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
+#define JO_WAIT_LDS0() __builtin_amdgcn_s_waitcnt(0xC07F)
 
 template <int PER>
 __device__ __forceinline__ void wait_loads(int later) {
   if (later >= 3)
-    JO_WAIT_VM_LDS0(3 * PER);
+    JO_WAIT_VM(3 * PER);
   else if (later == 2)
-    JO_WAIT_VM_LDS0(2 * PER);
+    JO_WAIT_VM(2 * PER);
   else if (later == 1)
-    JO_WAIT_VM_LDS0(PER);
+    JO_WAIT_VM(PER);
   else
-    JO_WAIT_VM_LDS0(0);
+    JO_WAIT_VM(0);
 }
 
 // Direct loads of one stage: BM rows of A then BN rows of B^T, 64 bytes each,
@@ -210,8 +211,9 @@ struct PipeLoads {
   static constexpr int kSlots = (BM + BN) / 16;
   static constexpr int kPerWave = (kSlots + NW - 1) / NW;
   static constexpr bool kEven = kSlots % NW == 0;
-  const uint8_t* src[kPerWave];  // this lane's 16-byte chunk of each slot at K offset 0
-  bool last;                     // the wave owns a slot kPerWave - 1 (always when kEven)
+  const uint8_t* base[kPerWave];  // wave-uniform: the tile's first row of A or B^T
+  uint32_t off[kPerWave];         // this lane's 16-byte chunk of each slot at K offset 0
+  bool last;                      // the wave owns a slot kPerWave - 1 (always when kEven)
 };
 
 // One output tile's K loop and epilogue for a wave holding MI row blocks of 32
@@ -234,7 +236,7 @@ __device__ __forceinline__ void fp8_gemm_pipe_tile(const GemmArgs& g, uint8_t* s
 #pragma unroll
     for (int i = 0; i < Loads::kPerWave; ++i)
       if (Loads::kEven || i + 1 < Loads::kPerWave || ld.last)
-        __builtin_amdgcn_global_load_lds(ld.src[i] + kb, (__attribute__((address_space(3))) void*)(base + (wave + i * NW) * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(ld.base[i] + (ld.off[i] + kb), (__attribute__((address_space(3))) void*)(base + (wave + i * NW) * 1024), 16, 0, 0);
   };
 
   f32x16 acc[MI][J];
@@ -282,6 +284,11 @@ __device__ __forceinline__ void fp8_gemm_pipe_tile(const GemmArgs& g, uint8_t* s
   // reading the stage before it. A bare s_barrier: a fenced barrier would
   // also wait for the loads of the later stages.
   auto sync_stage = [&](int later) {
+    // On its own, outside the branch below: the compiler then knows that no
+    // LDS read is pending after it and lets the MFMAs of the current
+    // fragments run while the next stage's reads are in flight.
+    __builtin_amdgcn_sched_barrier(0);  // the waits stay after the previous stage's MFMAs
+    JO_WAIT_LDS0();
     if (Loads::kEven || ld.last)
       wait_loads<Loads::kPerWave>(later);
     else
@@ -317,6 +324,13 @@ __device__ __forceinline__ void fp8_gemm_pipe_tile(const GemmArgs& g, uint8_t* s
     issue(s + NST);
     read_frags(s + 1, an, bn);
     mfmas(af, bf);
+    // Interleave: one MFMA, then two of the next stage's LDS reads (issuing
+    // every read first measured 5-10% slower than this order).
+#pragma unroll
+    for (int q = 0; q < MI * J; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+    }
   };
   auto drain = [&](int s, i32x8 (&af)[MI], i32x8 (&bf)[J], i32x8 (&an)[MI], i32x8 (&bn)[J]) {
     if (s + 1 < stages) {
@@ -421,16 +435,19 @@ __device__ __forceinline__ void fp8_gemm_pipe_body(const GemmArgs& g) {
 
   // Lane p of a slot fills row +p/4, chunk position p%4 with the global chunk
   // that belongs there. Rows beyond M (N) read row M-1 (N-1); they are never
-  // stored.
+  // stored. Addresses are a wave-uniform 64-bit tile base plus a 32-bit lane
+  // offset (the host keeps 256 rows of A and B^T under 4 GB), which saves the
+  // VGPRs of 64-bit per-lane pointers.
   Loads ld;
 #pragma unroll
   for (int i = 0; i < Loads::kPerWave; ++i) {
     const int slot = wave + i * NW;
     const bool is_a = slot < BM / 16;
     const int r = (is_a ? slot : slot - BM / 16) * 16 + lane / 4;
-    const uint8_t* row = is_a ? g.a + static_cast<int64_t>(min(m0 + r, g.M - 1)) * g.lda
-                              : g.b + static_cast<int64_t>(min(n0 + r, g.N - 1)) * g.ldb;
-    ld.src[i] = row + (((lane & 3) ^ pswz(r)) * 16);
+    const int row = is_a ? min(m0 + r, g.M - 1) - m0 : min(n0 + r, g.N - 1) - n0;
+    ld.base[i] = is_a ? g.a + static_cast<int64_t>(m0) * g.lda : g.b + static_cast<int64_t>(n0) * g.ldb;
+    ld.off[i] = static_cast<uint32_t>(row) * static_cast<uint32_t>(is_a ? g.lda : g.ldb) +
+                (((lane & 3) ^ pswz(r)) * 16);
   }
   ld.last = Loads::kEven || wave + (Loads::kPerWave - 1) * NW < Loads::kSlots;
   if constexpr (BM == 256) {
@@ -482,7 +499,8 @@ int pick_tile_rows(int M, int N) {
 template <class OutTag>
 int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   const dim3 grid((g.N + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
-  const bool pipe_ok = g.K % kPBK == 0 && aligned(g.sb, 16) && (g.bias == nullptr || aligned(g.bias, 8));
+  const bool pipe_ok = g.K % kPBK == 0 && aligned(g.sb, 16) && (g.bias == nullptr || aligned(g.bias, 8)) &&
+                       256 * max(g.lda, g.ldb) + g.K <= int64_t{UINT32_MAX};
   // 8-wave 256-column tiles measured faster than two 4-wave 128-column
   // workgroups per CU at every deployment shape (3120x12288x4096: 199 -> 185
   // us, 3120x16384x4096: 257 -> 233 us). JO_GEMM_SHAPE=0|1|2|3|4 forces
