@@ -415,6 +415,20 @@ __device__ __forceinline__ float row_reduce(float v, float* slot) {
   }
 }
 
+// True on every lane of the rows that share this thread's reduction group
+// when `pred` holds on any of their lanes: a wave-wide vote when a row fits in
+// a wave (no barrier; the rows of one wave then take the same branch), else a
+// block-wide one. (Measured on the per-token quantizer at [10530, 3072]:
+// 17.7 -> 17.4 us against a block-wide vote; the norm kernels measured the
+// same or slower with it and keep theirs.)
+template <int LPR>
+__device__ __forceinline__ bool rows_any(bool pred) {
+  if constexpr (LPR <= kWave)
+    return __builtin_amdgcn_ballot_w64(pred) != 0;
+  else
+    return __syncthreads_or(pred);
+}
+
 // Block-wide reduction for the generic (one row per block) kernels.
 template <class Op>
 __device__ __forceinline__ float block_reduce(float v, float* slot) {

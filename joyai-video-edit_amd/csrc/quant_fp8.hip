@@ -17,8 +17,9 @@ namespace {
 //   inv = (scale == 0) ? 0 : 1 / scale, q = e4m3fn(clamp(x * inv, +-448)).
 // The row maximum is first taken NaN-propagating; when it is finite (no NaN,
 // no inf in the row) it is the reference's amax and, with a finite inv, the
-// clamp cannot change a code, so it is skipped. Any workgroup holding a
-// non-finite row recomputes the NaN-skipping maximum and clamps that row.
+// clamp cannot change a code, so it is skipped. Any wave (workgroup, for
+// rows wider than a wave) holding a non-finite row recomputes the
+// NaN-skipping maximum and clamps that row.
 // ---------------------------------------------------------------------------
 template <class Tag, int LPR, int CH>
 __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restrict__ x, int64_t xs,
@@ -48,7 +49,7 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restri
   }
   amax = row_reduce<LPR, OpAmax>(amax, red);
   const bool finite_row = finite_bits(amax);
-  if (__syncthreads_or(!finite_row)) {
+  if (rows_any<LPR>(!finite_row)) {
     // Reference amax: NaNs skipped (fmaxf from 0).
     float m = 0.f;
 #pragma unroll
