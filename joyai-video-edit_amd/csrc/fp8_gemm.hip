@@ -18,6 +18,8 @@
 // reads with one ds_read_b128 fall in 16 distinct 16-byte bank groups.
 #include <stdlib.h>
 
+#include <atomic>
+
 #include "jo_device.hpp"
 #include "jo_host.hpp"
 
@@ -473,15 +475,18 @@ void launch_pipe(const GemmArgs& g, hipStream_t stream) {
                      dim3((g.N + BN - 1) / BN, (g.M + BM - 1) / BM), dim3(NW * 64), 0, stream, g);
 }
 
+// CUs of the current device (queried once per device; 256, MI355X's count,
+// if the query fails).
 int cu_count() {
-  static int cached[64] = {};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 // Tile rows for the 8-wave x 256-column kernel: one workgroup per CU, so the
