@@ -10,7 +10,11 @@ residual + LayerNorm + AdaLN with the per-token FP8 epilogue, C2 shape) and
 N4 (the graph runner's 40-layer KV-pool commit at the deployment shape), and
 the FP8 GEMMs G1-G3 (fp8_scaled_mm at Fp8Linear's deployment shapes), whose
 lines add TFLOP/s against the 5.0 PFLOP/s dense fp8 matrix-core peak and the
-time of torch._scaled_mm (hipBLASLt) on the same operands.
+time of torch._scaled_mm (hipBLASLt) on the same operands. R_* are the
+reference-signature ops at the DiT block's deployment shapes (hidden 4096,
+32 heads, 3120 tokens): table-mode QK norm + RoPE, LayerNorm with per-row
+modulation, per-token quant of [3120, 4096] and [3120, 16384], and the
+pre-RoPE K RMSNorm over [99840, 128].
 
 Timing: W eager warmup calls, then K calls captured into one HIP graph and
 replayed once untimed and once timed between HIP events recorded on the

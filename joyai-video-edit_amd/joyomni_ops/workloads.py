@@ -19,6 +19,14 @@ Next-row workloads (not BASELINE configs; same shapes):
        V of 40 layers x 1560 tokens x 32 heads x 128 into a [40, 1, 3120, 32, 128]
        pool at token offset 1560, fp32 [1560, 128] tables
 
+Deployment shapes through the reference-signature entry points (reported):
+  R_qk    fused_qk_norm_rope_3d_paired, q,k [1, 3120, 32, 128], bf16 [3120, 64] tables
+  R_ln    fused_norm_scale_shift (LayerNorm, no affine), x [3120, 4096] with
+          per-row scale / shift [3120, 4096] as the reference caller passes them
+  R_q4k   sgl_per_token_quant_fp8, x [3120, 4096]
+  R_q16k  sgl_per_token_quant_fp8, x [3120, 16384]
+  R_rms   rmsnorm of the pre-RoPE K rows, x [99840, 128]
+
 Inputs are generated on the CPU with torch.Generator().manual_seed(s)
 (s = config index) in fp32, cast to bf16, and copied to the device, so the
 CPU oracle and the GPU see identical tensors. Outliers: exactly
@@ -58,6 +66,13 @@ CONFIGS: dict[str, Config] = {
     "G1": Config("G1", "gemm", 7, dict(M=3120, N=12288, K=4096)),
     "G2": Config("G2", "gemm", 8, dict(M=3120, N=16384, K=4096)),
     "G3": Config("G3", "gemm", 9, dict(M=3120, N=4096, K=16384)),
+    # Deployment shapes of the DiT block (hidden 4096, 32 heads, 3120 tokens)
+    # through the reference-signature entry points; reported, not gated.
+    "R_qk": Config("R_qk", "qk_table", 10, dict(B=1, L=3120, H=32, D=128, eps=1e-6)),
+    "R_ln": Config("R_ln", "ln_rows", 11, dict(M=3120, N=4096, eps=1e-6)),
+    "R_q4k": Config("R_q4k", "quant", 12, dict(M=3120, K=4096)),
+    "R_q16k": Config("R_q16k", "quant", 13, dict(M=3120, K=16384)),
+    "R_rms": Config("R_rms", "rmsnorm", 14, dict(M=99840, N=128, eps=1e-6)),
 }
 
 
@@ -74,12 +89,17 @@ def make_inputs(cfg: Config, device="cpu") -> dict:
     g = torch.Generator().manual_seed(cfg.seed)
     d = cfg.dims
     out: dict = {}
-    if cfg.op in ("qk_grid", "qk_kvcache"):
+    if cfg.op in ("qk_grid", "qk_kvcache", "qk_table"):
         shape = (d["B"], d["L"] * d["H"], d["D"])
         out["q"] = torch.randn(shape, generator=g).to(torch.bfloat16)
         out["k"] = torch.randn(shape, generator=g).to(torch.bfloat16)
         out["q_weight"] = (1 + 0.1 * torch.randn(d["D"], generator=g)).to(torch.bfloat16)
         out["k_weight"] = (1 + 0.1 * torch.randn(d["D"], generator=g)).to(torch.bfloat16)
+        if cfg.op == "qk_table":
+            # bf16 [L, D/2] tables, as the reference caller slices them
+            ang = torch.rand(d["L"], d["D"] // 2, generator=g) * 100
+            out["cos"] = ang.cos().to(torch.bfloat16)
+            out["sin"] = ang.sin().to(torch.bfloat16)
         if cfg.op == "qk_kvcache":
             gh, gw = d["grid"]
             out["k_cache"] = torch.zeros((d["B"], d["cache_slots"] * gh * gw * d["H"], d["D"]),
@@ -110,6 +130,14 @@ def make_inputs(cfg: Config, device="cpu") -> dict:
         ang = torch.rand(d["T"], d["D"] // 2, generator=g) * 100
         out["cos"] = ang.cos().repeat_interleave(2, 1).contiguous()
         out["sin"] = ang.sin().repeat_interleave(2, 1).contiguous()
+    elif cfg.op == "ln_rows":
+        # per-row scale / shift [M, N], as the reference caller materialises them
+        out["x"] = torch.randn(d["M"], d["N"], generator=g).to(torch.bfloat16)
+        out["scale"] = (0.2 * torch.randn(d["M"], d["N"], generator=g)).to(torch.bfloat16)
+        out["shift"] = (0.2 * torch.randn(d["M"], d["N"], generator=g)).to(torch.bfloat16)
+    elif cfg.op == "rmsnorm":
+        out["x"] = torch.randn(d["M"], d["N"], generator=g).to(torch.bfloat16)
+        out["weight"] = (1 + 0.1 * torch.randn(d["N"], generator=g)).to(torch.bfloat16)
     elif cfg.op == "rms_quant":
         out["x"] = with_outliers(torch.randn(d["M"], d["N"], generator=g), g).to(torch.bfloat16)
         out["weight"] = (1 + 0.1 * torch.randn(d["N"], generator=g)).to(torch.bfloat16)
@@ -127,6 +155,13 @@ def algorithmic_bytes(cfg: Config) -> int:
     if cfg.op == "qk_kvcache":
         n = d["B"] * d["L"] * d["H"] * d["D"] * 2
         return 4 * n + 2 * d["D"] * 2                      # q r/w, k read, cache write
+    if cfg.op == "qk_table":
+        n = d["B"] * d["L"] * d["H"] * d["D"] * 2
+        return 4 * n + 2 * d["D"] * 2 + 2 * d["L"] * (d["D"] // 2) * 2   # + cos/sin tables
+    if cfg.op == "ln_rows":
+        return 4 * d["M"] * d["N"] * 2                     # x, scale, shift in; y out
+    if cfg.op == "rmsnorm":
+        return 2 * d["M"] * d["N"] * 2 + d["N"] * 2        # x in, out, weight
     if cfg.op == "quant":
         return d["M"] * d["K"] * 3 + d["M"] * 4            # bf16 in, fp8 out, scales
     if cfg.op == "add_ln":
@@ -162,8 +197,10 @@ def alloc_outputs(cfg: Config, inputs: dict) -> dict:
         ns = (d["M"],) if d["group"] == 0 else (d["M"], d["N"] // d["group"])
         return {"q": torch.empty(d["M"], d["N"], dtype=torch.float8_e4m3fn, device=dev),
                 "s": torch.empty(ns, dtype=torch.float32, device=dev)}
-    if cfg.op == "add_ln":
+    if cfg.op in ("add_ln", "ln_rows"):
         return {"y": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev)}
+    if cfg.op == "rmsnorm":
+        return {"out": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev)}
     if cfg.op == "gemm":
         return {"out": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev)}
     if cfg.op == "add_ln_quant":
@@ -191,6 +228,19 @@ def launch(cfg: Config, t: dict, stream_handle: int, freqs: torch.Tensor | None 
         _abi.call("jo_fused_add_layernorm_scale_shift", p(t["x"]), d["N"], p(t["residual"]),
                   d["N"], None, 0, None, None, p(t["scale"]), 0, p(t["shift"]), 0, p(t["y"]),
                   d["N"], d["M"], d["N"], _abi.JO_DTYPE_BF16, d["eps"], stream_handle)
+    elif cfg.op == "ln_rows":
+        _abi.call("jo_fused_norm_scale_shift", p(t["x"]), d["N"], None, None, p(t["scale"]),
+                  d["N"], p(t["shift"]), d["N"], p(t["y"]), d["N"], d["M"], d["N"],
+                  _abi.JO_DTYPE_BF16, _abi.JO_NORM_LAYER, d["eps"], stream_handle)
+    elif cfg.op == "rmsnorm":
+        _abi.call("jo_rmsnorm", p(t["x"]), d["N"], p(t["weight"]), p(t["out"]), d["N"], d["M"],
+                  d["N"], _abi.JO_DTYPE_BF16, d["eps"], stream_handle)
+    elif cfg.op == "qk_table":
+        B, L, H, D = d["B"], d["L"], d["H"], d["D"]
+        tok = H * D
+        _abi.call("jo_fused_qk_norm_rope_3d_paired", p(t["q"]), p(t["k"]), B, L, H, D, L * tok,
+                  tok, L * tok, tok, d["eps"], p(t["q_weight"]), p(t["k_weight"]), p(t["cos"]),
+                  p(t["sin"]), stream_handle)
     elif cfg.op == "add_ln_quant":
         _abi.call("jo_norm_scale_shift_quant_fp8", p(t["x"]), d["N"], p(t["residual"]), d["N"],
                   p(t["gate"]), 0, None, None, p(t["scale"]), 0, p(t["shift"]), 0, p(t["q"]),
