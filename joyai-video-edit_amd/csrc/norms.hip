@@ -170,6 +170,8 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
       for (int j = 0; j < 8; ++j) yq[i][j] = 0.f;
     }
     if (!(row_ok && e < N)) continue;
+    // Loaded here rather than with the row: issuing per-row scale and shift
+    // with x measured slower at [3120, 4096] (20.0 -> 22.7 us).
     const u32x4 sc = ld_mod<Tag>(a.scale, a.scs, row, e);
     const u32x4 sh = ld_mod<Tag>(a.shift, a.shs, row, e);
     u32x4 gm = u32x4{0u, 0u, 0u, 0u}, bt = u32x4{0u, 0u, 0u, 0u};
@@ -340,11 +342,19 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const void* __restrict_
   const int lane = threadIdx.x % LPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
   const bool row_ok = row < M;
-  u32x4 c[CH];
+  u32x4 c[CH], wv[CH];
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * V;
     c[i] = (row_ok && e < N) ? ld_row<Tag>(x, row * xs, e) : u32x4{0u, 0u, 0u, 0u};
+  }
+  // Weight chunks are issued with the row loads so their (cached) latency
+  // overlaps the row's instead of following the reduction ([99840, 128]:
+  // 10.8 -> 10.2 us).
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * V;
+    wv[i] = e < N ? ld_chunk<Tag>(w, 0, e) : u32x4{0u, 0u, 0u, 0u};
   }
   float ss = 0.f;
 #pragma unroll
@@ -361,10 +371,9 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const void* __restrict_
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * V;
     if (!(row_ok && e < N)) continue;
-    const u32x4 wc = ld_chunk<Tag>(w, 0, e);
     float o[V];
 #pragma unroll
-    for (int j = 0; j < V; ++j) o[j] = (elem<Tag>(c[i], j) * r) * elem<Tag>(wc, j);
+    for (int j = 0; j < V; ++j) o[j] = (elem<Tag>(c[i], j) * r) * elem<Tag>(wv[i], j);
     st_row<Tag>(out, row * os, e, pack<Tag>(o));
   }
 }
