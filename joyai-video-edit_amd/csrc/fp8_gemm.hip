@@ -411,8 +411,8 @@ __device__ __forceinline__ void fp8_gemm_pipe_tile(const GemmArgs& g, uint8_t* s
       const int rl = c / kChunksPerRow, ch = c % kChunksPerRow;
       const int m = m0 + half * 128 + rl, n = n0 + ch * 8;
       if (m < g.M && n < g.N)
-        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(g.out) + static_cast<int64_t>(m) * g.ldo + n) =
-            *reinterpret_cast<const u32x4*>(smem + rl * kRowBytes + ch * 16);
+        st16_nt(static_cast<uint16_t*>(g.out) + static_cast<int64_t>(m) * g.ldo + n,
+                *reinterpret_cast<const u32x4*>(smem + rl * kRowBytes + ch * 16));
     }
   }
 }
