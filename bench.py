@@ -8,7 +8,7 @@ bf16 [10530, 3072] activation. Every other BASELINE config is timed the same
 way and reported under "ops", as are the next-row workloads N3 (the gated
 residual + LayerNorm + AdaLN with the per-token FP8 epilogue, C2 shape) and
 N4 (the graph runner's 40-layer KV-pool commit at the deployment shape), and
-the FP8 GEMMs G1-G3 (fp8_scaled_mm at Fp8Linear's deployment shapes), whose
+the FP8 GEMMs G1-G4 (fp8_scaled_mm at Fp8Linear's deployment shapes), whose
 lines add TFLOP/s against the 5.0 PFLOP/s dense fp8 matrix-core peak and the
 time of torch._scaled_mm (hipBLASLt) on the same operands. R_* are the
 reference-signature ops at the DiT block's deployment shapes (hidden 4096,
