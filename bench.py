@@ -248,7 +248,9 @@ def cpu_fn(cfg):
     return qk
 
 
-def time_cpu(cfg, warmup: int, iters: int) -> dict:
+def time_cpu(cfg, warmup: int, iters: int, seconds: float = 0.0) -> dict:
+    """Median CPU time per call: at least `iters` calls and at least `seconds`
+    of timed CPU work (capped at 1000 calls)."""
     import torch
 
     from joyomni_ops import workloads as W
@@ -257,14 +259,15 @@ def time_cpu(cfg, warmup: int, iters: int) -> dict:
     for _ in range(warmup):
         fn(t)
     ts = []
-    for _ in range(iters):
+    while len(ts) < iters or (sum(ts) < seconds and len(ts) < 1000):
         t0 = time.perf_counter()
         fn(t)
         ts.append(time.perf_counter() - t0)
+    iters = len(ts)
     us = statistics.median(ts) * 1e6
     alg = W.algorithmic_bytes(cfg)
     return {"us_per_call": round(us, 1), "gbps": round(alg / (us * 1e-6) / 1e9, 2),
-            "threads": torch.get_num_threads(), "iters": iters}
+            "threads": torch.get_num_threads(), "iters": iters, "seconds": round(sum(ts), 1)}
 
 
 def cpu_model() -> str:
@@ -296,7 +299,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", default="", help="comma-separated config names")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-iters", type=int, default=10)
+    ap.add_argument("--cpu-iters", type=int, default=10, help="minimum timed CPU calls")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="minimum seconds of timed CPU work for the baseline")
     ap.add_argument("--no-graph", action="store_true",
                     help="time eager launches only (for profiler counter runs)")
     ap.add_argument("--copy-mb", type=int, default=0,
@@ -345,7 +350,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         log("cpu baseline: oracle per_token_quant_fp8 on the full C1 input")
-        cpu = time_cpu(W.CONFIGS[HEADLINE], 3, args.cpu_iters)
+        cpu = time_cpu(W.CONFIGS[HEADLINE], 3, args.cpu_iters, args.cpu_seconds)
         log(f"cpu: {cpu}")
 
     h = results[HEADLINE]
@@ -373,7 +378,8 @@ def main() -> int:
             "value": cpu["gbps"], "unit": "GB/s", "us_per_call": cpu["us_per_call"],
             "cores": cpu["threads"], "kind": "port",
             "sample": f"oracle.ops.per_token_quant_fp8 (torch CPU) on the full C1 input, "
-                      f"median of {cpu['iters']} calls after 3 warmups; host {cpu_model()}, "
+                      f"median of {cpu['iters']} calls (~{cpu['seconds']:.0f} s of CPU work) after "
+                      f"3 warmups; host {cpu_model()}, "
                       f"{os.cpu_count()} logical CPUs"},
         "ops": results,
     }
