@@ -1,0 +1,168 @@
+"""The committed fixtures (tests/golden/fixtures.npz, written by
+tests/golden/make_golden.py from seeded inputs through the CPU oracle):
+
+  CPU  the oracle still reproduces every stored output bit for bit, so a
+       change to a restatement cannot pass unnoticed;
+  GPU  the HIP kernels, through the torch ops the reference's callers use,
+       match the stored outputs: FP8 bytes, scales, residuals and the KV-pool
+       commit exactly, bf16 results within 1 bf16 ulp of the stored fp32
+       values, the GEMM within the fp32-accumulation bar.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_bf16_within_ulp, assert_within_ulp
+
+FIXTURES = Path(__file__).resolve().parent / "golden" / "fixtures.npz"
+
+
+@pytest.fixture(scope="module")
+def fx():
+    with np.load(FIXTURES, allow_pickle=False) as d:
+        return {k: d[k] for k in d.files}
+
+
+def bf16(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(a.astype(np.uint16).view(np.int16).copy()).view(torch.bfloat16)
+
+
+def row_floor(ref: torch.Tensor) -> torch.Tensor:
+    return ref.abs().amax(dim=-1, keepdim=True)
+
+
+def test_oracle_reproduces_fixtures(fx):
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("make_golden", FIXTURES.parent / "make_golden.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    fresh = mod.build()
+    assert sorted(fresh) == sorted(fx), "fixture keys differ"
+    for k, v in fresh.items():
+        assert v.dtype == fx[k].dtype and v.shape == fx[k].shape, k
+        equal_nan = v.dtype.kind == "f"
+        assert np.array_equal(v, fx[k], equal_nan=equal_nan), f"{k} differs from the fixture"
+
+
+@pytest.mark.gpu
+def test_golden_per_token_quant(fx, dev):
+    import joyomni_ops as jo
+    x = bf16(fx["quant_x"])
+    q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty(x.shape[0], dtype=torch.float32, device=dev)
+    jo.sgl_per_token_quant_fp8(x.to(dev), q, s)
+    torch.cuda.synchronize()
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), fx["quant_q"])
+    assert np.array_equal(s.cpu().numpy(), fx["quant_s"], equal_nan=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("group", [0, 128])
+def test_golden_rmsnorm_quant(fx, dev, group):
+    import joyomni_ops as jo
+    x, w = bf16(fx["rmsq_x"]), bf16(fx["rmsq_w"])
+    tag = "tok" if group == 0 else "blk"
+    q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty(fx[f"rmsq_{tag}_s"].shape, dtype=torch.float32, device=dev)
+    jo.rmsnorm_quant_fp8(x.to(dev), w.to(dev), 1e-6, q, s, group)
+    torch.cuda.synchronize()
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), fx[f"rmsq_{tag}_q"])
+    assert np.array_equal(s.cpu().numpy(), fx[f"rmsq_{tag}_s"])
+
+
+@pytest.mark.gpu
+def test_golden_qk_table(fx, dev):
+    import joyomni_ops as jo
+    q, k = bf16(fx["qkt_q"]).to(dev), bf16(fx["qkt_k"]).to(dev)
+    ref_q, ref_k = torch.from_numpy(fx["qkt_q_ref"]), torch.from_numpy(fx["qkt_k_ref"])
+    _, L, H, D = ref_q.shape
+    jo.fused_qk_norm_rope_3d_paired(q, k, L, H, 1e-6, bf16(fx["qkt_wq"]).to(dev),
+                                    bf16(fx["qkt_wk"]).to(dev), bf16(fx["qkt_cos"]).to(dev),
+                                    bf16(fx["qkt_sin"]).to(dev))
+    torch.cuda.synchronize()
+    assert_bf16_within_ulp(q.cpu().reshape(ref_q.shape), ref_q, row_floor(ref_q), what="table q")
+    assert_bf16_within_ulp(k.cpu().reshape(ref_k.shape), ref_k, row_floor(ref_k), what="table k")
+
+
+@pytest.mark.gpu
+def test_golden_qk_grid(fx, dev):
+    import joyomni_ops as jo
+    q, k = bf16(fx["qkg_q"]).to(dev), bf16(fx["qkg_k"]).to(dev)
+    ref_q, ref_k = torch.from_numpy(fx["qkg_q_ref"]), torch.from_numpy(fx["qkg_k_ref"])
+    _, L, H, D = ref_q.shape
+    dims = (44, 42, 42)
+    freqs = jo.rope_freqs(D, dims, 10000.0, 256.0, device=dev)
+    jo.fused_qk_norm_rope_3d_grid(q, k, L, H, 1e-6, bf16(fx["qkg_wq"]).to(dev),
+                                  bf16(fx["qkg_wk"]).to(dev), freqs, dims, (3, 5), 7, 1.0)
+    torch.cuda.synchronize()
+    assert_bf16_within_ulp(q.cpu().reshape(ref_q.shape), ref_q, row_floor(ref_q), what="grid q")
+    assert_bf16_within_ulp(k.cpu().reshape(ref_k.shape), ref_k, row_floor(ref_k), what="grid k")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("norm", ["layer", "rms"])
+def test_golden_norm_scale_shift(fx, dev, norm):
+    import joyomni_ops as jo
+    x, sc, sh = (bf16(fx[k]).to(dev) for k in ("nss_x", "nss_scale", "nss_shift"))
+    gamma = bf16(fx["nss_gamma"]).to(dev)
+    beta = bf16(fx["nss_beta"]).to(dev) if norm == "layer" else None
+    y = jo.fused_norm_scale_shift(x, gamma, beta, sc, sh, norm, 1e-5)
+    torch.cuda.synchronize()
+    ref = torch.from_numpy(fx["nss_ln_ref" if norm == "layer" else "nss_rms_ref"])
+    assert_within_ulp(y.cpu(), ref, torch.bfloat16, row_floor(ref), what=f"norm_scale_shift {norm}")
+
+
+@pytest.mark.gpu
+def test_golden_rmsnorm(fx, dev):
+    import joyomni_ops as jo
+    y = jo.rmsnorm(bf16(fx["rms_x"]).to(dev), bf16(fx["rms_w"]).to(dev), 1e-6)
+    torch.cuda.synchronize()
+    ref = torch.from_numpy(fx["rms_ref"])
+    assert_within_ulp(y.cpu(), ref, torch.bfloat16, row_floor(ref), what="rmsnorm")
+
+
+@pytest.mark.gpu
+def test_golden_add_layernorm(fx, dev):
+    import joyomni_ops as jo
+    res = bf16(fx["addln_res"]).to(dev)
+    y = jo.fused_add_layernorm_scale_shift(bf16(fx["addln_x"]).to(dev), res,
+                                           bf16(fx["addln_scale"]).to(dev),
+                                           bf16(fx["addln_shift"]).to(dev),
+                                           gate=bf16(fx["addln_gate"]).to(dev), eps=1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(res.cpu(), bf16(fx["addln_new_res"])), "residual differs"
+    ref = torch.from_numpy(fx["addln_y_ref"])
+    assert_within_ulp(y.cpu(), ref, torch.bfloat16, row_floor(ref), what="add + LN")
+
+
+@pytest.mark.gpu
+def test_golden_kv_commit(fx, dev):
+    import joyomni_ops as jo
+    pk, pv = bf16(fx["kvc_pool_k"]).to(dev), bf16(fx["kvc_pool_v"]).to(dev)
+    jo.kv_commit_rope(bf16(fx["kvc_stage_k"]).to(dev), pk, 2, torch.from_numpy(fx["kvc_cos"]).to(dev),
+                      torch.from_numpy(fx["kvc_sin"]).to(dev), src_v=bf16(fx["kvc_stage_v"]).to(dev),
+                      dst_v=pv)
+    torch.cuda.synchronize()
+    assert torch.equal(pk.cpu(), bf16(fx["kvc_new_k"])), "pool K differs"
+    assert torch.equal(pv.cpu(), bf16(fx["kvc_new_v"])), "pool V differs"
+
+
+@pytest.mark.gpu
+def test_golden_fp8_scaled_mm(fx, dev):
+    import joyomni_ops as jo
+    a = torch.from_numpy(fx["gemm_a"]).view(torch.float8_e4m3fn).to(dev)
+    bt = torch.from_numpy(fx["gemm_bt"]).view(torch.float8_e4m3fn).to(dev)
+    out = jo.fp8_scaled_mm(a, bt.t(), torch.from_numpy(fx["gemm_sa"]).to(dev),
+                           torch.from_numpy(fx["gemm_sb"]).to(dev), torch.bfloat16,
+                           bf16(fx["gemm_bias"]).to(dev))
+    torch.cuda.synchronize()
+    exact = torch.from_numpy(fx["gemm_exact"])
+    mag = torch.from_numpy(fx["gemm_mag"])
+    # one bf16 rounding of the exact value plus the fp32 accumulation-order bar
+    tol = exact.abs() * 2.0 ** -8 + mag * 2.0 ** -14 + 1e-6
+    err = (out.cpu().double() - exact).abs()
+    assert bool((err <= tol).all()), f"gemm: max err/tol {(err / tol).max().item():.3f}"
