@@ -74,17 +74,21 @@ __global__ __launch_bounds__(kBlock) void rope_commit_kernel(const CommitArgs a)
   const u32x4 c_lo = ld16(ct), c_hi = ld16(ct + 4);
   const u32x4 s_lo = ld16(st), s_hi = ld16(st + 4);
 
+  // Loads are never predicated (a predicated load's join forces an early
+  // wait): a chunk beyond the row reads a chunk inside it instead and is
+  // never stored.
+  const int e_safe = (lane * 8) % a.row_elems;
   u32x4 k[CH], v[CH];
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int e = i * 512 + lane * 8;
-    if (e < a.row_elems) k[i] = ld16_nt(byte_off(a.src_k, (so + e) * Tag::kBytes));
+    k[i] = ld16_nt(byte_off(a.src_k, (so + (e < a.row_elems ? e : e_safe)) * Tag::kBytes));
   }
   if (has_v) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int e = i * 512 + lane * 8;
-      if (e < a.row_elems) v[i] = ld16_nt(byte_off(a.src_v, (so + e) * Tag::kBytes));
+      v[i] = ld16_nt(byte_off(a.src_v, (so + (e < a.row_elems ? e : e_safe)) * Tag::kBytes));
     }
   }
   float cs[8], sn[8];
