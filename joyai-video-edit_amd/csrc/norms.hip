@@ -198,11 +198,12 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
   }
   if constexpr (QNT) {
     // As quant_rows_kernel: a finite NaN-propagating maximum is the
-    // reference's amax and lets the clamp go; workgroups with a non-finite
-    // row take the NaN-skipping maximum and clamp.
+    // reference's amax and lets the clamp go; waves (workgroups, for rows
+    // wider than a wave) with a non-finite row take the NaN-skipping maximum
+    // and clamp.
     float amax = row_reduce<LPR, OpAmax>(ymax, red_c);
     const bool finite_row = finite_bits(amax);
-    if (__syncthreads_or(!finite_row)) {
+    if (rows_any<LPR>(!finite_row)) {
       float m = 0.f;
 #pragma unroll
       for (int i = 0; i < CH; ++i)

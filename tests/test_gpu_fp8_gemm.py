@@ -99,6 +99,26 @@ def test_fp8_scaled_mm_strided_operands(abi, dev, stream_handle):
     check(out[:, :N], a, w.t(), sa, sb, bias, "strided")
 
 
+def test_fp8_scaled_mm_huge_row_stride(abi, dev, stream_handle):
+    """A row stride of 17 MiB: 255 rows of it overflow the 32-bit lane offsets
+    of the LDS-pipelined kernels, so the launch must take the 64-bit-addressed
+    kernel (a wrapped offset would read other rows and fail the check)."""
+    M, N, K = 257, 16, 64
+    lda = (1 << 24) + (1 << 20)
+    a, w, sa, sb, bias = operands(M, N, K, 9)
+    abuf = torch.empty(M * lda, dtype=torch.uint8, device=dev)
+    abuf.as_strided((M, K), (lda, 1)).copy_(a.view(torch.uint8).to(dev))
+    wd = w.view(torch.uint8).to(dev)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    sad, sbd, bd = sa.to(dev), sb.to(dev), bias.to(dev)
+    abi.call("jo_fp8_scaled_mm", abuf.data_ptr(), lda, wd.data_ptr(), K, sad.data_ptr(),
+             sbd.data_ptr(), bd.data_ptr(), out.data_ptr(), N, M, N, K,
+             abi.dtype_code(torch.bfloat16), stream_handle)
+    torch.cuda.synchronize()
+    del abuf
+    check(out, a, w.t(), sa, sb, bias, "17 MiB row stride")
+
+
 @pytest.mark.parametrize("N,K", [(12288, 4096), (16384, 4096), (4096, 16384)])
 def test_fp8_scaled_mm_deployment_shapes_sampled_rows(dev, N, K):
     """M = 3120 tokens (720x1248 image stream); 40 sampled rows, the ragged
