@@ -14,7 +14,9 @@ time of torch._scaled_mm (hipBLASLt) on the same operands. R_* are the
 reference-signature ops at the DiT block's deployment shapes (hidden 4096,
 32 heads, 3120 tokens): table-mode QK norm + RoPE, LayerNorm with per-row
 modulation, per-token quant of [3120, 4096] and [3120, 16384], and the
-pre-RoPE K RMSNorm over [99840, 128].
+pre-RoPE K RMSNorm over [99840, 128] — on a contiguous copy (R_rms, the
+reference caller's layout) and read straight from the packed qkv (R_kn, whose
+line adds the time of the caller's copy-then-norm path).
 
 Timing: W eager warmup calls, then K calls captured into one HIP graph and
 replayed once untimed and once timed between HIP events recorded on the
@@ -219,6 +221,38 @@ def torch_reference_us(cfg, dev, iters: int = 10):
     return round(us, 1)
 
 
+def copy_then_rmsnorm_us(cfg, dev, iters: int = 20):
+    """R_kn's path as the reference caller takes it (sgl_fused_ops.py:102-111):
+    .contiguous() of the K slice, then the rmsnorm kernel (this build's, the
+    reference's CUDA kernel not being runnable here), eager, per call."""
+    if cfg.op != "rms_heads":
+        return None
+    import torch
+
+    import joyomni_ops as jo
+    from joyomni_ops import workloads as W
+    d = cfg.dims
+    sets = [{k: v.to(dev) for k, v in W.make_inputs(cfg).items()} for _ in range(4)]
+
+    def call(t):
+        k = t["qkv"][:, :, 1].contiguous().reshape(-1, d["D"])
+        return jo.rmsnorm(k, t["weight"], d["eps"])
+
+    for i in range(4):
+        call(sets[i])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(iters):
+        call(sets[i % 4])
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / iters
+    del sets
+    torch.cuda.empty_cache()
+    return round(us, 1)
+
+
 def cpu_fn(cfg):
     """The oracle's restatement of the reference formula for a config (CPU tensors)."""
     from oracle import ops
@@ -332,6 +366,9 @@ def main() -> int:
         ref_us = torch_reference_us(cfg, dev)
         if ref_us is not None:
             results[n]["torch_reference_us_per_call"] = ref_us
+        caller_us = copy_then_rmsnorm_us(cfg, dev)
+        if caller_us is not None:
+            results[n]["copy_then_rmsnorm_us_per_call"] = caller_us
         flops = W.algorithmic_flops(cfg)
         if flops is not None:
             tf = flops / (results[n]["us_per_call"] * 1e-6) / 1e12

@@ -171,6 +171,25 @@ int jo_rmsnorm(const void* x, int64_t x_stride, const void* weight, void* out,
                void* stream);
 
 /* ------------------------------------------------------------------------
+ * Per-head RMSNorm over rows read from a [tokens, heads, head_dim] view:
+ * row (t, h) = x + t * x_token_stride + h * x_head_stride (elements), written
+ * to out + (t * heads + h) * out_stride. r = 1/sqrt(mean(x^2) + eps).
+ *   round_first == 0: out = (x * r) * w, one rounding — the caller
+ *     rmsnorm_qk_bf16 (deploy/xvideo/models/dit/sgl_fused_ops.py:102-111)
+ *     on the K slice of a packed qkv tensor, without its .contiguous() copy
+ *     (:108); the same kernel and summation order as jo_rmsnorm.
+ *   round_first == 1: out = round(round(x * r) * w), the torch RMSNorm
+ *     module (deploy/xvideo/models/dit/dit.py:228-250, forward :247-249) as
+ *     the text stream applies it to q and k (dit.py:384-385); the mean square
+ *     is the exactly rounded mean of the exact squares.
+ * head_dim >= 1; tokens * heads < 2^32.
+ * ------------------------------------------------------------------------ */
+int jo_rmsnorm_heads(const void* x, int64_t x_token_stride, int64_t x_head_stride,
+                     const void* weight, void* out, int64_t out_stride, int64_t tokens,
+                     int64_t heads, int64_t head_dim, int dtype, float eps, int round_first,
+                     void* stream);
+
+/* ------------------------------------------------------------------------
  * Residual add (optionally gated) + LayerNorm + AdaLN modulation, one pass:
  *   residual <- round(residual + x * gate)        (gate = 1 if NULL)
  *   y = LN(residual)(g, b) * (1 + scale) + shift  on the ROUNDED residual.

@@ -330,24 +330,71 @@ int launch_norm_mod_quant_dt(int dtype, const NormArgs& a, hipStream_t stream, c
 }
 
 // ---------------------------------------------------------------------------
-// RMSNorm: out = (x * r) * w, follows rmsnorm.cu:41-60.
+// RMSNorm rows.
+//   MODE kKernelRms: out = (x * r) * w, one rounding (rmsnorm.cu:41-60);
+//     the sum of squares in fp32 like the reference kernel.
+//   MODE kModuleRms: out = round(round(x * r) * w), the torch RMSNorm module
+//     (dit.py:244-249: the normalized row is cast back to the input type
+//     before the weight multiply). Its mean square is taken exactly (fp64
+//     sum of the exact squares, rounded once), as rmsnorm_quant_kernel does,
+//     so the intermediate rounding does not depend on a summation order.
+//   r = 1 / sqrt(mean(x^2) + eps) with IEEE sqrt and division.
+// HEADS: row m is head m % heads of token m / heads, read at
+// x + token * xs + head * xhs (a per-head norm straight from a packed qkv
+// view); otherwise row m starts at x + m * xs. Output rows are out + m * os.
 // ---------------------------------------------------------------------------
-template <class Tag, int LPR, int CH>
-__global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const void* __restrict__ x, int64_t xs,
-                                                         const void* __restrict__ w,
-                                                         void* __restrict__ out, int64_t os,
-                                                         int64_t M, int N, float eps) {
+constexpr int kKernelRms = 0;
+constexpr int kModuleRms = 1;
+
+// An fp32 product rounded on to the element type: two roundings, as
+// x.float() * rsqrt(...) followed by .type_as(x) does. The empty asm keeps the
+// product an fp32 value; without it the compiler folds multiply and
+// conversion into v_fma_mixlo_f16, which rounds the exact product once.
+template <class Tag>
+__device__ __forceinline__ float round_fp32_product(float v) {
+  asm volatile("" : "+v"(v));
+  return round_to<Tag>(v);
+}
+
+struct RmsArgs {
+  const void* x;
+  int64_t xs, xhs;
+  int heads;
+  const void* w;
+  void* out;
+  int64_t os;
+  int64_t M;
+  int N;
+  float eps;
+};
+
+template <bool HEADS>
+__device__ __forceinline__ int64_t rms_row_offset(const RmsArgs& a, int64_t row) {
+  if constexpr (HEADS) {
+    // M < 2^32 (checked on the host), so the division can be 32-bit.
+    const uint32_t t = static_cast<uint32_t>(row) / static_cast<uint32_t>(a.heads);
+    return static_cast<int64_t>(t) * a.xs + (row - static_cast<int64_t>(t) * a.heads) * a.xhs;
+  } else {
+    return row * a.xs;
+  }
+}
+
+template <class Tag, int LPR, int CH, bool HEADS, int MODE>
+__global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const RmsArgs a) {
   constexpr int V = Tag::kVec;
   constexpr int RPB = kBlock / LPR;
   __shared__ float red[kBlock / kWave];
+  __shared__ double red64[kBlock / kWave];
   const int lane = threadIdx.x % LPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
-  const bool row_ok = row < M;
+  const bool row_ok = row < a.M;
+  const int N = a.N;
+  const int64_t xo = row_ok ? rms_row_offset<HEADS>(a, row) : 0;
   u32x4 c[CH], wv[CH];
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * V;
-    c[i] = (row_ok && e < N) ? ld_row<Tag>(x, row * xs, e) : u32x4{0u, 0u, 0u, 0u};
+    c[i] = (row_ok && e < N) ? ld_row<Tag>(a.x, xo, e) : u32x4{0u, 0u, 0u, 0u};
   }
   // Weight chunks are issued with the row loads so their (cached) latency
   // overlaps the row's instead of following the reduction ([99840, 128]:
@@ -355,68 +402,111 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const void* __restrict_
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * V;
-    wv[i] = e < N ? ld_chunk<Tag>(w, 0, e) : u32x4{0u, 0u, 0u, 0u};
+    wv[i] = e < N ? ld_chunk<Tag>(a.w, 0, e) : u32x4{0u, 0u, 0u, 0u};
   }
-  float ss = 0.f;
+  float ms;
+  if constexpr (MODE == kModuleRms) {
+    double ss = 0.0;
 #pragma unroll
-  for (int i = 0; i < CH; ++i) {
+    for (int i = 0; i < CH; ++i) {
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-      const float v = elem<Tag>(c[i], j);
-      ss += v * v;
+      for (int j = 0; j < V; ++j) {
+        const double v = static_cast<double>(elem<Tag>(c[i], j));
+        ss = __builtin_fma(v, v, ss);
+      }
     }
+    ss = row_reduce_sum64<LPR>(ss, red64);
+    ms = static_cast<float>(ss / static_cast<double>(N));
+  } else {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float v = elem<Tag>(c[i], j);
+        ss += v * v;
+      }
+    }
+    ss = row_reduce<LPR, OpSum>(ss, red);
+    ms = ss / static_cast<float>(N);
   }
-  ss = row_reduce<LPR, OpSum>(ss, red);
-  const float r = 1.0f / sqrtf(ss / static_cast<float>(N) + eps);
+  const float r = 1.0f / sqrtf(ms + a.eps);
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * V;
     if (!(row_ok && e < N)) continue;
     float o[V];
 #pragma unroll
-    for (int j = 0; j < V; ++j) o[j] = (elem<Tag>(c[i], j) * r) * elem<Tag>(wv[i], j);
-    st_row<Tag>(out, row * os, e, pack<Tag>(o));
+    for (int j = 0; j < V; ++j) {
+      float xr = elem<Tag>(c[i], j) * r;
+      if constexpr (MODE == kModuleRms) xr = round_fp32_product<Tag>(xr);
+      o[j] = xr * elem<Tag>(wv[i], j);
+    }
+    st_row<Tag>(a.out, row * a.os, e, pack<Tag>(o));
   }
 }
 
-template <class Tag>
-__global__ __launch_bounds__(kBlock) void rmsnorm_generic_kernel(const void* __restrict__ x,
-                                                                 int64_t xs,
-                                                                 const void* __restrict__ w,
-                                                                 void* __restrict__ out,
-                                                                 int64_t os, int N, float eps) {
+// One row per workgroup, element-wise accesses: any row length and alignment.
+template <class Tag, bool HEADS, int MODE>
+__global__ __launch_bounds__(kBlock) void rmsnorm_generic_kernel(const RmsArgs a) {
   __shared__ float red[kBlock / kWave];
+  __shared__ double red64[kBlock / kWave];
   const int64_t row = blockIdx.x;
-  float ss = 0.f;
-  for (int i = threadIdx.x; i < N; i += kBlock) {
-    const float v = load_elem<Tag>(x, row * xs + i);
-    ss += v * v;
+  const int64_t xo = rms_row_offset<HEADS>(a, row);
+  float ms;
+  if constexpr (MODE == kModuleRms) {
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < a.N; i += kBlock) {
+      const double v = static_cast<double>(load_elem<Tag>(a.x, xo + i));
+      ss = __builtin_fma(v, v, ss);
+    }
+    ss = row_reduce_sum64<kBlock>(ss, red64);
+    ms = static_cast<float>(ss / static_cast<double>(a.N));
+  } else {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < a.N; i += kBlock) {
+      const float v = load_elem<Tag>(a.x, xo + i);
+      ss += v * v;
+    }
+    ss = block_reduce<OpSum>(ss, red);
+    ms = ss / static_cast<float>(a.N);
   }
-  ss = block_reduce<OpSum>(ss, red);
-  const float r = 1.0f / sqrtf(ss / static_cast<float>(N) + eps);
-  for (int i = threadIdx.x; i < N; i += kBlock)
-    store_elem<Tag>(out, row * os + i, (load_elem<Tag>(x, row * xs + i) * r) * load_elem<Tag>(w, i));
+  const float r = 1.0f / sqrtf(ms + a.eps);
+  for (int i = threadIdx.x; i < a.N; i += kBlock) {
+    float xr = load_elem<Tag>(a.x, xo + i) * r;
+    if constexpr (MODE == kModuleRms) xr = round_fp32_product<Tag>(xr);
+    store_elem<Tag>(a.out, row * a.os + i, xr * load_elem<Tag>(a.w, i));
+  }
 }
 
-template <class Tag>
-int launch_rmsnorm(const void* x, int64_t xs, const void* w, void* out, int64_t os, int64_t M,
-                   int64_t N, float eps, hipStream_t stream) {
+template <class Tag, bool HEADS, int MODE>
+int launch_rmsnorm(const RmsArgs& a, hipStream_t stream, const char* op) {
   const int b = Tag::kBytes;
-  const bool vec_ok = (N % Tag::kVec == 0) && aligned(x, 16) && (xs * b) % 16 == 0 &&
-                      aligned(w, 16) && aligned(out, 16) && (os * b) % 16 == 0;
+  const bool vec_ok = (a.N % Tag::kVec == 0) && aligned(a.x, 16) && (a.xs * b) % 16 == 0 &&
+                      (!HEADS || (a.xhs * b) % 16 == 0) && aligned(a.w, 16) &&
+                      aligned(a.out, 16) && (a.os * b) % 16 == 0;
   bool launched = false;
   if (vec_ok) {
-    launched = dispatch_row_shape<Tag::kVec>(N, [&](auto lpr, auto ch) {
+    launched = dispatch_row_shape<Tag::kVec>(a.N, [&](auto lpr, auto ch) {
       constexpr int LPR = decltype(lpr)::value;
       constexpr int CH = decltype(ch)::value;
-      hipLaunchKernelGGL((rmsnorm_kernel<Tag, LPR, CH>), dim3(row_blocks(M, LPR)), dim3(kBlock),
-                         0, stream, x, xs, w, out, os, M, static_cast<int>(N), eps);
+      hipLaunchKernelGGL((rmsnorm_kernel<Tag, LPR, CH, HEADS, MODE>), dim3(row_blocks(a.M, LPR)),
+                         dim3(kBlock), 0, stream, a);
     });
   }
   if (!launched)
-    hipLaunchKernelGGL((rmsnorm_generic_kernel<Tag>), dim3(M), dim3(kBlock), 0, stream, x, xs, w,
-                       out, os, static_cast<int>(N), eps);
-  return launch_status("rmsnorm");
+    hipLaunchKernelGGL((rmsnorm_generic_kernel<Tag, HEADS, MODE>), dim3(a.M), dim3(kBlock), 0,
+                       stream, a);
+  return launch_status(op);
+}
+
+template <bool HEADS, int MODE>
+int launch_rmsnorm_dt(int dtype, const RmsArgs& a, hipStream_t stream, const char* op) {
+  switch (dtype) {
+    case JO_DTYPE_BF16: return launch_rmsnorm<BF16, HEADS, MODE>(a, stream, op);
+    case JO_DTYPE_F16: return launch_rmsnorm<F16, HEADS, MODE>(a, stream, op);
+    default: return launch_rmsnorm<F32, HEADS, MODE>(a, stream, op);
+  }
 }
 
 }  // namespace
@@ -457,12 +547,32 @@ extern "C" int jo_rmsnorm(const void* x, int64_t x_stride, const void* weight, v
   JO_REQUIRE(x_stride >= N && out_stride >= N, "rmsnorm: bad row stride");
   if (M == 0 || N == 0) return JO_OK;
   JO_REQUIRE(x && weight && out, "rmsnorm: null pointer");
+  const RmsArgs a{x, x_stride, 0, 1, weight, out, out_stride, M, static_cast<int>(N), eps};
+  return launch_rmsnorm_dt<false, kKernelRms>(dtype, a, static_cast<hipStream_t>(stream),
+                                              "rmsnorm");
+}
+
+extern "C" int jo_rmsnorm_heads(const void* x, int64_t x_token_stride, int64_t x_head_stride,
+                                const void* weight, void* out, int64_t out_stride,
+                                int64_t tokens, int64_t heads, int64_t head_dim, int dtype,
+                                float eps, int round_first, void* stream) {
+  const char* op = "rmsnorm_heads";
+  JO_REQUIRE(valid_dtype(dtype), "Unsupported dtype; use float32/float16/bfloat16");
+  JO_REQUIRE(round_first == 0 || round_first == 1, "%s: round_first must be 0 or 1", op);
+  JO_REQUIRE(tokens >= 0 && heads > 0 && heads <= INT32_MAX && head_dim > 0 &&
+                 head_dim <= INT32_MAX && tokens * heads <= int64_t{UINT32_MAX},
+             "%s: bad shape [%lld, %lld, %lld]", op, static_cast<long long>(tokens),
+             static_cast<long long>(heads), static_cast<long long>(head_dim));
+  JO_REQUIRE((heads == 1 || x_head_stride >= head_dim) && x_head_stride >= 0 &&
+                 x_token_stride >= 0 && out_stride >= head_dim,
+             "%s: bad strides", op);
+  if (tokens == 0) return JO_OK;
+  JO_REQUIRE(x && weight && out, "%s: null pointer", op);
+  const RmsArgs a{x, x_token_stride, x_head_stride, static_cast<int>(heads), weight, out,
+                  out_stride, tokens * heads, static_cast<int>(head_dim), eps};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case JO_DTYPE_BF16: return launch_rmsnorm<BF16>(x, x_stride, weight, out, out_stride, M, N, eps, st);
-    case JO_DTYPE_F16: return launch_rmsnorm<F16>(x, x_stride, weight, out, out_stride, M, N, eps, st);
-    default: return launch_rmsnorm<F32>(x, x_stride, weight, out, out_stride, M, N, eps, st);
-  }
+  return round_first ? launch_rmsnorm_dt<true, kModuleRms>(dtype, a, st, op)
+                     : launch_rmsnorm_dt<true, kKernelRms>(dtype, a, st, op);
 }
 
 extern "C" int jo_fused_add_layernorm_scale_shift(

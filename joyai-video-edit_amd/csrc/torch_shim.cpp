@@ -6,7 +6,7 @@
 // rmsnorm.cu:77-81, per_token_quant_fp8.cu:149-156, fp8_gemm.cu:1457-1485), so
 // torch.ops.joyomni_ops.* behaves as the reference does for callers. The new
 // ops (grid RoPE, K ring-cache write, add+LayerNorm, RMSNorm->FP8,
-// norm+AdaLN->FP8, KV-pool commit, apply_rotary_emb) have their own names. Tensors on ROCm carry the CUDA
+// norm+AdaLN->FP8, KV-pool commit, apply_rotary_emb, per-head RMSNorm) have their own names. Tensors on ROCm carry the CUDA
 // device type, so the impls are
 // registered on the CUDA dispatch key like the reference's. Every op runs
 // on the current stream of the tensor's device and never synchronizes.
@@ -160,6 +160,40 @@ torch::Tensor rmsnorm(const torch::Tensor& x, const torch::Tensor& weight, doubl
   check_status(jo_rmsnorm(x.data_ptr(), row_stride(x), weight.data_ptr(), out.data_ptr(), N, M,
                           N, dt, static_cast<float>(eps), current_stream(x)),
                "rmsnorm");
+  return out;
+}
+
+// Per-head RMSNorm of a [..., heads, head_dim] view whose last dim is
+// contiguous and whose leading dims collapse to one token stride (e.g. the q
+// or k slice of a packed [B, L, 3, H, D] qkv tensor). round_first selects the
+// torch RMSNorm module's rounding (dit.py:247-249) over the kernel's
+// (rmsnorm.cu:57-60). Returns a new contiguous tensor of x's shape.
+torch::Tensor rmsnorm_heads(const torch::Tensor& x, const torch::Tensor& weight, double eps,
+                            int64_t round_first) {
+  JO_CHECK_CUDA(x);
+  JO_CHECK_CUDA(weight);
+  TORCH_CHECK(x.dim() >= 2, "x must be [..., heads, head_dim]");
+  TORCH_CHECK(x.stride(-1) == 1 || x.size(-1) <= 1, "x last dim must be contiguous");
+  const int64_t D = x.size(-1), H = x.size(-2);
+  TORCH_CHECK(weight.dim() == 1 && weight.numel() == D, "weight must be 1D [head_dim]");
+  TORCH_CHECK(x.dtype() == weight.dtype(), "x and weight dtype must match");
+  TORCH_CHECK(weight.stride(0) == 1 || weight.numel() <= 1, "weight must be contiguous");
+  int64_t tokens = 1, ts = 0, next = -1;
+  for (int64_t d = x.dim() - 3; d >= 0; --d) {
+    if (x.size(d) == 1) continue;
+    if (next < 0) ts = x.stride(d);
+    else TORCH_CHECK(x.stride(d) == next, "x leading dims must collapse to one token stride");
+    next = x.stride(d) * x.size(d);
+    tokens *= x.size(d);
+  }
+  const int dt = dtype_code(x);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  auto out = torch::empty(x.sizes(), x.options());
+  if (out.numel() == 0) return out;
+  check_status(jo_rmsnorm_heads(x.data_ptr(), ts, H <= 1 ? D : x.stride(-2), weight.data_ptr(),
+                                out.data_ptr(), D, tokens, H, D, dt, static_cast<float>(eps),
+                                round_first ? 1 : 0, current_stream(x)),
+               "rmsnorm_heads");
   return out;
 }
 
@@ -625,6 +659,7 @@ TORCH_LIBRARY(joyomni_ops, m) {
       "kv_commit_rope(Tensor src_k, Tensor? src_v, Tensor(a!) dst_k, Tensor(b!)? dst_v, "
       "int dst_offset, Tensor cos, Tensor sin) -> ()");
   m.def("apply_rotary_emb(Tensor x, Tensor cos, Tensor sin) -> Tensor");
+  m.def("rmsnorm_heads(Tensor x, Tensor weight, float eps, int round_first) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(joyomni_ops, CUDA, m) {
@@ -640,4 +675,5 @@ TORCH_LIBRARY_IMPL(joyomni_ops, CUDA, m) {
   m.impl("norm_scale_shift_quant_fp8", &joyomni_ops::norm_scale_shift_quant_fp8);
   m.impl("kv_commit_rope", &joyomni_ops::kv_commit_rope);
   m.impl("apply_rotary_emb", &joyomni_ops::apply_rotary_emb);
+  m.impl("rmsnorm_heads", &joyomni_ops::rmsnorm_heads);
 }

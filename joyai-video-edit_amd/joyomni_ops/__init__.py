@@ -10,8 +10,9 @@ for device tensors only, and importing fails if the libraries are missing.
 
 New ops (no reference signature): fused_qk_norm_rope_3d_grid,
 fused_qk_norm_rope_3d_kvcache, fused_add_layernorm_scale_shift,
-rmsnorm_quant_fp8, plus rope_freqs() to build the [2, head_dim/2] frequency
-table the grid ops read.
+rmsnorm_quant_fp8, norm_scale_shift_quant_fp8, kv_commit_rope,
+apply_rotary_emb, rmsnorm_heads, plus rope_freqs() to build the
+[2, head_dim/2] frequency table the grid ops read.
 """
 from __future__ import annotations
 
@@ -44,6 +45,10 @@ __all__ = [
     "fused_add_layernorm_scale_shift",
     "rmsnorm_quant_fp8",
     "kv_ring_slot",
+    "kv_commit_rope",
+    "apply_rotary_emb",
+    "norm_scale_shift_quant_fp8",
+    "rmsnorm_heads",
 ]
 
 _ops = torch.ops.joyomni_ops
@@ -206,3 +211,14 @@ def apply_rotary_emb(x, freqs_cis):
     bit: (x.float() * cos + rotate_half(x.float()) * sin).type_as(x)."""
     cos, sin = freqs_cis
     return _ops.apply_rotary_emb(x, _table(cos), _table(sin))
+
+
+def rmsnorm_heads(x, weight, eps=1e-6, round_first=False):
+    """Per-head RMSNorm of x [..., heads, head_dim] (last dim contiguous, any
+    token / head strides, e.g. the q or k slice of a packed qkv tensor) into a
+    new contiguous tensor of x's shape.
+
+    round_first=False: (x * r) * w with one rounding, as the reference's
+    rmsnorm kernel (rmsnorm.cu:57-60). round_first=True: the torch RMSNorm
+    module, round(round(x * r) * w) (dit.py:244-249)."""
+    return _ops.rmsnorm_heads(x, weight, eps, 1 if round_first else 0)

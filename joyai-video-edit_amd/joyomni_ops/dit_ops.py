@@ -10,6 +10,8 @@ Same arguments, same results; the differences are in the HBM traffic:
                             (sgl_fused_ops.py:44-51 expands and copies them).
   fused_qk_norm_rope_3d     identical contract (contiguous copies of q/k, tables
                             halved and cast to bf16 as sgl_fused_ops.py:73-94).
+  rmsnorm_qk_bf16           normalizes the K slice of the packed qkv in place of
+                            its .contiguous() copy (sgl_fused_ops.py:108).
 
 Additional entry points for callers that can use the new fused ops:
 
@@ -24,6 +26,9 @@ Additional entry points for callers that can use the new fused ops:
   fused_add_gate_layernorm_modulate_fp8  the same after residual + x * gate.
   commit_kv_pool            StreamingGraphRunner.run_commit (graph_runner.py:137-142)
                             for all layers in one launch.
+  rms_norm_module           the torch RMSNorm module's forward (dit.py:244-249) that
+                            the text stream applies to q and k (dit.py:384-385),
+                            read from the packed qkv view.
   fp8_linear                Fp8Linear.forward (fp8_linear.py:155-169): per-token
                             quantization + fp8_scaled_mm; quantize_weight_per_channel
                             is its weight preparation (fp8_linear.py:100-110).
@@ -36,8 +41,8 @@ import torch
 
 from . import (fp8_scaled_mm, fused_add_layernorm_scale_shift, fused_norm_scale_shift,
                fused_qk_norm_rope_3d_grid, fused_qk_norm_rope_3d_paired,
-               kv_commit_rope, norm_scale_shift_quant_fp8, rmsnorm, rope_freqs,
-               sgl_per_token_quant_fp8)
+               kv_commit_rope, norm_scale_shift_quant_fp8, rmsnorm, rmsnorm_heads,
+               rope_freqs, sgl_per_token_quant_fp8)
 
 
 def available() -> bool:
@@ -114,16 +119,54 @@ def fused_qk_norm_rope_3d(
     return q, k
 
 
+def _heads_view(x: torch.Tensor) -> bool:
+    """x [..., H, D] with a contiguous last dim whose leading dims collapse to
+    one token stride (what rmsnorm_heads reads without a copy)."""
+    if x.dim() < 2 or (x.stride(-1) != 1 and x.shape[-1] > 1):
+        return False
+    nxt = None
+    for d in range(x.dim() - 3, -1, -1):
+        if x.shape[d] == 1:
+            continue
+        if nxt is not None and x.stride(d) != nxt:
+            return False
+        nxt = x.stride(d) * x.shape[d]
+    return True
+
+
 def rmsnorm_qk_bf16(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    """RMSNorm over the last dim of a bf16 tensor (sgl_fused_ops.py:102-111)."""
+    """RMSNorm over the last dim of a bf16 tensor (sgl_fused_ops.py:102-111).
+
+    A [..., H, D] view such as the K slice of the packed qkv is read in place
+    (the reference copies it with .contiguous() first, :108); the result is a
+    new contiguous tensor of x's shape, bit-identical to the rmsnorm op on the
+    copy (same kernel, same summation order)."""
     assert x.dtype == torch.bfloat16, f"rmsnorm_qk_bf16 needs bf16, got {x.dtype}"
+    w = weight.to(dtype=torch.bfloat16)
+    if _heads_view(x):
+        return rmsnorm_heads(x, w, eps)
     orig_shape = x.shape
     D = orig_shape[-1]
-    x_flat = x.reshape(-1, D)
-    if x_flat.stride(-1) != 1:
-        x_flat = x_flat.contiguous()
-    out = rmsnorm(x_flat, weight.to(dtype=torch.bfloat16), eps)
+    out = rmsnorm(x.reshape(-1, D).contiguous(), w, eps)
     return out.reshape(orig_shape)
+
+
+def rms_norm_module(x: torch.Tensor, weight: Optional[torch.Tensor] = None,
+                    eps: float = 1e-6) -> torch.Tensor:
+    """The torch RMSNorm module's forward (dit.py:244-249):
+    (x.float() * rsqrt(mean(x.float()^2) + eps)).type_as(x), times weight
+    (a separately rounded product) when the module is affine. x: [..., D]
+    (the text stream's q or k view, [B, Lt, H, D] inside the packed qkv);
+    weight: [D] in x's dtype or None. Returns a new contiguous tensor."""
+    D = x.shape[-1]
+    if weight is None:
+        weight = torch.ones(D, dtype=x.dtype, device=x.device)
+    if weight.dtype != x.dtype:
+        raise RuntimeError(f"rms_norm_module: weight dtype {weight.dtype} != x dtype {x.dtype}")
+    if _heads_view(x):
+        return rmsnorm_heads(x, weight, eps, round_first=True)
+    return rmsnorm_heads(x.reshape(-1, 1, D).contiguous(), weight, eps,
+                         round_first=True).reshape(x.shape)
 
 
 def fused_add_gate(residual: torch.Tensor, x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:

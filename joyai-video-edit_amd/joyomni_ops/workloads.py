@@ -27,6 +27,9 @@ Deployment shapes through the reference-signature entry points (reported):
   R_q4k   sgl_per_token_quant_fp8, x [3120, 4096]
   R_q16k  sgl_per_token_quant_fp8, x [3120, 16384]
   R_rms   rmsnorm of the pre-RoPE K rows, x [99840, 128]
+  R_kn    rmsnorm_qk_bf16's per-head norm read straight from the K slice of the
+          packed qkv [1, 3120, 3, 32, 128] (jo_rmsnorm_heads; the reference
+          first copies that slice with .contiguous())
 
 Inputs are generated on the CPU with torch.Generator().manual_seed(s)
 (s = config index) in fp32, cast to bf16, and copied to the device, so the
@@ -75,6 +78,7 @@ CONFIGS: dict[str, Config] = {
     "R_q4k": Config("R_q4k", "quant", 12, dict(M=3120, K=4096)),
     "R_q16k": Config("R_q16k", "quant", 13, dict(M=3120, K=16384)),
     "R_rms": Config("R_rms", "rmsnorm", 14, dict(M=99840, N=128, eps=1e-6)),
+    "R_kn": Config("R_kn", "rms_heads", 16, dict(B=1, L=3120, H=32, D=128, eps=1e-6)),
 }
 
 
@@ -143,6 +147,9 @@ def make_inputs(cfg: Config, device="cpu") -> dict:
     elif cfg.op == "rms_quant":
         out["x"] = with_outliers(torch.randn(d["M"], d["N"], generator=g), g).to(torch.bfloat16)
         out["weight"] = (1 + 0.1 * torch.randn(d["N"], generator=g)).to(torch.bfloat16)
+    elif cfg.op == "rms_heads":
+        out["qkv"] = torch.randn(d["B"], d["L"], 3, d["H"], d["D"], generator=g).to(torch.bfloat16)
+        out["weight"] = (1 + 0.1 * torch.randn(d["D"], generator=g)).to(torch.bfloat16)
     else:
         raise ValueError(cfg.op)
     return {k: v.to(device) for k, v in out.items()}
@@ -164,6 +171,8 @@ def algorithmic_bytes(cfg: Config) -> int:
         return 4 * d["M"] * d["N"] * 2                     # x, scale, shift in; y out
     if cfg.op == "rmsnorm":
         return 2 * d["M"] * d["N"] * 2 + d["N"] * 2        # x in, out, weight
+    if cfg.op == "rms_heads":
+        return 2 * d["B"] * d["L"] * d["H"] * d["D"] * 2 + d["D"] * 2   # K slice in, out, weight
     if cfg.op == "quant":
         return d["M"] * d["K"] * 3 + d["M"] * 4            # bf16 in, fp8 out, scales
     if cfg.op == "add_ln":
@@ -203,6 +212,9 @@ def alloc_outputs(cfg: Config, inputs: dict) -> dict:
         return {"y": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev)}
     if cfg.op == "rmsnorm":
         return {"out": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev)}
+    if cfg.op == "rms_heads":
+        return {"out": torch.empty(d["B"], d["L"], d["H"], d["D"], dtype=torch.bfloat16,
+                                   device=dev)}
     if cfg.op == "gemm":
         return {"out": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev)}
     if cfg.op == "add_ln_quant":
@@ -237,6 +249,11 @@ def launch(cfg: Config, t: dict, stream_handle: int, freqs: torch.Tensor | None 
     elif cfg.op == "rmsnorm":
         _abi.call("jo_rmsnorm", p(t["x"]), d["N"], p(t["weight"]), p(t["out"]), d["N"], d["M"],
                   d["N"], _abi.JO_DTYPE_BF16, d["eps"], stream_handle)
+    elif cfg.op == "rms_heads":
+        B, L, H, D = d["B"], d["L"], d["H"], d["D"]
+        k = t["qkv"][:, :, 1]
+        _abi.call("jo_rmsnorm_heads", p(k), 3 * H * D, D, p(t["weight"]), p(t["out"]), D, B * L,
+                  H, D, _abi.JO_DTYPE_BF16, d["eps"], 0, stream_handle)
     elif cfg.op == "qk_table":
         B, L, H, D = d["B"], d["L"], d["H"], d["D"]
         tok = H * D

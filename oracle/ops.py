@@ -94,6 +94,20 @@ def rmsnorm_exact_f32(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Ten
 
 
 # ---------------------------------------------------------------------------
+# torch RMSNorm module — deploy/xvideo/models/dit/dit.py:228-250 (forward
+# :244-249), applied to the text stream's q and k (dit.py:384-385).
+# ---------------------------------------------------------------------------
+def rms_norm_module(x: torch.Tensor, w, eps: float) -> torch.Tensor:
+    """_norm(x.float()).type_as(x) * weight: x * r in fp32 rounded to x's dtype,
+    then the product with the weight (two tensors of that dtype: an fp32
+    product rounded once). r from rms_rstd_exact; w None = a non-affine module."""
+    t = f32_op(torch.mul, x.float(), rms_rstd_exact(x, eps)).to(x.dtype)
+    if w is None:
+        return t
+    return f32_op(torch.mul, t.float(), w.float()).to(x.dtype)
+
+
+# ---------------------------------------------------------------------------
 # (Layer|RMS)Norm + AdaLN — deploy/joyomni_ops/csrc/fused_norm_scale_shift.cu:88-142;
 # formula of test_parity_light.py:47-51 / test_bench.py:91-96.
 # gamma is the affine switch (:125, :192); beta only applies with gamma (:130).

@@ -154,6 +154,13 @@ def build() -> dict[str, np.ndarray]:
     fx.update(gemm_a=a.view(torch.uint8).numpy(), gemm_bt=bt8.view(torch.uint8).numpy(),
               gemm_sa=f32(sa), gemm_sb=f32(sbv), gemm_bias=bits(bias), gemm_out=bits(out),
               gemm_exact=exact.numpy(), gemm_mag=mag.numpy())
+
+    # The torch RMSNorm module (dit.py:244-249) on per-head rows [T, H, D]:
+    # rounded to bf16 before the weight multiply.
+    g = torch.Generator().manual_seed(109)
+    x = (torch.randn(5, 3, 128, generator=g) * 2).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16)
+    fx.update(rmsmod_x=bits(x), rmsmod_w=bits(w), rmsmod_y=bits(ops.rms_norm_module(x, w, 1e-6)))
     return fx
 
 

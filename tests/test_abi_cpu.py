@@ -30,7 +30,8 @@ def test_header_declares_all_entry_points():
     for name in ("jo_last_error", "jo_abi_version", "jo_sgl_per_token_quant_fp8",
                  "jo_fused_qk_norm_rope_3d_paired", "jo_fused_qk_norm_rope_3d_grid",
                  "jo_fused_qk_norm_rope_3d_kvcache", "jo_fused_norm_scale_shift", "jo_rmsnorm",
-                 "jo_fused_add_layernorm_scale_shift", "jo_rmsnorm_quant_fp8"):
+                 "jo_fused_add_layernorm_scale_shift", "jo_rmsnorm_quant_fp8",
+                 "jo_rmsnorm_heads"):
         assert name in fns, name
 
 
@@ -89,6 +90,11 @@ BAD_CALLS = [
     ("jo_fused_norm_scale_shift", (16, 8, None, None, 16, 8, 16, 8, 16, 8, 4, 8, 7, 0, 1e-6, None),
      "dtype"),
     ("jo_rmsnorm", (16, 8, 16, None, 8, 4, 8, 2, 1e-6, None), "null pointer"),
+    ("jo_rmsnorm_heads", (16, 1152, 128, 16, 16, 128, 4, 3, 128, 2, 1e-6, 2, None), "round_first"),
+    ("jo_rmsnorm_heads", (16, 1152, 128, 16, 16, 128, 4, 0, 128, 2, 1e-6, 0, None), "bad shape"),
+    ("jo_rmsnorm_heads", (16, 1152, 64, 16, 16, 128, 4, 3, 128, 2, 1e-6, 0, None), "bad strides"),
+    ("jo_rmsnorm_heads", (16, 1152, 128, None, 16, 128, 4, 3, 128, 2, 1e-6, 1, None), "null pointer"),
+    ("jo_rmsnorm_heads", (16, 1152, 128, 16, 16, 128, 4, 3, 128, 9, 1e-6, 1, None), "dtype"),
     ("jo_fused_add_layernorm_scale_shift",
      (16, 12, 16, 12, None, 0, None, None, 16, 0, 16, 0, 16, 8, 4, 12, 2, 1e-6, None),
      "bad row stride"),
@@ -110,6 +116,8 @@ def test_empty_inputs_are_noops(abi):
     # zero rows / zero tokens: valid, nothing to launch
     assert lib.jo_sgl_per_token_quant_fp8(None, 2, 0, 8, 8, None, 8, None, None) == abi.JO_OK
     assert lib.jo_rmsnorm(None, 8, None, None, 8, 0, 8, 2, 1e-6, None) == abi.JO_OK
+    assert lib.jo_rmsnorm_heads(None, 1152, 128, None, None, 128, 0, 3, 128, 2, 1e-6, 1,
+                                None) == abi.JO_OK
     assert lib.jo_fused_norm_scale_shift(None, 8, None, None, None, 0, None, 0, None, 8, 0, 8, 2,
                                          0, 1e-6, None) == abi.JO_OK
     assert lib.jo_fused_qk_norm_rope_3d_paired(None, None, 1, 0, 2, 128, 0, 256, 0, 256, 1e-6,

@@ -166,3 +166,12 @@ def test_golden_fp8_scaled_mm(fx, dev):
     tol = exact.abs() * 2.0 ** -8 + mag * 2.0 ** -14 + 1e-6
     err = (out.cpu().double() - exact).abs()
     assert bool((err <= tol).all()), f"gemm: max err/tol {(err / tol).max().item():.3f}"
+
+
+@pytest.mark.gpu
+def test_golden_rms_norm_module(fx, dev):
+    from joyomni_ops import dit_ops
+    x = bf16(fx["rmsmod_x"]).to(dev)
+    y = dit_ops.rms_norm_module(x, bf16(fx["rmsmod_w"]).to(dev), 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), bf16(fx["rmsmod_y"])), "module rmsnorm differs"

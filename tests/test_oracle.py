@@ -141,6 +141,70 @@ def test_rmsnorm_oracle_matches_library_and_invariant():
     assert torch.allclose(unit.pow(2).mean(-1), torch.ones(64), rtol=1e-5)
 
 
+def _module_forward_torch(x, w, eps):
+    """RMSNorm.forward as dit.py:244-249 writes it, evaluated by torch on the CPU
+    (its own fp32 summation order and rsqrt)."""
+    xf = x.float()
+    out = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).type_as(x)
+    return out if w is None else out * w
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("affine", [True, False])
+def test_rms_norm_module_oracle_matches_the_module_formula(dtype, affine):
+    """Against the module's own torch expression: equal wherever torch's fp32
+    r agrees with the exactly rounded one (nearly everywhere), within one
+    ulp of the intermediate row (times |w|) elsewhere."""
+    g = torch.Generator().manual_seed(21)
+    x = (torch.randn(512, 4, 128, generator=g) * 2).to(dtype)
+    w = (1 + 0.1 * torch.randn(128, generator=g)).to(dtype) if affine else None
+    ref = _module_forward_torch(x, w, 1e-6).float()
+    out = ops.rms_norm_module(x, w, 1e-6).float()
+    assert out.dtype == ref.dtype and out.shape == ref.shape
+    same = (out == ref).float().mean().item()
+    assert same > 0.995, same
+    mb = 7 if dtype == torch.bfloat16 else 10
+    wf = torch.ones(128) if w is None else w.float().abs()
+    ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -30))) - mb)
+    assert bool(((out - ref).abs() <= 2 * ulp * torch.maximum(wf, torch.ones(128))).all())
+
+
+def test_rms_norm_module_oracle_rounds_before_the_weight():
+    """A planted slip — no rounding between x * r and the weight (the kernel
+    rmsnorm's single rounding) — differs from the oracle on a visible share of
+    elements; with a unit weight the two coincide."""
+    g = torch.Generator().manual_seed(22)
+    x = torch.randn(256, 128, generator=g).to(torch.bfloat16)
+    w = (1 + 0.3 * torch.randn(128, generator=g)).to(torch.bfloat16)
+    out = ops.rms_norm_module(x, w, 1e-6)
+    slip = ops.rmsnorm_exact_f32(x, w, 1e-6).to(torch.bfloat16)
+    assert (out != slip).float().mean().item() > 0.05
+    one = torch.ones(128, dtype=torch.bfloat16)
+    assert torch.equal(ops.rms_norm_module(x, one, 1e-6),
+                       ops.rmsnorm_exact_f32(x, one, 1e-6).to(torch.bfloat16))
+    assert torch.equal(ops.rms_norm_module(x, None, 1e-6), ops.rms_norm_module(x, one, 1e-6))
+
+
+def test_rms_norm_module_oracle_special_rows():
+    """Closed forms: a zero row stays zero; a row of +-a has r = 1/sqrt(a^2 + eps)
+    (fp32 ops), so every element is round(+-a * r); NaN spreads over its row;
+    an inf makes r = 0 (inf element NaN, the rest zero)."""
+    x = torch.zeros(4, 64)
+    x[1] = 3.0
+    x[1, ::2] = -3.0
+    x[2, 5] = float("nan")
+    x[3, 7] = float("inf")
+    x = x.to(torch.bfloat16)
+    out = ops.rms_norm_module(x, None, 1e-6).float()
+    assert bool((out[0] == 0).all())
+    f32 = np.float32
+    r32 = f32(1) / np.sqrt(f32(9) + f32(1e-6))  # numpy: IEEE fp32 add, sqrt, division
+    expect = (torch.tensor(3.0) * torch.tensor(float(r32))).to(torch.bfloat16).float()
+    assert bool((out[1, 1::2] == expect).all()) and bool((out[1, ::2] == -expect).all())
+    assert bool(torch.isnan(out[2]).all())
+    assert torch.isnan(out[3, 7]) and bool((out[3, :7] == 0).all()) and bool((out[3, 8:] == 0).all())
+
+
 @pytest.mark.parametrize("affine", [False, True])
 def test_layernorm_modulate_oracle_matches_library(affine):
     g = torch.Generator().manual_seed(5)
