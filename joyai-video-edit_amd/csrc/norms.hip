@@ -301,12 +301,12 @@ int launch_norm_mod(const NormArgs& a, hipStream_t stream, const char* op) {
              (a.gs * b) % 16 == 0;
   bool launched = false;
   if (vec_ok) {
-    launched = dispatch_row_shape<Tag::kVec, true>(a.N, [&](auto lpr, auto ch) {
+    launched = dispatch_row_shape<Tag::kVec, true, 256>(a.N, [&](auto lpr, auto ch) {
       constexpr int LPR = decltype(lpr)::value;
       constexpr int CH = decltype(ch)::value;
       hipLaunchKernelGGL((norm_mod_kernel<Tag, LPR, CH, NT, ADD, QNT>),
                          dim3(row_blocks(a.M, LPR)), dim3(kBlock), 0, stream, a);
-    });
+    }, a.M);
   }
   if (!launched)
     hipLaunchKernelGGL((norm_mod_generic_kernel<Tag, NT, ADD, QNT>), dim3(a.M), dim3(kBlock), 0,

@@ -103,13 +103,13 @@ int launch_quant(const void* x, int64_t M, int64_t N, int64_t xs, void* q, int64
                       aligned(q, 8) && (qs % 8 == 0);
   bool launched = false;
   if (vec_ok) {
-    launched = dispatch_row_shape<8>(N, [&](auto lpr, auto ch) {
+    launched = dispatch_row_shape<8, false, 128>(N, [&](auto lpr, auto ch) {
       constexpr int LPR = decltype(lpr)::value;
       constexpr int CH = decltype(ch)::value;
       hipLaunchKernelGGL((quant_rows_kernel<Tag, LPR, CH>), dim3(row_blocks(M, LPR)), dim3(kBlock),
                          0, stream, x, xs, static_cast<uint8_t*>(q), qs, s, M,
                          static_cast<int>(N));
-    });
+    }, M);
   }
   if (!launched) {
     hipLaunchKernelGGL((quant_generic_kernel<Tag>), dim3(M), dim3(kBlock), 0, stream, x, xs,

@@ -110,7 +110,7 @@ def test_norm_quant_matches_unfused_pair(abi, dev, stream_handle, dtype, M, N, n
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("N", [3072, 100])
+@pytest.mark.parametrize("N", [3072, 4096, 100])
 def test_norm_quant_nonfinite_and_special_rows(abi, dev, stream_handle, dtype, N):
     """NaN / inf inputs, a constant row (LN -> y = shift), a zero row with zero
     modulation (scale 0, inv 0), and y overflowing the 16-bit range."""

@@ -43,7 +43,8 @@ def assert_quant_equal(q, s, x_cpu, what):
 
 
 SHAPES = [(1, 4), (3, 12), (7, 64), (33, 128), (5, 256), (9, 512), (17, 1000), (17, 3072),
-          (64, 4096), (9, 8192), (3, 16384), (2, 32768), (2, 40000), (5, 100), (4, 1020), (1, 8)]
+          (64, 4096), (8191, 4096), (8192, 4096), (9, 8192), (3, 16384), (2, 32768), (2, 40000),
+          (5, 100), (4, 1020), (1, 8)]   # 4096-wide rows: two waves per row below 8192 rows
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -86,7 +87,7 @@ def inject_nonfinite(x: torch.Tensor, seed: int) -> torch.Tensor:
     return x
 
 
-@pytest.mark.parametrize("N", [64, 3072, 16384])
+@pytest.mark.parametrize("N", [64, 3072, 4096, 16384])
 def test_quant_nonfinite_rows(abi, dev, stream_handle, N):
     """Rows with NaN/inf and rows whose inverse scale overflows take the
     clamped path; finite rows sharing their workgroup must be unaffected."""
