@@ -10,7 +10,9 @@ residual + LayerNorm + AdaLN with the per-token FP8 epilogue, C2 shape) and
 N4 (the graph runner's 40-layer KV-pool commit at the deployment shape), and
 the FP8 GEMMs G1-G4 (fp8_scaled_mm at Fp8Linear's deployment shapes), whose
 lines add TFLOP/s against the 5.0 PFLOP/s dense fp8 matrix-core peak and the
-time of torch._scaled_mm (hipBLASLt) on the same operands. R_* are the
+time of torch._scaled_mm (hipBLASLt) on the same operands (both launched
+eagerly in alternating blocks over the same rotating operand sets:
+ab_eager_us_per_call, hipblaslt_us_per_call, hipblaslt_over_ours). R_* are the
 reference-signature ops at the DiT block's deployment shapes (hidden 4096,
 32 heads, 3120 tokens): table-mode QK norm + RoPE, LayerNorm with per-row
 modulation, per-token quant of [3120, 4096] and [3120, 16384], and the
@@ -147,34 +149,61 @@ def time_gpu(cfg, steps: int, warmup: int, dev, use_graph: bool = True) -> dict:
             "rotated_mb": round(n_sets * set_bytes / 1e6, 1), "timing": "hip-graph"}
 
 
-def hipblaslt_us(cfg, dev, iters: int = 20):
-    """torch._scaled_mm (hipBLASLt) on a GEMM config's operands, row-wise scales
-    and bias — the vendor library's time for the same problem. None if this
-    torch build cannot run it."""
+def gemm_vs_hipblaslt(cfg, dev, rounds: int = 7, calls: int = 10):
+    """This build's GEMM and torch._scaled_mm (hipBLASLt; row-wise scales and
+    bias) on the same operands, both launched eagerly, rotating over the same
+    >= 640 MB of operand sets, in alternating blocks of `calls` launches so
+    that clock and power drift reach both alike. Returns the medians over
+    `rounds` blocks of (ours, hipBLASLt) per-call times, or None if this torch
+    build cannot run torch._scaled_mm."""
     if cfg.op != "gemm":
         return None
     import torch
     from joyomni_ops import workloads as W
     d = cfg.dims
-    t = {k: v.to(dev) for k, v in W.make_inputs(cfg).items()}
-    a = t["a"].view(torch.float8_e4m3fn)
-    b = t["w"].view(torch.float8_e4m3fn).t()
-    sa, sb = t["sa"].view(d["M"], 1), t["sb"].view(1, d["N"])
+    host = W.make_inputs(cfg)
+    set_bytes = tensor_bytes(host) + tensor_bytes(W.alloc_outputs(cfg, host))
+    n_sets = max(4, math.ceil(ROT_BYTES / set_bytes))
+    sets = []
+    for _ in range(n_sets):
+        t = {k: v.to(dev) for k, v in host.items()}
+        t.update(W.alloc_outputs(cfg, t))
+        sets.append(t)
+    cur = torch.cuda.current_stream(dev)
+
+    def ours(i):
+        W.launch(cfg, sets[i % n_sets], cur.cuda_stream)
+
+    def lib(i):
+        t = sets[i % n_sets]
+        torch._scaled_mm(t["a"].view(torch.float8_e4m3fn), t["w"].view(torch.float8_e4m3fn).t(),
+                         scale_a=t["sa"].view(d["M"], 1), scale_b=t["sb"].view(1, d["N"]),
+                         out_dtype=torch.bfloat16, bias=t["bias"])
+
     try:
-        for _ in range(3):
-            torch._scaled_mm(a, b, scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16, bias=t["bias"])
+        for i in range(3):
+            lib(i)
         torch.cuda.synchronize()
     except Exception as ex:  # noqa: BLE001 - report, do not fail the bench
         log(f"torch._scaled_mm unavailable: {str(ex)[:120]}")
         return None
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(iters):
-        torch._scaled_mm(a, b, scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16, bias=t["bias"])
-    e1.record()
-    torch.cuda.synchronize()
-    del t
-    return round(e0.elapsed_time(e1) * 1000.0 / iters, 2)
+
+    def block(fn, first):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        for i in range(calls):
+            fn(first + i)
+        e1.record(cur)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / calls
+
+    t_ours, t_lib = [], []
+    for r in range(rounds):
+        t_ours.append(block(ours, r * calls))
+        t_lib.append(block(lib, r * calls))
+    del sets
+    torch.cuda.empty_cache()
+    return round(statistics.median(t_ours), 2), round(statistics.median(t_lib), 2)
 
 
 def torch_reference_us(cfg, dev, iters: int = 10):
@@ -376,10 +405,12 @@ def main() -> int:
             results[n].pop("frac_of_peak", None)
             results[n].update(bound="mfma", algorithmic_flops=flops, tflops=round(tf, 1),
                               frac_of_fp8_peak=round(tf / PEAK_FP8_TFLOPS, 4))
-            lib_us = hipblaslt_us(cfg, dev)
-            if lib_us is not None:
-                results[n]["hipblaslt_us_per_call"] = lib_us
-                results[n]["hipblaslt_tflops"] = round(flops / (lib_us * 1e-6) / 1e12, 1)
+            ab = gemm_vs_hipblaslt(cfg, dev)
+            if ab is not None:
+                results[n]["ab_eager_us_per_call"] = ab[0]
+                results[n]["hipblaslt_us_per_call"] = ab[1]
+                results[n]["hipblaslt_tflops"] = round(flops / (ab[1] * 1e-6) / 1e12, 1)
+                results[n]["hipblaslt_over_ours"] = round(ab[1] / ab[0], 3)
         log(f"{n}: {results[n]}")
     copy = None
     if args.copy_mb:
