@@ -134,6 +134,29 @@ def test_fp8_scaled_mm_deployment_shapes_sampled_rows(dev, N, K):
     check(out.cpu()[rows], a, w.t(), sa, sb, bias, f"[{M},{N},{K}] sampled", rows=rows)
 
 
+def test_fp8_linear_reference_bench_shape(dev):
+    """The reference benchmark's FP8 linear (test_bench.py:160-200): x [4096, 4096]
+    bf16 through Fp8Linear's per-token quantization and the GEMM with a
+    per-channel quantized [4096, 4096] weight. Sampled rows against the exact
+    oracle of the quantized operands; and, as the reference reports it, the
+    error against the unquantized product (fp8 e4m3 operands: a few percent)."""
+    from joyomni_ops import dit_ops
+    g = torch.Generator().manual_seed(4096)
+    M = N = K = 4096
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    wq, ws = dit_ops.quantize_weight_per_channel(w.to(dev))
+    y = dit_ops.fp8_linear(x.to(dev), wq, ws)
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.randperm(M, generator=g)[:24], torch.arange(M - 8, M)])
+    xq, xs = ops.per_token_quant_fp8(x[rows])
+    check(y.cpu()[rows], xq.view(torch.float8_e4m3fn), wq.cpu(), xs, ws.cpu(), None,
+          "fp8_linear 4096^3 sampled")
+    exact = x[rows].double() @ w.double().t()
+    rel = ((y.cpu()[rows].double() - exact).norm() / exact.norm()).item()
+    assert rel < 0.08, rel
+
+
 def test_fp8_linear_shim_and_rejects(dev):
     """dit_ops.fp8_linear == per-token quantization + GEMM (Fp8Linear.forward),
     with the weight prepared like Fp8Linear.from_linear; reference errors."""
