@@ -31,6 +31,12 @@ Deployment shapes through the reference-signature entry points (reported):
           packed qkv [1, 3120, 3, 32, 128] (jo_rmsnorm_heads; the reference
           first copies that slice with .contiguous())
 
+The shapes of the reference's own benchmark script (test_bench.py; reported):
+  T_rms   rmsnorm, x [4096, 4096]
+  T_ln    fused_norm_scale_shift, x [4096, 4096] with per-row scale / shift
+  T_qk    fused_qk_norm_rope_3d_paired, q,k [1, 1560, 32, 128]
+  T_gemm  fp8_scaled_mm 4096 x 4096 x 4096
+
 Inputs are generated on the CPU with torch.Generator().manual_seed(s)
 (s = config index) in fp32, cast to bf16, and copied to the device, so the
 CPU oracle and the GPU see identical tensors. Outliers: exactly
@@ -79,6 +85,12 @@ CONFIGS: dict[str, Config] = {
     "R_q16k": Config("R_q16k", "quant", 13, dict(M=3120, K=16384)),
     "R_rms": Config("R_rms", "rmsnorm", 14, dict(M=99840, N=128, eps=1e-6)),
     "R_kn": Config("R_kn", "rms_heads", 16, dict(B=1, L=3120, H=32, D=128, eps=1e-6)),
+    # The shapes of the reference's own benchmark script
+    # (deploy/joyomni_ops/tests/test_bench.py:59-200); reported, not gated.
+    "T_rms": Config("T_rms", "rmsnorm", 17, dict(M=4096, N=4096, eps=1e-6)),
+    "T_ln": Config("T_ln", "ln_rows", 18, dict(M=4096, N=4096, eps=1e-6)),
+    "T_qk": Config("T_qk", "qk_table", 19, dict(B=1, L=1560, H=32, D=128, eps=1e-6)),
+    "T_gemm": Config("T_gemm", "gemm", 20, dict(M=4096, N=4096, K=4096)),
 }
 
 
