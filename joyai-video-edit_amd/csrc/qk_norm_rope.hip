@@ -102,8 +102,8 @@ __device__ __forceinline__ void grid_pair_cs(float pos, float f, float source_id
 }
 
 // SPLIT = 1: one wave does q and k of its token. SPLIT = 2: two waves per
-// token, one for q and one for k. SPLIT = 4: four waves per token, q and k
-// each split into two halves of their head groups. The rotation coefficients
+// token, one for q and one for k. SPLIT = 4 (8): four (eight) waves per
+// token, q and k each split into two (four) parts of their head groups. The rotation coefficients
 // are evaluated by every wave.
 //
 // Issue order matters: the memory counter retires loads in order, so the
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
   // consecutive rows of one tensor (measured against interleaving q and k
   // waves per token: [1, 3510, 24, 128] 16.38 -> 16.15 us, C3 43.9 -> 43.4 us,
   // table mode at [1, 3120, 32, 128] 19.0 -> 18.7 us). part: bit 0 = k, bit 1
-  // = second half of the head groups (SPLIT == 4).
+  // and up = the part of the head groups (SPLIT >= 4).
   int64_t tok;
   int part;
   if constexpr (SPLIT == 1) {
@@ -168,11 +168,13 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
     dst[0] = is_k ? kdst : qrow;
     wsrc[0] = static_cast<const char*>(is_k ? a.kw : a.qw);
   }
-  // Head groups (512 elements each) this wave handles: all, or one half.
+  // Head groups (512 elements each) this wave handles: all of its tensor's,
+  // or one of SPLIT / 2 equal parts of them.
+  constexpr int kParts = SPLIT >= 4 ? SPLIT / 2 : 1;
   const int all_groups = (a.row_elems + 511) / 512;
-  const int half_groups = (all_groups + 1) / 2;
-  const int gbeg = SPLIT == 4 ? (part >> 1) * half_groups : 0;
-  const int groups = SPLIT == 4 ? min(all_groups, gbeg + half_groups) : all_groups;
+  const int part_groups = (all_groups + kParts - 1) / kParts;
+  const int gbeg = (part >> 1) * part_groups;
+  const int groups = min(all_groups, gbeg + part_groups);
 
   // 1. Parameter loads: rotation table row or frequencies, weights.
   u32x2 cw, sw;
@@ -285,21 +287,28 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
 // saved rotation-coefficient work. Four (each of q and k split into halves of
 // its head groups) helps further when the grid is small (3510 tokens:
 // 17.3 -> 17.0 us) and costs at 10530 tokens (44.5 -> 45.5 us), so it is used
-// below 8192 tokens. JO_QK_SPLIT=1|2|4 overrides the choice (launch shape
-// only; results are identical).
+// below 8192 tokens. Eight (quarters of q's and k's head groups) helps
+// further where the groups divide evenly into quarters of two or more
+// ([1, 3120, 32, 128] tables 18.6 -> 18.0 us, [1, 1560, 32, 128] 11.3 ->
+// 10.4 us); with 24 heads (six groups) a quarter would be 1.5 groups and it
+// costs ([1, 3510, 24, 128] 16.1 -> 18.5 us). JO_QK_SPLIT=1|2|4|8 overrides
+// the choice (launch shape only; results are identical).
 int qk_split(int64_t tokens, int all_groups) {
   const char* e = getenv("JO_QK_SPLIT");
   const int forced = e ? atoi(e) : 0;
   if (forced == 1 || forced == 2) return forced;
-  if (forced == 4) return all_groups >= 2 ? 4 : 2;
-  return (tokens < 8192 && all_groups >= 2) ? 4 : 2;
+  if (forced == 8 && all_groups >= 4) return 8;
+  if (forced == 4 || forced == 8) return all_groups >= 2 ? 4 : 2;
+  if (tokens >= 8192 || all_groups < 2) return 2;
+  return (all_groups >= 8 && all_groups % 4 == 0) ? 8 : 4;
 }
 
 template <int MODE>
 int launch_qk(const QKArgs& a, int head_dim, hipStream_t stream, const char* op) {
   const int all_groups = (a.row_elems + 511) / 512;
   const int split = qk_split(a.tokens, all_groups);
-  const int groups = split == 4 ? (all_groups + 1) / 2 : all_groups;  // per wave
+  const int parts = split >= 4 ? split / 2 : 1;
+  const int groups = (all_groups + parts - 1) / parts;  // per wave
   const dim3 grid(static_cast<unsigned>((a.tokens * split + 3) / 4));
   auto go = [&](auto hd, auto sp) {
     constexpr int HD = decltype(hd)::value;
@@ -318,7 +327,9 @@ int launch_qk(const QKArgs& a, int head_dim, hipStream_t stream, const char* op)
       hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 8, MODE, S>), grid, dim3(kBlock), 0, stream, a);
   };
   auto go_hd = [&](auto hd) {
-    if (split == 4)
+    if (split == 8)
+      go(hd, std::integral_constant<int, 8>{});
+    else if (split == 4)
       go(hd, std::integral_constant<int, 4>{});
     else if (split == 2)
       go(hd, std::integral_constant<int, 2>{});
