@@ -285,22 +285,23 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
 // than one at every BASELINE shape (3510 tokens: 19.0 -> 17.5 us; 10530
 // tokens: 46.4 -> 45.2 us): the extra waves hide HBM latency better than the
 // saved rotation-coefficient work. Four (each of q and k split into halves of
-// its head groups) helps further when the grid is small (3510 tokens:
-// 17.3 -> 17.0 us) and costs at 10530 tokens (44.5 -> 45.5 us), so it is used
-// below 8192 tokens. Eight (quarters of q's and k's head groups) helps
-// further where the groups divide evenly into quarters of two or more
-// ([1, 3120, 32, 128] tables 18.6 -> 18.0 us, [1, 1560, 32, 128] 11.3 ->
-// 10.4 us); with 24 heads (six groups) a quarter would be 1.5 groups and it
-// costs ([1, 3510, 24, 128] 16.1 -> 18.5 us). JO_QK_SPLIT=1|2|4|8 overrides
+// its head groups) is faster again, at 3510 tokens (17.3 -> 17.0 us) and, once
+// the waves of q precede those of k, at 10530 (C3 42.8 -> 41.7 us). Eight
+// (quarters) helps further on small grids whose groups divide evenly into
+// quarters of two or more ([1, 3120, 32, 128] tables 18.6 -> 18.0 us,
+// [1, 1560, 32, 128] 11.3 -> 10.4 us); with 24 heads (six groups) a quarter
+// would be 1.5 groups and it costs ([1, 3510, 24, 128] 16.1 -> 18.5 us); six
+// (thirds) measured level with four there. JO_QK_SPLIT=1|2|4|6|8 overrides
 // the choice (launch shape only; results are identical).
 int qk_split(int64_t tokens, int all_groups) {
   const char* e = getenv("JO_QK_SPLIT");
   const int forced = e ? atoi(e) : 0;
   if (forced == 1 || forced == 2) return forced;
   if (forced == 8 && all_groups >= 4) return 8;
-  if (forced == 4 || forced == 8) return all_groups >= 2 ? 4 : 2;
-  if (tokens >= 8192 || all_groups < 2) return 2;
-  return (all_groups >= 8 && all_groups % 4 == 0) ? 8 : 4;
+  if (forced == 6 && all_groups >= 3) return 6;
+  if (forced == 4 || forced == 6 || forced == 8) return all_groups >= 2 ? 4 : 2;
+  if (all_groups < 2) return 2;
+  return (tokens < 8192 && all_groups >= 8 && all_groups % 4 == 0) ? 8 : 4;
 }
 
 template <int MODE>
@@ -329,6 +330,8 @@ int launch_qk(const QKArgs& a, int head_dim, hipStream_t stream, const char* op)
   auto go_hd = [&](auto hd) {
     if (split == 8)
       go(hd, std::integral_constant<int, 8>{});
+    else if (split == 6)
+      go(hd, std::integral_constant<int, 6>{});
     else if (split == 4)
       go(hd, std::integral_constant<int, 4>{});
     else if (split == 2)

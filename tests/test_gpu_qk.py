@@ -17,10 +17,10 @@ from joyomni_ops import workloads as W
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["auto", "1", "2", "4", "8"], autouse=True)
+@pytest.fixture(params=["auto", "1", "2", "4", "6", "8"], autouse=True)
 def qk_split(request, monkeypatch):
-    """Run every QK test with the automatic launch shape and with one, two, four
-    and eight waves per token forced (JO_QK_SPLIT): results must not depend on it."""
+    """Run every QK test with the automatic launch shape and with one, two, four,
+    six and eight waves per token forced (JO_QK_SPLIT): results must not depend on it."""
     if request.param != "auto":
         monkeypatch.setenv("JO_QK_SPLIT", request.param)
     else:
