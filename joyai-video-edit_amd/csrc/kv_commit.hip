@@ -13,11 +13,15 @@
 // columns of a pair), so any table the reference's builders produce is
 // reproduced bit for bit.
 //
-// One wave64 per (layer, batch, token) row of H*D elements: 16-byte streaming
-// loads/stores, the row in registers, V copied by the same wave. A lane's
-// table columns repeat every head (512 elements per pass is a whole number
-// of heads when D divides 512), so a lane reads its 8 cos and 8 sin values
-// once per row.
+// One wave64 per (layer, batch, token) row of H*D elements and tensor: 16-byte
+// streaming loads/stores, the row in registers; the V rows are copied by
+// waves of their own, after all the K waves. A lane's table columns repeat
+// every head (512 elements per pass is a whole number of heads when D divides
+// 512), so a lane reads its 8 cos and 8 sin values once per row.
+#include <stdlib.h>
+
+#include <type_traits>
+
 #include "jo_device.hpp"
 #include "jo_host.hpp"
 
@@ -52,12 +56,16 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float c0, float s0
   o1 = c + d;
 }
 
-template <class Tag, int CH>
+// KV2: K rows and V rows on separate waves, all K waves first (each wave
+// streams one tensor; a V wave is a plain copy and reads no table).
+template <class Tag, int CH, bool KV2>
 __global__ __launch_bounds__(kBlock) void rope_commit_kernel(const CommitArgs a) {
   static_assert(Tag::kVec == 8, "16-bit rows");
   const int lane = threadIdx.x % kWave;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + threadIdx.x / kWave;
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + threadIdx.x / kWave;
   const int64_t rows = a.layers * a.batch * a.tokens;
+  const bool v_wave = KV2 && wid >= rows;  // wave-uniform
+  const int64_t row = v_wave ? wid - rows : wid;
   if (row >= rows) return;
   const int64_t n = row % a.tokens;
   const int64_t lb = row / a.tokens;
@@ -65,52 +73,59 @@ __global__ __launch_bounds__(kBlock) void rope_commit_kernel(const CommitArgs a)
   const int64_t l = lb / a.batch;
   const int64_t so = l * a.s_ls + b * a.s_bs + n * a.s_ts;
   const int64_t dof = l * a.d_ls + b * a.d_bs + (a.d_off + n) * a.d_ts;
-  const bool has_v = a.src_v != nullptr;
+  const bool do_k = !v_wave;
+  const bool do_v = a.src_v != nullptr && (!KV2 || v_wave);
 
-  // Table columns of this lane (same in every chunk: 512 % D == 0).
-  const int d0 = (lane * 8) % a.head_dim;
-  const float* ct = a.cos + b * a.tab_bs + n * a.tab_ts + d0;
-  const float* st = a.sin + b * a.tab_bs + n * a.tab_ts + d0;
-  const u32x4 c_lo = ld16(ct), c_hi = ld16(ct + 4);
-  const u32x4 s_lo = ld16(st), s_hi = ld16(st + 4);
-
-  // Loads are never predicated (a predicated load's join forces an early
-  // wait): a chunk beyond the row reads a chunk inside it instead and is
-  // never stored.
+  // Loads are never predicated per lane (a predicated load's join forces an
+  // early wait): a chunk beyond the row reads a chunk inside it instead and
+  // is never stored. The branches below are uniform over the wave.
   const int e_safe = (lane * 8) % a.row_elems;
   u32x4 k[CH], v[CH];
+  u32x4 c_lo, c_hi, s_lo, s_hi;
+  if (do_k) {
+    // Table columns of this lane (same in every chunk: 512 % D == 0).
+    const int d0 = (lane * 8) % a.head_dim;
+    const float* ct = a.cos + b * a.tab_bs + n * a.tab_ts + d0;
+    const float* st = a.sin + b * a.tab_bs + n * a.tab_ts + d0;
+    c_lo = ld16(ct);
+    c_hi = ld16(ct + 4);
+    s_lo = ld16(st);
+    s_hi = ld16(st + 4);
 #pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const int e = i * 512 + lane * 8;
-    k[i] = ld16_nt(byte_off(a.src_k, (so + (e < a.row_elems ? e : e_safe)) * Tag::kBytes));
+    for (int i = 0; i < CH; ++i) {
+      const int e = i * 512 + lane * 8;
+      k[i] = ld16_nt(byte_off(a.src_k, (so + (e < a.row_elems ? e : e_safe)) * Tag::kBytes));
+    }
   }
-  if (has_v) {
+  if (do_v) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int e = i * 512 + lane * 8;
       v[i] = ld16_nt(byte_off(a.src_v, (so + (e < a.row_elems ? e : e_safe)) * Tag::kBytes));
     }
   }
-  float cs[8], sn[8];
+  if (do_k) {
+    float cs[8], sn[8];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    cs[j] = elem<F32>(c_lo, j);
-    cs[j + 4] = elem<F32>(c_hi, j);
-    sn[j] = elem<F32>(s_lo, j);
-    sn[j + 4] = elem<F32>(s_hi, j);
+    for (int j = 0; j < 4; ++j) {
+      cs[j] = elem<F32>(c_lo, j);
+      cs[j + 4] = elem<F32>(c_hi, j);
+      sn[j] = elem<F32>(s_lo, j);
+      sn[j + 4] = elem<F32>(s_hi, j);
+    }
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int e = i * 512 + lane * 8;
+      if (e >= a.row_elems) continue;
+      float o[8];
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+        rope_pair(elem<Tag>(k[i], 2 * p), elem<Tag>(k[i], 2 * p + 1), cs[2 * p], sn[2 * p],
+                  cs[2 * p + 1], sn[2 * p + 1], o[2 * p], o[2 * p + 1]);
+      st16_nt(byte_off(a.dst_k, (dof + e) * Tag::kBytes), pack<Tag>(o));
+    }
   }
-#pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const int e = i * 512 + lane * 8;
-    if (e >= a.row_elems) continue;
-    float o[8];
-#pragma unroll
-    for (int p = 0; p < 4; ++p)
-      rope_pair(elem<Tag>(k[i], 2 * p), elem<Tag>(k[i], 2 * p + 1), cs[2 * p], sn[2 * p],
-                cs[2 * p + 1], sn[2 * p + 1], o[2 * p], o[2 * p + 1]);
-    st16_nt(byte_off(a.dst_k, (dof + e) * Tag::kBytes), pack<Tag>(o));
-  }
-  if (has_v) {
+  if (do_v) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int e = i * 512 + lane * 8;
@@ -161,18 +176,30 @@ int launch_commit(const CommitArgs& a, hipStream_t stream) {
                       aligned(a.cos, 16) && aligned(a.sin, 16) && a.tab_ts % 4 == 0 &&
                       a.tab_bs % 4 == 0;
   const int chunks = (a.row_elems + 511) / 512;
-  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  // K and V on separate waves: 40 x 1560 x [32, 128] 357 -> 340 us (twice the
+  // waves, each streaming one tensor). JO_KV_SPLIT=1 keeps them on one wave
+  // (launch shape only; results are identical).
+  const char* env = getenv("JO_KV_SPLIT");
+  const bool kv2 = a.src_v != nullptr && !(env && atoi(env) == 1);
+  const dim3 grid(static_cast<unsigned>(((kv2 ? 2 : 1) * rows + 3) / 4));
   bool launched = true;
+  auto go = [&](auto ch) {
+    constexpr int CH = decltype(ch)::value;
+    if (kv2)
+      hipLaunchKernelGGL((rope_commit_kernel<Tag, CH, true>), grid, dim3(kBlock), 0, stream, a);
+    else
+      hipLaunchKernelGGL((rope_commit_kernel<Tag, CH, false>), grid, dim3(kBlock), 0, stream, a);
+  };
   if (vec_ok && chunks <= 1)
-    hipLaunchKernelGGL((rope_commit_kernel<Tag, 1>), grid, dim3(kBlock), 0, stream, a);
+    go(std::integral_constant<int, 1>{});
   else if (vec_ok && chunks <= 2)
-    hipLaunchKernelGGL((rope_commit_kernel<Tag, 2>), grid, dim3(kBlock), 0, stream, a);
+    go(std::integral_constant<int, 2>{});
   else if (vec_ok && chunks <= 4)
-    hipLaunchKernelGGL((rope_commit_kernel<Tag, 4>), grid, dim3(kBlock), 0, stream, a);
+    go(std::integral_constant<int, 4>{});
   else if (vec_ok && chunks <= 6)
-    hipLaunchKernelGGL((rope_commit_kernel<Tag, 6>), grid, dim3(kBlock), 0, stream, a);
+    go(std::integral_constant<int, 6>{});
   else if (vec_ok && chunks <= 8)
-    hipLaunchKernelGGL((rope_commit_kernel<Tag, 8>), grid, dim3(kBlock), 0, stream, a);
+    go(std::integral_constant<int, 8>{});
   else
     launched = false;
   if (!launched)

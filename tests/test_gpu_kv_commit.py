@@ -17,6 +17,18 @@ from oracle import ops
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(params=["auto", "1", "2"], autouse=True)
+def kv_split(request, monkeypatch):
+    """Every commit test with the automatic launch shape and with K and V on
+    the same wave (1) or on separate waves (2) forced (JO_KV_SPLIT): results
+    must not depend on it."""
+    if request.param != "auto":
+        monkeypatch.setenv("JO_KV_SPLIT", request.param)
+    else:
+        monkeypatch.delenv("JO_KV_SPLIT", raising=False)
+    return request.param
+
+
 def tables(B, T, D, seed, per_batch=False):
     """fp32 cos/sin [T, D] (or [B, T, D]) from random angles up to 200 rad,
     repeat-interleaved like rope.py:50-51, with a few unequal pair columns so
