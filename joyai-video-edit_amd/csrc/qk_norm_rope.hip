@@ -102,9 +102,9 @@ __device__ __forceinline__ void grid_pair_cs(float pos, float f, float source_id
 }
 
 // SPLIT = 1: one wave does q and k of its token. SPLIT = 2: two waves per
-// token, one for q and one for k. SPLIT = 4 (8): four (eight) waves per
-// token, q and k each split into two (four) parts of their head groups. The rotation coefficients
-// are evaluated by every wave.
+// token, one for q and one for k. SPLIT = 4, 6, 8: that many waves per token,
+// q and k each split into SPLIT / 2 parts of their head groups. The rotation
+// coefficients are evaluated by every wave.
 //
 // Issue order matters: the memory counter retires loads in order, so the
 // small parameter loads (rotation table or frequencies, weights) go out
@@ -354,7 +354,9 @@ int check_qk(const char* op, const void* q, const void* k, int64_t batch, int64_
   JO_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
              "Unsupported head_dim for %s: %lld", op, static_cast<long long>(head_dim));
   JO_REQUIRE(batch >= 0 && seq_len >= 0 && num_heads > 0, "%s: bad shape", op);
-  JO_REQUIRE(seq_len <= INT32_MAX && num_heads * head_dim <= INT32_MAX, "%s: shape too large", op);
+  JO_REQUIRE(seq_len <= INT32_MAX && num_heads * head_dim <= INT32_MAX &&
+                 batch * seq_len <= INT32_MAX / 8,
+             "%s: shape too large", op);
   JO_REQUIRE(q_ts >= num_heads * head_dim && k_ts >= num_heads * head_dim,
              "%s: token stride smaller than num_heads*head_dim", op);
   JO_REQUIRE(q_bs >= 0 && k_bs >= 0, "%s: negative batch stride", op);
