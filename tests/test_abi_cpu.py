@@ -89,6 +89,9 @@ BAD_CALLS = [
      "divisible by 4"),
     ("jo_fused_norm_scale_shift", (16, 8, None, None, 16, 8, 16, 8, 16, 8, 4, 8, 7, 0, 1e-6, None),
      "dtype"),
+    ("jo_fused_qk_norm_rope_3d_paired",
+     (16, 16, 2, 1 << 28, 2, 128, 256 << 28, 256, 256 << 28, 256, 1e-6, 16, 16, 16, 16, None),
+     "shape too large"),
     ("jo_rmsnorm", (16, 8, 16, None, 8, 4, 8, 2, 1e-6, None), "null pointer"),
     ("jo_rmsnorm_heads", (16, 1152, 128, 16, 16, 128, 4, 3, 128, 2, 1e-6, 2, None), "round_first"),
     ("jo_rmsnorm_heads", (16, 1152, 128, 16, 16, 128, 4, 0, 128, 2, 1e-6, 0, None), "bad shape"),
