@@ -125,7 +125,7 @@ int launch_quant(const void* x, int64_t M, int64_t N, int64_t xs, void* q, int64
 // the per_token_quant_fp8.cu:56-82 rule over the row (GROUP == 0) or over
 // each 1x128 block (GROUP == 128, 16 lanes x 8 values).
 // ---------------------------------------------------------------------------
-template <class Tag, int LPR, int CH, int GROUP>
+template <class Tag, int LPR, int CH, int GROUP, bool WAVE_VOTE = false>
 __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
     const void* __restrict__ x, int64_t xs, const void* __restrict__ w, uint8_t* __restrict__ q,
     int64_t qs, float* __restrict__ s, int64_t M, int N, float eps) {
@@ -189,10 +189,11 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
   }
   // NaN-skipping maximum of chunk i's part of this lane (the reference's
   // fmaxf rule), for workgroups that hold a non-finite value. The decision
-  // is workgroup-wide: a wave-level vote measured faster only at
-  // T = 10530 per token (20.0 -> 19.3 us) and slower in the other three C4
-  // cases (T = 4725: 9.9 -> 10.2 / 10.4 -> 11.0 us; per block at 10530:
-  // 20.1 -> 20.5 us).
+  // is workgroup-wide except with WAVE_VOTE (per token, at least as many
+  // rows as the GPU has wave slots): a wave-level vote measured faster only
+  // there (T = 10530 per token 20.1 -> 19.5 us) and slower in the other three
+  // C4 cases (T = 4725: 10.0 -> 10.3 / 10.4 -> 10.9 us; per block at 10530:
+  // 20.4 -> 20.6 us).
   auto skip_nan_max = [&](int i) {
     float m = 0.f;
 #pragma unroll
@@ -260,7 +261,9 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
     for (int i = 0; i < CH; ++i) amax = __builtin_elementwise_maximum(amax, gmax[i]);
     amax = row_reduce<LPR, OpAmax>(amax, red_max);
     const bool finite_row = finite_bits(amax);
-    if (__syncthreads_or(!finite_row)) {
+    const bool any_nonfinite =
+        WAVE_VOTE ? rows_any<LPR>(!finite_row) : __syncthreads_or(!finite_row);
+    if (any_nonfinite) {
       float m = 0.f;
 #pragma unroll
       for (int i = 0; i < CH; ++i) m = fmaxf(m, skip_nan_max(i));
@@ -287,9 +290,14 @@ int launch_rmsnorm_quant(const void* x, int64_t xs, const void* w, void* q, int6
     launched = dispatch_row_shape<8>(N, [&](auto lpr, auto ch) {
       constexpr int LPR = decltype(lpr)::value;
       constexpr int CH = decltype(ch)::value;
-      hipLaunchKernelGGL((rmsnorm_quant_kernel<Tag, LPR, CH, 0>), dim3(row_blocks(M, LPR)),
-                         dim3(kBlock), 0, stream, x, xs, w, static_cast<uint8_t*>(q), qs, s, M,
-                         static_cast<int>(N), eps);
+      if (M >= kFewRows)
+        hipLaunchKernelGGL((rmsnorm_quant_kernel<Tag, LPR, CH, 0, true>), dim3(row_blocks(M, LPR)),
+                           dim3(kBlock), 0, stream, x, xs, w, static_cast<uint8_t*>(q), qs, s, M,
+                           static_cast<int>(N), eps);
+      else
+        hipLaunchKernelGGL((rmsnorm_quant_kernel<Tag, LPR, CH, 0>), dim3(row_blocks(M, LPR)),
+                           dim3(kBlock), 0, stream, x, xs, w, static_cast<uint8_t*>(q), qs, s, M,
+                           static_cast<int>(N), eps);
     });
   } else {
     launched = dispatch_row_shape<8>(N, [&](auto lpr, auto ch) {

@@ -187,6 +187,20 @@ def test_rmsnorm_quant_nonfinite(abi, dev, stream_handle, group, N, where):
     check_rms_quant(q, s, x, w, 1e-6, group, f"nonfinite {where} [13,{N}] g{group}")
 
 
+def test_rmsnorm_quant_nonfinite_many_rows(abi, dev, stream_handle):
+    """Per-token mode from 8192 rows on takes its non-finite decision per wave:
+    NaN/inf rows and rows whose 1/scale overflows, spread over 8200 rows."""
+    g = torch.Generator().manual_seed(8200)
+    M, N = 8200, 3072
+    x = torch.randn(M, N, generator=g)
+    for r in (0, 4099, 8187):
+        x[r:r + 13] = inject_nonfinite(x[r:r + 13].clone(), N)
+    w = 1 + 0.1 * torch.randn(N, generator=g)
+    x, w = x.to(torch.bfloat16), w.to(torch.bfloat16)
+    q, s = rms_quant_gpu(abi, stream_handle, x.to(dev), w.to(dev), 1e-6, 0)
+    check_rms_quant(q, s, x, w, 1e-6, 0, "nonfinite [8200,3072] per token")
+
+
 @pytest.mark.parametrize("name", ["C4_4725_tok", "C4_4725_blk", "C4_10530_tok", "C4_10530_blk"])
 def test_rmsnorm_quant_full_c4(abi, dev, stream_handle, name):
     cfg = W.CONFIGS[name]
