@@ -1,7 +1,8 @@
 """Build the C part of the oracle (TEST INFRASTRUCTURE): oracle/_build/libfp8ref.so.
 
 The reference's own kernels are CUDA and cannot be compiled in this image
-(no nvcc), so there is no oracle/_ref build; see DESIGN.md.
+(no nvcc), so there is no oracle/_ref build; the restatement in oracle/ is pinned by
+the reference's golden vectors and closed-form checks instead.
 """
 from __future__ import annotations
 
