@@ -4,6 +4,7 @@ validation errors come back as status codes without touching a GPU, and the
 torch op library registers the reference's schemas byte-for-byte."""
 from __future__ import annotations
 
+import ctypes
 import re
 import subprocess
 from pathlib import Path
@@ -31,7 +32,8 @@ def test_header_declares_all_entry_points():
                  "jo_fused_qk_norm_rope_3d_paired", "jo_fused_qk_norm_rope_3d_grid",
                  "jo_fused_qk_norm_rope_3d_kvcache", "jo_fused_norm_scale_shift", "jo_rmsnorm",
                  "jo_fused_add_layernorm_scale_shift", "jo_rmsnorm_quant_fp8",
-                 "jo_rmsnorm_heads"):
+                 "jo_rmsnorm_heads", "jo_norm_scale_shift_quant_fp8", "jo_fp8_scaled_mm",
+                 "jo_kv_commit_rope"):
         assert name in fns, name
 
 
@@ -125,6 +127,27 @@ def test_empty_inputs_are_noops(abi):
                                          0, 1e-6, None) == abi.JO_OK
     assert lib.jo_fused_qk_norm_rope_3d_paired(None, None, 1, 0, 2, 128, 0, 256, 0, 256, 1e-6,
                                                None, None, None, None, None) == abi.JO_OK
+    assert lib.jo_fused_add_layernorm_scale_shift(None, 8, None, 8, None, 0, None, None, None, 0,
+                                                  None, 0, None, 8, 0, 8, 2, 1e-6,
+                                                  None) == abi.JO_OK
+    assert lib.jo_rmsnorm_quant_fp8(None, 8, None, None, 8, None, 0, 8, 2, 1e-6, 0,
+                                    None) == abi.JO_OK
+    assert lib.jo_norm_scale_shift_quant_fp8(None, 8, None, 8, None, 0, None, None, None, 0, None,
+                                             0, None, 8, None, 0, 8, 2, 0, 1e-6,
+                                             None) == abi.JO_OK
+    assert lib.jo_fp8_scaled_mm(None, 16, None, 16, None, None, None, None, 8, 0, 8, 16, 2,
+                                None) == abi.JO_OK
+    assert lib.jo_kv_commit_rope(None, None, None, None, 1, 1, 0, 2, 128, 0, 0, 256, 0, 0, 256, 4,
+                                 0, None, None, 128, 0, 2, None) == abi.JO_OK
+    # the grid modes check their pointers first (the frequency table is always read), then
+    # return at zero tokens; host addresses stand in, as nothing is dereferenced
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.addressof(buf)
+    assert lib.jo_fused_qk_norm_rope_3d_grid(p, p, 1, 0, 2, 128, 0, 256, 0, 256, 1e-6, p, p, p,
+                                             22, 21, 4, 4, 0, 0.0, None) == abi.JO_OK
+    assert lib.jo_fused_qk_norm_rope_3d_kvcache(p, p, p, 1, 0, 2, 128, 0, 256, 0, 256, 0, 256, 2,
+                                                0, 1e-6, p, p, p, 22, 21, 4, 4, 0, 0.0,
+                                                None) == abi.JO_OK
 
 
 REFERENCE_SCHEMAS = {
