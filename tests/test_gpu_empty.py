@@ -1,0 +1,91 @@
+"""Zero-row and zero-token inputs through the torch ops: each returns (or
+fills) an empty result of the right shape and dtype and launches nothing
+(the C ABI returns before any launch when there are no rows; the CPU tests
+check that entry point by entry point)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+BF = torch.bfloat16
+FP8 = torch.float8_e4m3fn
+
+
+def _rows(dev, N=256):
+    return torch.empty(0, N, dtype=BF, device=dev)
+
+
+def case_norm_scale_shift(jo, dev):
+    x = _rows(dev)
+    y = jo.fused_norm_scale_shift(x, None, None, x, x, "layer", 1e-6)
+    return [(y, (0, 256), BF)]
+
+
+def case_rmsnorm(jo, dev):
+    y = jo.rmsnorm(_rows(dev), torch.ones(256, dtype=BF, device=dev), 1e-6)
+    return [(y, (0, 256), BF)]
+
+
+def case_per_token_quant(jo, dev):
+    q = torch.empty(0, 256, dtype=FP8, device=dev)
+    s = torch.empty(0, 1, dtype=torch.float32, device=dev)
+    jo.sgl_per_token_quant_fp8(_rows(dev), q, s)
+    return [(q, (0, 256), FP8), (s, (0, 1), torch.float32)]
+
+
+def case_fp8_scaled_mm(jo, dev):
+    a = torch.empty(0, 64, dtype=FP8, device=dev)
+    b = torch.zeros(32, 64, dtype=FP8, device=dev).t()
+    y = jo.fp8_scaled_mm(a, b, torch.empty(0, device=dev), torch.ones(32, device=dev), BF, None)
+    return [(y, (0, 32), BF)]
+
+
+def case_add_layernorm(jo, dev):
+    x, r = _rows(dev), _rows(dev)
+    sc = torch.zeros(256, dtype=BF, device=dev)
+    y = jo.fused_add_layernorm_scale_shift(x, r, sc, sc, eps=1e-6)
+    return [(y, (0, 256), BF)]
+
+
+def case_rmsnorm_quant(jo, dev):
+    q = torch.empty(0, 256, dtype=FP8, device=dev)
+    s = torch.empty(0, dtype=torch.float32, device=dev)
+    jo.rmsnorm_quant_fp8(_rows(dev), torch.ones(256, dtype=BF, device=dev), 1e-6, q, s)
+    return [(q, (0, 256), FP8), (s, (0,), torch.float32)]
+
+
+def case_norm_quant(jo, dev):
+    q = torch.empty(0, 256, dtype=FP8, device=dev)
+    s = torch.empty(0, dtype=torch.float32, device=dev)
+    sc = torch.zeros(256, dtype=BF, device=dev).expand(0, 256)
+    jo.norm_scale_shift_quant_fp8(_rows(dev), sc, sc, q, s)
+    return [(q, (0, 256), FP8), (s, (0,), torch.float32)]
+
+
+def case_rmsnorm_heads(jo, dev):
+    x = torch.empty(1, 0, 4, 128, dtype=BF, device=dev)
+    y = jo.rmsnorm_heads(x, torch.ones(128, dtype=BF, device=dev), 1e-6, True)
+    return [(y, (1, 0, 4, 128), BF)]
+
+
+def case_apply_rotary_emb(jo, dev):
+    x = torch.empty(1, 0, 4, 128, dtype=BF, device=dev)
+    t = torch.empty(0, 128, dtype=torch.float32, device=dev)
+    y = jo.apply_rotary_emb(x, (t, t))
+    return [(y, (1, 0, 4, 128), BF)]
+
+
+CASES = [case_norm_scale_shift, case_rmsnorm, case_per_token_quant, case_fp8_scaled_mm,
+         case_add_layernorm, case_rmsnorm_quant, case_norm_quant, case_rmsnorm_heads,
+         case_apply_rotary_emb]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c.__name__[5:] for c in CASES])
+def test_empty_input(dev, case):
+    import joyomni_ops as jo
+    outs = case(jo, dev)
+    torch.cuda.synchronize()
+    for t, shape, dtype in outs:
+        assert tuple(t.shape) == shape and t.dtype == dtype, (tuple(t.shape), t.dtype)
