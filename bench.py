@@ -23,16 +23,30 @@ the reference's own benchmark script (test_bench.py): rmsnorm and LayerNorm +
 modulation at [4096, 4096], table-mode QK at [1, 1560, 32, 128], the FP8 GEMM
 at 4096^3.
 
-Timing: W eager warmup calls, then K calls captured into one HIP graph and
-replayed once untimed and once timed between HIP events recorded on the
-replay stream (the stream the kernels run on); per-call time = elapsed / K.
-The calls rotate over >= 4 input/output buffer sets totalling > 640 MB so the
-256 MB Infinity Cache cannot hold the working set. Inputs are resident in HBM
-before the timed region. achieved GB/s = algorithmic bytes (compulsory reads
-+ writes, joyomni_ops.workloads.algorithmic_bytes) / per-call time.
+Timing: max(W, 20) eager warmup calls, then K calls captured into one HIP
+graph, replayed once untimed and then ceil(100 / K) times between HIP events
+recorded on the replay stream (the stream the kernels run on), so that at
+least 100 calls are timed whatever K is (`timed_calls` in each line);
+per-call time = elapsed / timed calls. The calls rotate over >= 4
+input/output buffer sets totalling > 640 MB so the 256 MB Infinity Cache
+cannot hold the working set. Inputs are resident in HBM before the timed
+region. achieved GB/s = algorithmic bytes (compulsory reads + writes,
+joyomni_ops.workloads.algorithmic_bytes) / per-call time.
 
-cpu_baseline: the CPU oracle's restatement of the reference formula for the
-headline op, timed on the host's cores on the full C1 input.
+S_* lines are bare row streams (csrc/bench/stream_ceiling.hip, built into
+libjoyomni_stream.so, not part of the op library): for a config they move the
+same bytes in the same launch shape as its kernel (workgroups, lanes per row,
+16-byte chunks per lane, nontemporal accesses, scales) with no arithmetic
+beyond the whole-row dependency every row kernel has. Their time is the
+ceiling of that access shape on this GPU; the config's line carries
+`stream_ceiling_us` and `frac_of_stream_ceiling` (ceiling time / kernel
+time). Alternative shapes of the same bytes (S_*@LPRxCH) show whether another
+launch shape would stream faster.
+
+cpu_baseline: the CPU oracle's restatement of the reference formula of every
+BASELINE config (C0-C4), timed on the host's cores with the same inputs:
+3 warmups, then at least 10 timed calls (more while under ~2 s), median
+(`cpu_us_per_call` in each config's line; the headline one in cpu_baseline).
 
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
@@ -86,6 +100,74 @@ def copy_probe(mb: int, steps: int, dev) -> dict:
     return {"bytes_each_way": n, "us_per_call": round(us, 3), "gbps": round(2 * n / (us * 1e-6) / 1e9, 1)}
 
 
+MIN_TIMED = 100   # timed calls per line, whatever --steps is
+MIN_WARMUP = 20   # eager warmup calls per line, whatever --warmup is
+
+
+def time_launches(launch, n_sets: int, steps: int, warmup: int, dev,
+                  use_graph: bool = True) -> dict:
+    """Times launch(i, stream_handle) (call i uses buffer set i % n_sets).
+
+    max(warmup, MIN_WARMUP) eager warmups; `steps` eager launches timed for
+    eager_us_per_call; then `steps` launches captured into one HIP graph,
+    replayed once untimed and ceil(MIN_TIMED / steps) times between HIP events
+    on the replay stream. Returns per-call times and the timed call count."""
+    import torch
+    warmup = max(warmup, MIN_WARMUP)
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            launch(i, stream.cuda_stream)
+    torch.cuda.synchronize()
+
+    # eager back-to-back launches (host launch path included)
+    with torch.cuda.stream(stream):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            launch(i, stream.cuda_stream)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    eager_us = e0.elapsed_time(e1) * 1000.0 / steps
+    if not use_graph:
+        return {"us_per_call": eager_us, "eager_us_per_call": eager_us, "timed_calls": steps,
+                "warmup_calls": warmup, "timing": "eager"}
+
+    # HIP graph of `steps` launches, replayed until >= MIN_TIMED calls are timed
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        h = torch.cuda.current_stream().cuda_stream
+        for i in range(steps):
+            launch(i, h)
+    graph.replay()
+    torch.cuda.synchronize()
+    replays = max(1, math.ceil(MIN_TIMED / steps))
+    cur = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(cur)
+    for _ in range(replays):
+        graph.replay()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / (steps * replays)
+    del graph
+    return {"us_per_call": us, "eager_us_per_call": eager_us, "timed_calls": steps * replays,
+            "warmup_calls": warmup, "timing": "hip-graph"}
+
+
+def _finish(res: dict, alg: int, n_sets: int, set_bytes: int) -> dict:
+    us = res["us_per_call"]
+    gbps = alg / (us * 1e-6) / 1e9
+    out = {"us_per_call": round(us, 3), "eager_us_per_call": round(res["eager_us_per_call"], 3),
+           "gbps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_GBPS, 4),
+           "algorithmic_bytes": alg, "buffer_sets": n_sets,
+           "rotated_mb": round(n_sets * set_bytes / 1e6, 1),
+           "timed_calls": res["timed_calls"], "warmup_calls": res["warmup_calls"],
+           "timing": res["timing"]}
+    return out
+
+
 def time_gpu(cfg, steps: int, warmup: int, dev, use_graph: bool = True) -> dict:
     import torch
 
@@ -93,8 +175,7 @@ def time_gpu(cfg, steps: int, warmup: int, dev, use_graph: bool = True) -> dict:
     from joyomni_ops import workloads as W
 
     host = W.make_inputs(cfg)
-    probe = {k: v for k, v in host.items()}
-    set_bytes = tensor_bytes(probe) + tensor_bytes(W.alloc_outputs(cfg, probe))
+    set_bytes = tensor_bytes(host) + tensor_bytes(W.alloc_outputs(cfg, host))
     n_sets = max(4, math.ceil(ROT_BYTES / set_bytes))
     sets = []
     for _ in range(n_sets):
@@ -105,51 +186,98 @@ def time_gpu(cfg, steps: int, warmup: int, dev, use_graph: bool = True) -> dict:
     if cfg.op in ("qk_grid", "qk_kvcache"):
         d = cfg.dims
         freqs = jo.rope_freqs(d["D"], d["rope_dims"], d["theta"], device=dev)
-    stream = torch.cuda.Stream(dev)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        for i in range(warmup):
-            W.launch(cfg, sets[i % n_sets], stream.cuda_stream, freqs)
-    torch.cuda.synchronize()
-
-    # eager back-to-back launches (host launch path included)
-    with torch.cuda.stream(stream):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(steps):
-            W.launch(cfg, sets[i % n_sets], stream.cuda_stream, freqs)
-        e1.record(stream)
-    torch.cuda.synchronize()
-    eager_us = e0.elapsed_time(e1) * 1000.0 / steps
-    alg = W.algorithmic_bytes(cfg)
-    if not use_graph:
-        gbps = alg / (eager_us * 1e-6) / 1e9
-        return {"us_per_call": round(eager_us, 3), "eager_us_per_call": round(eager_us, 3),
-                "gbps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_GBPS, 4),
-                "algorithmic_bytes": alg, "buffer_sets": n_sets, "timing": "eager"}
-
-    # HIP graph of `steps` launches
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        h = torch.cuda.current_stream().cuda_stream
-        for i in range(steps):
-            W.launch(cfg, sets[i % n_sets], h, freqs)
-    graph.replay()
-    torch.cuda.synchronize()
-    cur = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(cur)
-    graph.replay()
-    e1.record(cur)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / steps
-    gbps = alg / (us * 1e-6) / 1e9
-    del graph, sets
+    res = time_launches(lambda i, h: W.launch(cfg, sets[i % n_sets], h, freqs), n_sets, steps,
+                        warmup, dev, use_graph)
+    del sets
     torch.cuda.empty_cache()
-    return {"us_per_call": round(us, 3), "eager_us_per_call": round(eager_us, 3),
-            "gbps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_GBPS, 4),
-            "algorithmic_bytes": alg, "buffer_sets": n_sets,
-            "rotated_mb": round(n_sets * set_bytes / 1e6, 1), "timing": "hip-graph"}
+    return _finish(res, W.algorithmic_bytes(cfg), n_sets, set_bytes)
+
+
+# ---------------------------------------------------------------------------
+# Stream ceilings: (config it bounds, rows, lanes per row, chunks per lane,
+# input streams, output streams, bytes stored per 16 read, fp32 scalars per
+# row, in place). The first entry of a config is its kernel's launch shape;
+# entries named S_<cfg>@<LPR>x<CH> are other shapes of the same bytes.
+# ---------------------------------------------------------------------------
+STREAMS = {
+    "S_C0": ("C0", 3510 * 4, 64, 3, 1, 1, 16, 0, True),
+    "S_C0@64x1": ("C0", 3510 * 12, 64, 1, 1, 1, 16, 0, True),
+    "S_C0@64x2": ("C0", 3510 * 6, 64, 2, 1, 1, 16, 0, True),
+    "S_C1": ("C1", 10530, 64, 6, 1, 1, 8, 1, False),
+    "S_C1@128x3": ("C1", 10530, 128, 3, 1, 1, 8, 1, False),
+    "S_C2": ("C2", 10530, 128, 3, 2, 2, 16, 0, False),
+    "S_C2@64x6": ("C2", 10530, 64, 6, 2, 2, 16, 0, False),
+    "S_C3": ("C3", 10530 * 4, 64, 3, 1, 1, 16, 0, True),
+    "S_C4_4725_tok": ("C4_4725_tok", 4725, 64, 6, 1, 1, 8, 1, False),
+    "S_C4_4725_tok@128x3": ("C4_4725_tok", 4725, 128, 3, 1, 1, 8, 1, False),
+    "S_C4_4725_tok@256x2": ("C4_4725_tok", 4725, 256, 2, 1, 1, 8, 1, False),
+    "S_C4_4725_blk": ("C4_4725_blk", 4725, 64, 6, 1, 1, 8, 24, False),
+    "S_C4_10530_tok": ("C4_10530_tok", 10530, 64, 6, 1, 1, 8, 1, False),
+    "S_C4_10530_blk": ("C4_10530_blk", 10530, 64, 6, 1, 1, 8, 24, False),
+    "S_R_q4k": ("R_q4k", 3120, 128, 4, 1, 1, 8, 1, False),
+    "S_R_q4k@64x8": ("R_q4k", 3120, 64, 8, 1, 1, 8, 1, False),
+    "S_R_q16k": ("R_q16k", 3120, 256, 8, 1, 1, 8, 1, False),
+    "S_R_rms": ("R_rms", 99840, 16, 1, 1, 1, 16, 0, False),
+    "S_R_ln": ("R_ln", 3120, 256, 2, 3, 1, 16, 0, False),
+    "S_R_ln@64x8": ("R_ln", 3120, 64, 8, 3, 1, 16, 0, False),
+    "S_R_qk": ("R_qk", 3120 * 8, 64, 2, 1, 1, 16, 0, True),
+    "S_T_rms": ("T_rms", 4096, 64, 8, 1, 1, 16, 0, False),
+    "S_T_ln": ("T_ln", 4096, 256, 2, 3, 1, 16, 0, False),
+    "S_T_qk": ("T_qk", 1560 * 8, 64, 2, 1, 1, 16, 0, True),
+}
+
+_STREAM_LIB = None
+
+
+def stream_lib():
+    global _STREAM_LIB
+    if _STREAM_LIB is None:
+        import ctypes
+        path = ROOT / "joyai-video-edit_amd" / "joyomni_ops" / "libjoyomni_stream.so"
+        lib = ctypes.CDLL(str(path))
+        P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        lib.jo_stream_rows.argtypes = [P, P, P, P, P, P, I64, I, I, I, I, I, I, P]
+        lib.jo_stream_rows.restype = I
+        _STREAM_LIB = lib
+    return _STREAM_LIB
+
+
+def stream_bytes(spec) -> int:
+    _, rows, lpr, ch, nin, nout, outb, nscal, _ = spec
+    return rows * (nin * lpr * ch * 16 + nout * lpr * ch * outb + nscal * 4)
+
+
+def time_stream(spec, steps: int, warmup: int, dev) -> dict:
+    import torch
+    _, rows, lpr, ch, nin, nout, outb, nscal, inplace = spec
+    rin, rout = rows * lpr * ch * 16, rows * lpr * ch * outb
+    set_bytes = stream_bytes(spec)
+    n_sets = max(4, math.ceil(ROT_BYTES / set_bytes))
+    sets = []
+    for _ in range(n_sets):
+        ins = [torch.randint(0, 255, (rin,), dtype=torch.uint8, device=dev) for _ in range(nin)]
+        outs = ins[:1] if inplace else [torch.empty(rout, dtype=torch.uint8, device=dev)
+                                        for _ in range(nout)]
+        scal = torch.empty(max(1, rows * nscal), dtype=torch.float32, device=dev)
+        sets.append((ins, outs, scal))
+    lib = stream_lib()
+
+    def launch(i, h):
+        ins, outs, scal = sets[i % n_sets]
+        p = [t.data_ptr() for t in ins] + [None] * (3 - len(ins))
+        o = [t.data_ptr() for t in outs] + [None] * (2 - len(outs))
+        rc = lib.jo_stream_rows(p[0], p[1], p[2], o[0], o[1], scal.data_ptr() if nscal else None,
+                                rows, lpr, ch, nin, nout, outb, nscal, h)
+        if rc != 0:
+            raise RuntimeError(f"jo_stream_rows failed ({rc}) for {spec}")
+
+    res = time_launches(launch, n_sets, steps, warmup, dev)
+    del sets
+    torch.cuda.empty_cache()
+    out = _finish(res, set_bytes, n_sets, set_bytes)
+    out.update(shape=f"{rows} rows, {lpr} lanes x {ch} chunks, {nin} in / {nout} out",
+               kind="stream-ceiling")
+    return out
 
 
 def gemm_vs_hipblaslt(cfg, dev, rounds: int = 7, calls: int = 20):
@@ -316,6 +444,21 @@ def cpu_fn(cfg):
     return qk
 
 
+def cpu_threads() -> int:
+    """Threads for the CPU baseline: every CPU this process may run on, capped
+    by OMP_NUM_THREADS where the host sets it (the GPU boxes give a process a
+    16-CPU share of a larger machine and say so there)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+BASELINE_CONFIGS = ("C0", "C1", "C2", "C3", "C4_4725_tok", "C4_4725_blk", "C4_10530_tok",
+                    "C4_10530_blk")
+
+
 def time_cpu(cfg, warmup: int, iters: int, seconds: float = 0.0) -> dict:
     """Median CPU time per call: at least `iters` calls and at least `seconds`
     of timed CPU work (capped at 1000 calls)."""
@@ -365,11 +508,12 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", default="", help="comma-separated config names")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-iters", type=int, default=10, help="minimum timed CPU calls")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="minimum seconds of timed CPU work for the baseline")
+    ap.add_argument("--only", default="", help="comma-separated config names (C*, S_*, ...)")
+    ap.add_argument("--no-streams", action="store_true", help="skip the S_* stream ceilings")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--cpu-iters", type=int, default=10, help="minimum timed CPU calls per config")
+    ap.add_argument("--cpu-seconds", type=float, default=2.0,
+                    help="keep timing a config's CPU calls while under this many seconds")
     ap.add_argument("--no-graph", action="store_true",
                     help="time eager launches only (for profiler counter runs)")
     ap.add_argument("--copy-mb", type=int, default=0,
@@ -389,13 +533,21 @@ def main() -> int:
     from joyomni_ops import workloads as W
 
     dev = torch.device("cuda", 0)
-    names = [n for n in (args.only.split(",") if args.only else W.CONFIGS) if n]
+    if args.only:
+        names = [n for n in args.only.split(",") if n]
+    else:
+        names = list(W.CONFIGS) + ([] if args.no_streams else list(STREAMS))
     if HEADLINE not in names:
         names.insert(0, HEADLINE)
     results = {}
     for n in names:
+        if n in STREAMS:
+            log(f"{n}: timing bare stream")
+            results[n] = time_stream(STREAMS[n], args.steps, args.warmup, dev)
+            log(f"{n}: {results[n]}")
+            continue
         cfg = W.CONFIGS[n]
-        log(f"{n}: timing {args.steps} {'eager' if args.no_graph else 'graph-replayed'} calls")
+        log(f"{n}: timing {'eager' if args.no_graph else 'graph-replayed'} calls")
         results[n] = time_gpu(cfg, args.steps, args.warmup, dev, use_graph=not args.no_graph)
         ref_us = torch_reference_us(cfg, dev)
         if ref_us is not None:
@@ -417,6 +569,22 @@ def main() -> int:
                 results[n]["hipblaslt_tflops"] = round(flops / (ab[1] * 1e-6) / 1e12, 1)
                 results[n]["hipblaslt_over_ours"] = round(ab[1] / ab[0], 3)
         log(f"{n}: {results[n]}")
+
+    # Each config's stream ceiling: its kernel's own shape, and the fastest shape.
+    for sname, spec in STREAMS.items():
+        cname = spec[0]
+        if sname not in results or cname not in results:
+            continue
+        r, s_us = results[cname], results[sname]["us_per_call"]
+        if "@" not in sname:
+            r["stream_ceiling"] = sname
+            r["stream_ceiling_us"] = s_us
+            r["frac_of_stream_ceiling"] = round(s_us / r["us_per_call"], 4)
+        if s_us < r.get("best_stream_us", float("inf")):
+            r["best_stream"] = sname
+            r["best_stream_us"] = s_us
+            r["frac_of_best_stream"] = round(s_us / r["us_per_call"], 4)
+
     copy = None
     if args.copy_mb:
         copy = copy_probe(args.copy_mb, args.steps, dev)
@@ -424,9 +592,19 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        log("cpu baseline: oracle per_token_quant_fp8 on the full C1 input")
-        cpu = time_cpu(W.CONFIGS[HEADLINE], 3, args.cpu_iters, args.cpu_seconds)
-        log(f"cpu: {cpu}")
+        threads = cpu_threads()
+        torch.set_num_threads(threads)
+        for n in BASELINE_CONFIGS:
+            if n not in results:
+                continue
+            log(f"cpu baseline {n}: oracle restatement on the full input, {threads} threads")
+            c = time_cpu(W.CONFIGS[n], 3, args.cpu_iters, args.cpu_seconds)
+            results[n].update(cpu_us_per_call=c["us_per_call"], cpu_gbps=c["gbps"],
+                              cpu_iters=c["iters"], cpu_threads=c["threads"],
+                              gpu_over_cpu=round(c["us_per_call"] / results[n]["us_per_call"], 1))
+            log(f"cpu {n}: {c}")
+            if n == HEADLINE:
+                cpu = c
 
     h = results[HEADLINE]
     cfg = W.CONFIGS[HEADLINE]
@@ -437,6 +615,8 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "timed_calls": h["timed_calls"],
+        "warmup_calls": h["warmup_calls"],
         "ms_per_step": round(h["us_per_call"] / 1000.0, 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -448,14 +628,16 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": HEADLINE_KERNEL, "achieved": h["gbps"],
                      "peak": PEAK_GBPS, "unit": "GB/s", "frac": h["frac_of_peak"],
                      "traffic": load_traffic(HEADLINE_KERNEL),
-                     "algorithmic_bytes": h["algorithmic_bytes"]},
+                     "algorithmic_bytes": h["algorithmic_bytes"],
+                     "stream_ceiling_us": h.get("stream_ceiling_us")},
         "cpu_baseline": None if cpu is None else {
             "value": cpu["gbps"], "unit": "GB/s", "us_per_call": cpu["us_per_call"],
             "cores": cpu["threads"], "kind": "port",
             "sample": f"oracle.ops.per_token_quant_fp8 (torch CPU) on the full C1 input, "
-                      f"median of {cpu['iters']} calls (~{cpu['seconds']:.0f} s of CPU work) after "
-                      f"3 warmups; host {cpu_model()}, "
-                      f"{os.cpu_count()} logical CPUs"},
+                      f"median of {cpu['iters']} calls ({cpu['seconds']:.1f} s of CPU work) after "
+                      f"3 warmups, torch.set_num_threads({cpu['threads']}); host {cpu_model()}, "
+                      f"{os.cpu_count()} logical CPUs; every BASELINE config's CPU time is in "
+                      f"ops[cfg].cpu_us_per_call"},
         "ops": results,
     }
     if copy is not None:

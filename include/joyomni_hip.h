@@ -57,6 +57,26 @@ const char* jo_last_error(void);
 /* JO_ABI_VERSION of the loaded library. */
 int jo_abi_version(void);
 
+/* Launch-shape knobs. Each selects how a kernel is spread over waves, never
+ * what it computes: results are identical under every setting. The value is
+ * -1 (the library's own choice) unless the environment variable named below
+ * was set when the library was loaded, or jo_set_launch_override() changed it.
+ *   JO_KNOB_QK_SPLIT    waves per token of the QK norm + RoPE kernels: 1, 2,
+ *                       4, 6 or 8 (env JO_QK_SPLIT)
+ *   JO_KNOB_KV_SPLIT    1 = K and V of a KV-pool row on one wave, 2 = on two
+ *                       (env JO_KV_SPLIT)
+ *   JO_KNOB_GEMM_SHAPE  FP8 GEMM tile: 0 = 256x256, 1 = 256x128, 2 = the
+ *                       register-staged kernel, 3 = 224x256, 4 = 224x128
+ *                       (env JO_GEMM_SHAPE)
+ * No reference counterpart (tuning and test hook). */
+#define JO_KNOB_QK_SPLIT 0
+#define JO_KNOB_KV_SPLIT 1
+#define JO_KNOB_GEMM_SHAPE 2
+
+/* Sets knob `knob` to `value` (-1 restores the automatic choice) for every
+ * later launch in the process. Returns JO_ERR_INVALID for an unknown knob. */
+int jo_set_launch_override(int knob, int value);
+
 /* ------------------------------------------------------------------------
  * Per-token FP8 e4m3 quantization.
  * Replaces joyomni_ops::sgl_per_token_quant_fp8

@@ -1,8 +1,11 @@
 """Build the gfx950 kernel library and the torch op shim in-tree.
 
 Outputs (next to the Python package, so they travel with the source tree):
-  joyomni_ops/libjoyomni_hip.so  HIP kernels + the C ABI of include/joyomni_hip.h
-  joyomni_ops/_C.so              TORCH_LIBRARY(joyomni_ops) registration over the C ABI
+  joyomni_ops/libjoyomni_hip.so     HIP kernels + the C ABI of include/joyomni_hip.h
+  joyomni_ops/_C.so                 TORCH_LIBRARY(joyomni_ops) registration over the C ABI
+  joyomni_ops/libjoyomni_stream.so  bare row streams that bench.py times as the
+                                    HBM ceiling of each kernel's access shape
+                                    (csrc/bench/; not part of the op library)
 
 The library is compiled with hipcc for gfx950 only. The shim is plain C++
 compiled with g++ against torch's ROCm headers; it holds no device code.
@@ -33,6 +36,7 @@ ARCH = "gfx950"
 
 LIB_NAME = "libjoyomni_hip.so"
 SHIM_NAME = "_C.so"
+STREAM_NAME = "libjoyomni_stream.so"
 
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -83,6 +87,14 @@ def build_lib(jobs: int) -> Path:
     return out
 
 
+def build_stream() -> Path:
+    out = OUT_DIR / STREAM_NAME
+    tmp = out.with_suffix(".so.tmp")
+    _run([HIPCC, *HIP_FLAGS, "-shared", str(CSRC / "bench" / "stream_ceiling.hip"), "-o", str(tmp)])
+    os.replace(tmp, out)
+    return out
+
+
 def build_shim() -> Path:
     import torch
     from torch.utils import cpp_extension
@@ -119,6 +131,7 @@ def build(jobs: int | None = None, only: str | None = None) -> None:
     jobs = jobs or min(8, os.cpu_count() or 1)
     if only in (None, "lib"):
         build_lib(jobs)
+        build_stream()
     if only in (None, "shim"):
         if (CSRC / "torch_shim.cpp").exists():
             build_shim()

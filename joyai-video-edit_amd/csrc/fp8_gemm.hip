@@ -16,7 +16,6 @@
 // (2 x 64 KB). LDS rows are 128 bytes; chunk c of row r is stored at chunk
 // position c ^ (r % 8) ^ ((r / 8) % 2), so the 16 rows a 16-lane group
 // reads with one ds_read_b128 fall in 16 distinct 16-byte bank groups.
-#include <stdlib.h>
 
 #include <atomic>
 
@@ -508,11 +507,12 @@ int launch_gemm(const GemmArgs& g, hipStream_t stream) {
                        256 * (g.lda > g.ldb ? g.lda : g.ldb) + g.K <= int64_t{UINT32_MAX};
   // 8-wave 256-column tiles measured faster than two 4-wave 128-column
   // workgroups per CU at every deployment shape (3120x12288x4096: 199 -> 185
-  // us, 3120x16384x4096: 257 -> 233 us). JO_GEMM_SHAPE=0|1|2|3|4 forces
-  // 256x256, 256x128, the register-staged kernel, 224x256 or 224x128 (results
-  // are the same up to the fp32 accumulation order inside the matrix cores).
-  const char* w = getenv("JO_GEMM_SHAPE");
-  const int shape = w ? atoi(w) : (pick_tile_rows(g.M, g.N) == 224 ? 3 : 0);
+  // us, 3120x16384x4096: 257 -> 233 us). The JO_KNOB_GEMM_SHAPE override
+  // 0|1|2|3|4 forces 256x256, 256x128, the register-staged kernel, 224x256 or
+  // 224x128 (results are the same up to the fp32 accumulation order inside
+  // the matrix cores).
+  const int forced = launch_knob(JO_KNOB_GEMM_SHAPE);
+  const int shape = forced >= 0 ? forced : (pick_tile_rows(g.M, g.N) == 224 ? 3 : 0);
   if (pipe_ok && shape == 1)
     launch_pipe<OutTag, 256, 128, 4, 3>(g, stream);
   else if (pipe_ok && shape == 0)

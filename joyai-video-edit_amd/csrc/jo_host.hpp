@@ -18,6 +18,12 @@ void clear_error();
 // Converts the launch status of the kernel just enqueued into a JO_ status.
 int launch_status(const char* op);
 
+// Launch-shape override of a JO_KNOB_* knob: -1 (automatic choice) unless the
+// environment set it when the library was loaded (JO_QK_SPLIT, JO_KV_SPLIT,
+// JO_GEMM_SHAPE) or jo_set_launch_override() changed it since. Results never
+// depend on a knob, only the launch shape does.
+int launch_knob(int knob);
+
 #define JO_REQUIRE(cond, ...)      \
   do {                             \
     if (!(cond)) {                 \

@@ -18,7 +18,6 @@
 // waves of their own, after all the K waves. A lane's table columns repeat
 // every head (512 elements per pass is a whole number of heads when D divides
 // 512), so a lane reads its 8 cos and 8 sin values once per row.
-#include <stdlib.h>
 
 #include <type_traits>
 
@@ -177,10 +176,9 @@ int launch_commit(const CommitArgs& a, hipStream_t stream) {
                       a.tab_bs % 4 == 0;
   const int chunks = (a.row_elems + 511) / 512;
   // K and V on separate waves: 40 x 1560 x [32, 128] 357 -> 340 us (twice the
-  // waves, each streaming one tensor). JO_KV_SPLIT=1 keeps them on one wave
-  // (launch shape only; results are identical).
-  const char* env = getenv("JO_KV_SPLIT");
-  const bool kv2 = a.src_v != nullptr && !(env && atoi(env) == 1);
+  // waves, each streaming one tensor). The JO_KNOB_KV_SPLIT override 1 keeps
+  // them on one wave (launch shape only; results are identical).
+  const bool kv2 = a.src_v != nullptr && launch_knob(JO_KNOB_KV_SPLIT) != 1;
   const dim3 grid(static_cast<unsigned>(((kv2 ? 2 : 1) * rows + 3) / 4));
   bool launched = true;
   auto go = [&](auto ch) {

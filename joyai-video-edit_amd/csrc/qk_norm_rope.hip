@@ -13,8 +13,6 @@
 //          and the wave redistributes them with ds_bpermute;
 //   KVC    GRID, with the rotated k written to a frame ring buffer instead
 //          of in place.
-#include <stdlib.h>
-
 #include "jo_device.hpp"
 #include "jo_host.hpp"
 
@@ -117,7 +115,12 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
   constexpr int K = P > 64 ? P / 64 : 1;  // pairs evaluated per lane in grid modes
   constexpr int NS = SPLIT == 1 ? 2 : 1;  // tensor streams per wave (q and k, or one)
   const int lane = threadIdx.x % kWave;
-  const int64_t wid = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + threadIdx.x / kWave;
+  // The wave index through readfirstlane: the token and part arithmetic below
+  // (divisions included) is then scalar instead of repeated in every lane
+  // (858 instead of 1048 vector instructions; C0 16.0 -> 15.85 us, every QK
+  // shape 0.6-1.5% faster).
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) +
+                      __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   // Waves of q come first, then waves of k (SPLIT >= 2): a workgroup streams
   // consecutive rows of one tensor (measured against interleaving q and k
   // waves per token: [1, 3510, 24, 128] 16.38 -> 16.15 us, C3 43.9 -> 43.4 us,
@@ -291,11 +294,12 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
 // quarters of two or more ([1, 3120, 32, 128] tables 18.6 -> 18.0 us,
 // [1, 1560, 32, 128] 11.3 -> 10.4 us); with 24 heads (six groups) a quarter
 // would be 1.5 groups and it costs ([1, 3510, 24, 128] 16.1 -> 18.5 us); six
-// (thirds) measured level with four there. JO_QK_SPLIT=1|2|4|6|8 overrides
-// the choice (launch shape only; results are identical).
+// (thirds) measured level with four there; twelve (one head group per wave)
+// no better than four ([1, 3510, 24, 128] 16.4 -> 16.3 us, C3 42.6 -> 43.0 us),
+// sixteen at 32 heads level with eight. The JO_KNOB_QK_SPLIT override (1, 2,
+// 4, 6, 8) forces the choice (launch shape only; results are identical).
 int qk_split(int64_t tokens, int all_groups) {
-  const char* e = getenv("JO_QK_SPLIT");
-  const int forced = e ? atoi(e) : 0;
+  const int forced = launch_knob(JO_KNOB_QK_SPLIT);
   if (forced == 1 || forced == 2) return forced;
   if (forced == 8 && all_groups >= 4) return 8;
   if (forced == 6 && all_groups >= 3) return 6;

@@ -30,7 +30,7 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restri
   __shared__ float red[kBlock / kWave];
   __shared__ float red2[kBlock / kWave];
   const int lane = threadIdx.x % LPR;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + wave_uniform_row<LPR>();
   const bool row_ok = row < M;
   const void* xr = byte_off(x, row * xs * Tag::kBytes);
 
@@ -122,15 +122,108 @@ int launch_quant(const void* x, int64_t M, int64_t N, int64_t xs, void* q, int64
 // RMSNorm -> FP8. v = (x * r) * w in fp32 (rmsnorm.cu:41-60 without the
 // rounding to the input type), r = 1/sqrt(mean(x^2) + eps) with the mean
 // square rounded once from its exact value and IEEE sqrt and division; then
-// the per_token_quant_fp8.cu:56-82 rule over the row (GROUP == 0) or over
-// each 1x128 block (GROUP == 128, 16 lanes x 8 values).
+// the per_token_quant_fp8.cu:56-82 rule over the row (per token) or over
+// each 1x128 block (16 lanes x 8 values of one chunk).
+//
+// These kernels are bound by VALU issue as much as by HBM: a wave holds a
+// whole 3072-wide row (48 values per lane) and runs ~10 instructions per value
+// (4 cycles each on a 16-lane SIMD), most of them only once its last chunk
+// has arrived. So the loads are not predicated (a predicated load's join
+// makes the compiler wait for every load before the first use), the sum of
+// squares advances chunk by chunk as the chunks arrive, and the register
+// budget is kept low enough that every row of a one-round grid is resident.
 // ---------------------------------------------------------------------------
-template <class Tag, int LPR, int CH, int GROUP, bool WAVE_VOTE = false>
-__global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
+
+// At least 5 resident waves per SIMD (at most 96 registers): with one wave
+// per row, 5120 slots hold a [4725, 3072] grid in one round. The compiler
+// otherwise spends registers on unpacking the next phase's operands early
+// (104 for the per-token kernel, 4 waves per SIMD).
+constexpr int kC4WavesPerSimd = 5;
+
+// Weight chunks first (cached: they arrive before the row), then the row's.
+// A row past M reads row M - 1 and a lane past N reads chunk 0 of its row;
+// their values are cleared (EXACT == false) and never stored.
+template <class Tag, int LPR, int CH, bool EXACT>
+__device__ __forceinline__ void load_row_weight(const void* x, int64_t xs, const void* w,
+                                                int64_t row, int lane, int N, u32x4 (&c)[CH],
+                                                u32x4 (&wc)[CH]) {
+  const void* xr = byte_off(x, row * xs * Tag::kBytes);
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * 8;
+    wc[i] = ld16(byte_off(w, static_cast<int64_t>((EXACT || e < N) ? e : 0) * Tag::kBytes));
+  }
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * 8;
+    c[i] = ld16_nt(byte_off(xr, static_cast<int64_t>((EXACT || e < N) ? e : 0) * Tag::kBytes));
+  }
+  if constexpr (!EXACT) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const bool in = (i * LPR + lane) * 8 < N;
+      c[i] = u32x4{in ? c[i].x : 0u, in ? c[i].y : 0u, in ? c[i].z : 0u, in ? c[i].w : 0u};
+      wc[i] = u32x4{in ? wc[i].x : 0u, in ? wc[i].y : 0u, in ? wc[i].z : 0u, in ? wc[i].w : 0u};
+    }
+  }
+}
+
+// This lane's sum of squares in fp64. The squares of bf16/fp16 values are
+// exact in fp32 and their fp64 sum carries ~29 more bits than the fp32 mean
+// square it is rounded to, so the mean does not depend on the summation order
+// (the launch shape) — only a sum within ~2^-50 of an fp32 rounding midpoint
+// could tell orders apart. Each chunk's part is issued before the next chunk
+// is waited for. KEEPX keeps the fp32 values of x for the product that
+// follows (48 more registers, 48 fewer instructions per row); otherwise the
+// unpacked values die here and are unpacked again.
+template <class Tag, int CH, bool KEEPX>
+__device__ __forceinline__ double lane_sum_squares(u32x4 (&c)[CH], float (&xf)[KEEPX ? CH : 1][8]) {
+  double acc[2] = {0.0, 0.0};
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f = elem<Tag>(c[i], j);
+      if constexpr (KEEPX) xf[i][j] = f;
+      const double d = static_cast<double>(f);
+      acc[j & 1] = __builtin_fma(d, d, acc[j & 1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const double ss = acc[0] + acc[1];
+  if constexpr (!KEEPX) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) asm volatile("" : "+v"(c[i]));
+  }
+  return ss;
+}
+
+template <class Tag, int CH, bool KEEPX>
+__device__ __forceinline__ float x_at(const u32x4 (&c)[CH], const float (&xf)[KEEPX ? CH : 1][8],
+                                      int i, int j) {
+  if constexpr (KEEPX)
+    return xf[i][j];
+  else
+    return elem<Tag>(c[i], j);
+}
+
+// r = 1 / sqrt(ms + eps), ms the fp32 rounding of the exact mean square.
+__device__ __forceinline__ float rms_rstd(double ss, int N, float eps) {
+  const float ms = static_cast<float>(ss / static_cast<double>(N));
+  return 1.0f / sqrtf(ms + eps);
+}
+
+// Per token. The row maximum is taken NaN-propagating: when it is finite (no
+// NaN, no inf) it is the reference's amax and, with a finite inverse scale,
+// the clamp cannot change a code, so it is skipped; rows of a wave
+// (workgroup, for rows wider than a wave) holding a non-finite value take the
+// NaN-skipping maximum and the clamp.
+template <class Tag, int LPR, int CH, bool EXACT, bool KEEPX>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kC4WavesPerSimd)))
+void rmsnorm_quant_tok_kernel(
     const void* __restrict__ x, int64_t xs, const void* __restrict__ w, uint8_t* __restrict__ q,
     int64_t qs, float* __restrict__ s, int64_t M, int N, float eps) {
   static_assert(Tag::kVec == 8, "fp8 rows are built from 8-element chunks");
-  static_assert(GROUP == 0 || (GROUP == 128 && LPR >= 16), "group layout");
   constexpr int RPB = kBlock / LPR;
   __shared__ double red_ss[kBlock / kWave];
   __shared__ float red_max[kBlock / kWave];
@@ -138,174 +231,177 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_quant_kernel(
   const int lane = threadIdx.x % LPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
   const bool row_ok = row < M;
-  const void* xr = byte_off(x, row * xs * Tag::kBytes);
+  u32x4 c[CH], wc[CH];
+  load_row_weight<Tag, LPR, CH, EXACT>(x, xs, w, row_ok ? row : M - 1, lane, N, c, wc);
+  float xf[KEEPX ? CH : 1][8];
+  const float r =
+      rms_rstd(row_reduce_sum64<LPR>(lane_sum_squares<Tag, CH, KEEPX>(c, xf), red_ss), N, eps);
 
-  u32x4 c[CH];
-#pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const int e = (i * LPR + lane) * 8;
-    c[i] = (row_ok && e < N) ? ld16_nt(byte_off(xr, static_cast<int64_t>(e) * Tag::kBytes))
-                             : u32x4{0u, 0u, 0u, 0u};
-  }
-  // Weight chunks are issued with the row loads so their (cached) latency
-  // overlaps the HBM latency instead of following the row reduction.
-  u32x4 wc[CH];
-#pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const int e = (i * LPR + lane) * 8;
-    wc[i] = (e < N) ? ld16(byte_off(w, static_cast<int64_t>(e) * Tag::kBytes))
-                    : u32x4{0u, 0u, 0u, 0u};
-  }
-  // The squares of bf16/fp16 values are exact in fp32; summing them in fp64
-  // makes the mean square the correctly rounded fp32 value of the exact
-  // mean, independent of the summation order. r then follows with two IEEE
-  // fp32 operations, so r, v and the scales do not depend on the launch shape.
-  double ss = 0.0;
-#pragma unroll
-  for (int i = 0; i < CH; ++i) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const double v = static_cast<double>(elem<Tag>(c[i], j));
-      ss = __builtin_fma(v, v, ss);  // v*v is exact: one rounding per step, as a sum of squares
-    }
-  }
-  ss = row_reduce_sum64<LPR>(ss, red_ss);
-  const float ms = static_cast<float>(ss / static_cast<double>(N));
-  const float r = 1.0f / sqrtf(ms + eps);
-
-  // v = (x * r) * w, kept in registers for the quantization pass. The
-  // per-chunk maxima are NaN-propagating (see quant_rows_kernel): a finite
-  // maximum is the reference's and lets the clamp be skipped.
   float v[CH][8];
-  float gmax[CH];
+  float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
-    gmax[i] = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      v[i][j] = (elem<Tag>(c[i], j) * r) * elem<Tag>(wc[i], j);
-      gmax[i] = nan_max_abs(gmax[i], v[i][j]);
+      v[i][j] = (x_at<Tag, CH, KEEPX>(c, xf, i, j) * r) * elem<Tag>(wc[i], j);
+      amax = nan_max_abs(amax, v[i][j]);
     }
   }
-  // NaN-skipping maximum of chunk i's part of this lane (the reference's
-  // fmaxf rule), for workgroups that hold a non-finite value. The decision
-  // is workgroup-wide except with WAVE_VOTE (per token, at least as many
-  // rows as the GPU has wave slots): a wave-level vote measured faster only
-  // there (T = 10530 per token 20.1 -> 19.5 us) and slower in the other three
-  // C4 cases (T = 4725: 10.0 -> 10.3 / 10.4 -> 10.9 us; per block at 10530:
-  // 20.4 -> 20.6 us).
-  auto skip_nan_max = [&](int i) {
+  amax = row_reduce<LPR, OpAmax>(amax, red_max);
+  const bool finite_row = finite_bits(amax);
+  if (rows_any<LPR>(!finite_row)) {
     float m = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[i][j]));
-    return m;
-  };
-  if constexpr (GROUP == 128) {
-    // Each 16-lane DPP row of a chunk holds one 1x128 block.
-    bool all_finite = true;
+    for (int i = 0; i < CH; ++i)
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      gmax[i] = allreduce_amax<16>(gmax[i]);
-      all_finite = all_finite && finite_bits(gmax[i]);
-    }
-    bool fast[CH];
-#pragma unroll
-    for (int i = 0; i < CH; ++i) fast[i] = finite_bits(gmax[i]);
-    if (__syncthreads_or(!all_finite)) {
-#pragma unroll
-      for (int i = 0; i < CH; ++i) gmax[i] = allreduce_amax<16>(skip_nan_max(i));
-    }
-    float ginv[CH];
-    if constexpr (LPR >= kWave) {
-      // A wave holds 4*CH blocks: gather their maxima into lanes 0..4*CH-1
-      // so the two IEEE divisions run once per block, then hand each chunk
-      // its inverse scale back.
-      const int wl = threadIdx.x % kWave;
-      const int wave_in_row = lane / kWave;
-      float mine = 0.f;
-#pragma unroll
-      for (int i = 0; i < CH; ++i) {
-        const float t = __builtin_bit_cast(
-            float, __builtin_amdgcn_ds_bpermute((wl & 3) * 16 * 4, __builtin_bit_cast(int, gmax[i])));
-        if ((wl >> 2) == i) mine = t;
-      }
-      const float gs = mine / kFp8Max;
-      const float gi = (gs == 0.f) ? 0.f : 1.0f / gs;
-      const int gc = wl >> 2;  // chunk of the block this lane owns
-      const int ge = (gc * LPR + wave_in_row * kWave + (wl & 3) * 16) * 8;  // its first element
-      if (row_ok && wl < 4 * CH && ge < N) s[row * (N / 128) + ge / 128] = gs;
-#pragma unroll
-      for (int i = 0; i < CH; ++i)
-        ginv[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
-                                                (i * 4 + (wl >> 4)) * 4, __builtin_bit_cast(int, gi)));
-    } else {
-#pragma unroll
-      for (int i = 0; i < CH; ++i) {
-        const int e = (i * LPR + lane) * 8;
-        const float gs = gmax[i] / kFp8Max;
-        ginv[i] = (gs == 0.f) ? 0.f : 1.0f / gs;
-        if (row_ok && e < N && (lane & 15) == 0) s[row * (N / 128) + e / 128] = gs;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int e = (i * LPR + lane) * 8;
-      if (row_ok && e < N)
-        st8_nt(q + row * qs + e, (fast[i] && finite_bits(ginv[i])) ? quant8<false>(v[i], ginv[i])
-                                                                   : quant8<true>(v[i], ginv[i]));
-    }
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[i][j]));
+    amax = row_reduce<LPR, OpAmax>(m, red_max2);
   }
-  if constexpr (GROUP == 0) {
-    float amax = 0.f;
+  const float scale = amax / kFp8Max;
+  if (row_ok && lane == 0) s[row] = scale;
+  const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;
+  const bool fast = finite_row && finite_bits(inv);
+  if (!row_ok) return;
 #pragma unroll
-    for (int i = 0; i < CH; ++i) amax = __builtin_elementwise_maximum(amax, gmax[i]);
-    amax = row_reduce<LPR, OpAmax>(amax, red_max);
-    const bool finite_row = finite_bits(amax);
-    const bool any_nonfinite =
-        WAVE_VOTE ? rows_any<LPR>(!finite_row) : __syncthreads_or(!finite_row);
-    if (any_nonfinite) {
-      float m = 0.f;
-#pragma unroll
-      for (int i = 0; i < CH; ++i) m = fmaxf(m, skip_nan_max(i));
-      amax = row_reduce<LPR, OpAmax>(m, red_max2);
-    }
-    const float scale = amax / kFp8Max;
-    if (row_ok && lane == 0) s[row] = scale;
-    const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;
-    const bool fast = finite_row && finite_bits(inv);
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int e = (i * LPR + lane) * 8;
-      if (row_ok && e < N)
-        st8_nt(q + row * qs + e, fast ? quant8<false>(v[i], inv) : quant8<true>(v[i], inv));
-    }
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * 8;
+    if (EXACT || e < N)
+      st8_nt(q + row * qs + e, fast ? quant8<false>(v[i], inv) : quant8<true>(v[i], inv));
   }
 }
 
+// Per 1x128 block: each 16-lane DPP row of a chunk holds one block. Same
+// fast / exact paths as per token, decided per block; the vote for the
+// NaN-skipping maxima is wave-wide (workgroup-wide for rows wider than a wave).
+template <class Tag, int LPR, int CH, bool EXACT>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kC4WavesPerSimd)))
+void rmsnorm_quant_blk_kernel(
+    const void* __restrict__ x, int64_t xs, const void* __restrict__ w, uint8_t* __restrict__ q,
+    int64_t qs, float* __restrict__ s, int64_t M, int N, float eps) {
+  static_assert(Tag::kVec == 8 && LPR >= 16, "block layout");
+  constexpr int RPB = kBlock / LPR;
+  __shared__ double red_ss[kBlock / kWave];
+  const int lane = threadIdx.x % LPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
+  const bool row_ok = row < M;
+  u32x4 c[CH], wc[CH];
+  load_row_weight<Tag, LPR, CH, EXACT>(x, xs, w, row_ok ? row : M - 1, lane, N, c, wc);
+  float xf[1][8];
+  const float r =
+      rms_rstd(row_reduce_sum64<LPR>(lane_sum_squares<Tag, CH, false>(c, xf), red_ss), N, eps);
+
+  float v[CH][8];
+  float gmax[CH];
+  bool all_finite = true;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[i][j] = (elem<Tag>(c[i], j) * r) * elem<Tag>(wc[i], j);
+      m = nan_max_abs(m, v[i][j]);
+    }
+    gmax[i] = allreduce_amax<16>(m);
+    all_finite = all_finite && finite_bits(gmax[i]);
+    __builtin_amdgcn_sched_barrier(0);  // chunk by chunk: c[i], wc[i] die here
+  }
+  bool fast[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) fast[i] = finite_bits(gmax[i]);
+  if (rows_any<LPR>(!all_finite)) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      float m = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[i][j]));
+      gmax[i] = allreduce_amax<16>(m);
+    }
+  }
+  const int nblk = N / 128;
+  float ginv[CH];
+  if constexpr (LPR >= kWave) {
+    // A wave holds 4*CH blocks: lane b < 4*CH takes block b's maximum, runs
+    // the two IEEE divisions once, and hands each chunk its inverse back.
+    const int wl = threadIdx.x % kWave;
+    const int wave_in_row = lane / kWave;
+    float mine = 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const float t = __builtin_bit_cast(
+          float, __builtin_amdgcn_ds_bpermute((wl & 3) * 16 * 4, __builtin_bit_cast(int, gmax[i])));
+      if ((wl >> 2) == i) mine = t;
+    }
+    const float gs = mine / kFp8Max;
+    const float gi = (gs == 0.f) ? 0.f : 1.0f / gs;
+    const int ge = ((wl >> 2) * LPR + wave_in_row * kWave + (wl & 3) * 16) * 8;  // block's first element
+    if (row_ok && wl < 4 * CH && ge < N) s[row * nblk + ge / 128] = gs;
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+      ginv[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                              (i * 4 + (wl >> 4)) * 4, __builtin_bit_cast(int, gi)));
+  } else {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int e = (i * LPR + lane) * 8;
+      const float gs = gmax[i] / kFp8Max;
+      ginv[i] = (gs == 0.f) ? 0.f : 1.0f / gs;
+      if (row_ok && e < N && (lane & 15) == 0) s[row * nblk + e / 128] = gs;
+    }
+  }
+  if (!row_ok) return;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int e = (i * LPR + lane) * 8;
+    if (EXACT || e < N)
+      st8_nt(q + row * qs + e, (fast[i] && finite_bits(ginv[i])) ? quant8<false>(v[i], ginv[i])
+                                                                : quant8<true>(v[i], ginv[i]));
+  }
+}
+
+// Launch shapes (MI355X, [T, 3072] bf16, interleaved A/B against the previous
+// kernels): per token, fewer rows than wave slots keeps 74 registers so all
+// rows are resident in one round (T = 4725: 10.3 -> 9.7 us), more rows keeps
+// x in fp32 (T = 10530: 18.5 -> 17.8 us); per block (T = 10530: 19.7 -> 18.6
+// us, T = 4725 level).
 template <class Tag>
 int launch_rmsnorm_quant(const void* x, int64_t xs, const void* w, void* q, int64_t qs, float* s,
                          int64_t M, int64_t N, float eps, int64_t group, hipStream_t stream) {
+  uint8_t* q8 = static_cast<uint8_t*>(q);
+  const int n = static_cast<int>(N);
   bool launched = false;
   if (group == 0) {
     launched = dispatch_row_shape<8>(N, [&](auto lpr, auto ch) {
       constexpr int LPR = decltype(lpr)::value;
       constexpr int CH = decltype(ch)::value;
-      if (M >= kFewRows)
-        hipLaunchKernelGGL((rmsnorm_quant_kernel<Tag, LPR, CH, 0, true>), dim3(row_blocks(M, LPR)),
-                           dim3(kBlock), 0, stream, x, xs, w, static_cast<uint8_t*>(q), qs, s, M,
-                           static_cast<int>(N), eps);
-      else
-        hipLaunchKernelGGL((rmsnorm_quant_kernel<Tag, LPR, CH, 0>), dim3(row_blocks(M, LPR)),
-                           dim3(kBlock), 0, stream, x, xs, w, static_cast<uint8_t*>(q), qs, s, M,
-                           static_cast<int>(N), eps);
+      const dim3 grid(static_cast<unsigned>(row_blocks(M, LPR)));
+      const bool exact = int64_t{LPR} * CH * 8 == N;
+      if (M >= kFewRows) {
+        if (exact)
+          hipLaunchKernelGGL((rmsnorm_quant_tok_kernel<Tag, LPR, CH, true, true>), grid,
+                             dim3(kBlock), 0, stream, x, xs, w, q8, qs, s, M, n, eps);
+        else
+          hipLaunchKernelGGL((rmsnorm_quant_tok_kernel<Tag, LPR, CH, false, true>), grid,
+                             dim3(kBlock), 0, stream, x, xs, w, q8, qs, s, M, n, eps);
+      } else {
+        if (exact)
+          hipLaunchKernelGGL((rmsnorm_quant_tok_kernel<Tag, LPR, CH, true, false>), grid,
+                             dim3(kBlock), 0, stream, x, xs, w, q8, qs, s, M, n, eps);
+        else
+          hipLaunchKernelGGL((rmsnorm_quant_tok_kernel<Tag, LPR, CH, false, false>), grid,
+                             dim3(kBlock), 0, stream, x, xs, w, q8, qs, s, M, n, eps);
+      }
     });
   } else {
     launched = dispatch_row_shape<8>(N, [&](auto lpr, auto ch) {
       constexpr int LPR = decltype(lpr)::value < 16 ? 16 : decltype(lpr)::value;
       constexpr int CH = decltype(ch)::value;
-      hipLaunchKernelGGL((rmsnorm_quant_kernel<Tag, LPR, CH, 128>), dim3(row_blocks(M, LPR)),
-                         dim3(kBlock), 0, stream, x, xs, w, static_cast<uint8_t*>(q), qs, s, M,
-                         static_cast<int>(N), eps);
+      const dim3 grid(static_cast<unsigned>(row_blocks(M, LPR)));
+      if (int64_t{LPR} * CH * 8 == N)
+        hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, true>), grid, dim3(kBlock), 0,
+                           stream, x, xs, w, q8, qs, s, M, n, eps);
+      else
+        hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, false>), grid, dim3(kBlock), 0,
+                           stream, x, xs, w, q8, qs, s, M, n, eps);
     });
   }
   if (!launched) {

@@ -26,12 +26,17 @@ JO_DTYPE_BF16 = 2
 JO_NORM_LAYER = 0
 JO_NORM_RMS = 1
 
+JO_KNOB_QK_SPLIT = 0
+JO_KNOB_KV_SPLIT = 1
+JO_KNOB_GEMM_SHAPE = 2
+
 _P = c_void_p
 _I64 = c_int64
 _F = c_float
 
 # name -> argument types, in header order.
 SIGNATURES: dict[str, list] = {
+    "jo_set_launch_override": [c_int, c_int],
     "jo_sgl_per_token_quant_fp8": [_P, c_int, _I64, _I64, _I64, _P, _I64, _P, _P],
     "jo_fused_qk_norm_rope_3d_paired": [
         _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P, _P],

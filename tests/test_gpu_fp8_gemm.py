@@ -19,13 +19,15 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture(params=["auto", "0", "1", "2", "3", "4"], autouse=True)
-def gemm_shape(request, monkeypatch):
+def gemm_shape(request):
     """Every kernel variant: the default choice, 256x256 (8 waves), 256x128
     (4 waves), the register-staged kernel (also the K % 64 != 0 path), 224x256
     (8 waves, 4 and 3 row blocks) and 224x128 (4 waves)."""
-    if request.param != "auto":
-        monkeypatch.setenv("JO_GEMM_SHAPE", request.param)
-    return request.param
+    from joyomni_ops import _abi
+    value = -1 if request.param == "auto" else int(request.param)
+    _abi.call("jo_set_launch_override", _abi.JO_KNOB_GEMM_SHAPE, value)
+    yield request.param
+    _abi.call("jo_set_launch_override", _abi.JO_KNOB_GEMM_SHAPE, -1)
 
 
 def ulp(x, dtype):

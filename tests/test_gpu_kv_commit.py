@@ -18,15 +18,15 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture(params=["auto", "1", "2"], autouse=True)
-def kv_split(request, monkeypatch):
+def kv_split(request):
     """Every commit test with the automatic launch shape and with K and V on
-    the same wave (1) or on separate waves (2) forced (JO_KV_SPLIT): results
+    the same wave (1) or on separate waves (2) forced (the JO_KNOB_KV_SPLIT launch override): results
     must not depend on it."""
-    if request.param != "auto":
-        monkeypatch.setenv("JO_KV_SPLIT", request.param)
-    else:
-        monkeypatch.delenv("JO_KV_SPLIT", raising=False)
-    return request.param
+    from joyomni_ops import _abi
+    value = -1 if request.param == "auto" else int(request.param)
+    _abi.call("jo_set_launch_override", _abi.JO_KNOB_KV_SPLIT, value)
+    yield request.param
+    _abi.call("jo_set_launch_override", _abi.JO_KNOB_KV_SPLIT, -1)
 
 
 def tables(B, T, D, seed, per_batch=False):

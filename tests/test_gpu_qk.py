@@ -18,14 +18,15 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture(params=["auto", "1", "2", "4", "6", "8"], autouse=True)
-def qk_split(request, monkeypatch):
+def qk_split(request):
     """Run every QK test with the automatic launch shape and with one, two, four,
-    six and eight waves per token forced (JO_QK_SPLIT): results must not depend on it."""
-    if request.param != "auto":
-        monkeypatch.setenv("JO_QK_SPLIT", request.param)
-    else:
-        monkeypatch.delenv("JO_QK_SPLIT", raising=False)
-    return request.param
+    six and eight waves per token forced (the JO_KNOB_QK_SPLIT launch override):
+    results must not depend on it."""
+    from joyomni_ops import _abi
+    value = -1 if request.param == "auto" else int(request.param)
+    _abi.call("jo_set_launch_override", _abi.JO_KNOB_QK_SPLIT, value)
+    yield request.param
+    _abi.call("jo_set_launch_override", _abi.JO_KNOB_QK_SPLIT, -1)
 
 
 def head_floor(ref):
