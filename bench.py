@@ -185,7 +185,7 @@ def time_gpu(cfg, steps: int, warmup: int, dev, use_graph: bool = True) -> dict:
     freqs = None
     if cfg.op in ("qk_grid", "qk_kvcache"):
         d = cfg.dims
-        freqs = jo.rope_freqs(d["D"], d["rope_dims"], d["theta"], device=dev)
+        freqs = jo.rope_freqs(d["D"], d["rope_dims"], d["theta"])
     res = time_launches(lambda i, h: W.launch(cfg, sets[i % n_sets], h, freqs), n_sets, steps,
                         warmup, dev, use_graph)
     del sets

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define JO_ABI_VERSION 1
+#define JO_ABI_VERSION 2
 
 /* Status codes. */
 #define JO_OK 0
@@ -130,8 +130,10 @@ int jo_fused_qk_norm_rope_3d_paired(void* q, void* k, int64_t batch, int64_t seq
  * i < pairs_t + pairs_h, w otherwise; its angle is pos_axis * freqs[i]
  * (fp32 product). If source_id != 0 the pair is further rotated by
  * source_id * freqs[head_dim/2 + i] by angle addition.
- * freqs: device fp32 [2, head_dim/2] (axis frequencies, source-id
- * frequencies); the second row is read only when source_id != 0.
+ * freqs: HOST fp32 [2, head_dim/2] (axis frequencies, source-id
+ * frequencies), copied into the launch's kernel arguments: nothing is
+ * copied to the device, so a call needs no setup and can be captured into
+ * a HIP graph on first use. The second row is used only when source_id != 0.
  * ------------------------------------------------------------------------ */
 int jo_fused_qk_norm_rope_3d_grid(void* q, void* k, int64_t batch, int64_t seq_len,
                                   int64_t num_heads, int64_t head_dim,

@@ -36,6 +36,11 @@ inline bool aligned(const void* p, int64_t bytes) {
   return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes)) == 0;
 }
 
+// Most rows a row-kernel launch takes: at one 256-thread workgroup per row
+// (the generic kernels, and rows wider than a wave) the launch's work-item
+// count must stay below 2^32.
+constexpr int64_t kMaxRows = int64_t{UINT32_MAX} / 256;
+
 // Number of row-kernel workgroups needed for M rows at LPR lanes per row.
 inline int64_t row_blocks(int64_t M, int lpr) {
   const int64_t rows_per_block = 256 / lpr;

@@ -238,7 +238,10 @@ extern "C" int jo_kv_commit_rope(const void* src_k, const void* src_v, void* dst
              static_cast<long long>(dst_tokens));
   const int64_t rows = layers * batch * tokens;
   if (rows == 0) return JO_OK;
-  JO_REQUIRE(rows <= INT32_MAX, "%s: too many rows", op);
+  // Up to two waves of 64 lanes per row: the launch's work-item count must stay
+  // below 2^32.
+  JO_REQUIRE(rows <= int64_t{UINT32_MAX} / (2 * 64), "%s: too many rows (%lld, at most %lld)", op,
+             static_cast<long long>(rows), static_cast<long long>(int64_t{UINT32_MAX} / (2 * 64)));
   JO_REQUIRE(src_k && dst_k && cos && sin, "%s: null pointer", op);
   CommitArgs a{src_k, src_v, dst_k, dst_v, layers, batch, tokens,
                static_cast<int>(num_heads * head_dim), static_cast<int>(head_dim),

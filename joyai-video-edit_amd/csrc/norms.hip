@@ -549,7 +549,8 @@ extern "C" int jo_fused_norm_scale_shift(const void* x, int64_t x_stride, const 
   JO_REQUIRE(valid_dtype(dtype), "Unsupported dtype; use float32/float16/bfloat16");
   JO_REQUIRE(norm_type == JO_NORM_LAYER || norm_type == JO_NORM_RMS,
              "norm_type must be 0 (layer) or 1 (rms)");
-  JO_REQUIRE(M >= 0 && N >= 0 && N <= INT32_MAX, "fused_norm_scale_shift: bad shape");
+  JO_REQUIRE(M >= 0 && N >= 0 && N <= INT32_MAX && M <= kMaxRows,
+             "fused_norm_scale_shift: bad shape");
   JO_REQUIRE(N % 4 == 0, "N must be divisible by 4");
   JO_REQUIRE(x_stride >= N && y_stride >= N && scale_stride >= 0 && shift_stride >= 0,
              "fused_norm_scale_shift: bad row stride");
@@ -568,7 +569,7 @@ extern "C" int jo_rmsnorm(const void* x, int64_t x_stride, const void* weight, v
                           void* stream) {
   // Checks of rmsnorm.cu:77-81.
   JO_REQUIRE(valid_dtype(dtype), "Unsupported dtype; use float32/float16/bfloat16");
-  JO_REQUIRE(M >= 0 && N >= 0 && N <= INT32_MAX, "rmsnorm: bad shape");
+  JO_REQUIRE(M >= 0 && N >= 0 && N <= INT32_MAX && M <= kMaxRows, "rmsnorm: bad shape");
   JO_REQUIRE(x_stride >= N && out_stride >= N, "rmsnorm: bad row stride");
   if (M == 0 || N == 0) return JO_OK;
   JO_REQUIRE(x && weight && out, "rmsnorm: null pointer");
@@ -585,7 +586,7 @@ extern "C" int jo_rmsnorm_heads(const void* x, int64_t x_token_stride, int64_t x
   JO_REQUIRE(valid_dtype(dtype), "Unsupported dtype; use float32/float16/bfloat16");
   JO_REQUIRE(round_first == 0 || round_first == 1, "%s: round_first must be 0 or 1", op);
   JO_REQUIRE(tokens >= 0 && heads > 0 && heads <= INT32_MAX && head_dim > 0 &&
-                 head_dim <= INT32_MAX && tokens * heads <= int64_t{UINT32_MAX},
+                 head_dim <= INT32_MAX && tokens <= kMaxRows && tokens * heads <= kMaxRows,
              "%s: bad shape [%lld, %lld, %lld]", op, static_cast<long long>(tokens),
              static_cast<long long>(heads), static_cast<long long>(head_dim));
   JO_REQUIRE((heads == 1 || x_head_stride >= head_dim) && x_head_stride >= 0 &&
@@ -606,7 +607,8 @@ extern "C" int jo_fused_add_layernorm_scale_shift(
     int64_t scale_stride, const void* shift, int64_t shift_stride, void* y, int64_t y_stride,
     int64_t M, int64_t N, int dtype, float eps, void* stream) {
   JO_REQUIRE(valid_dtype(dtype), "Unsupported dtype; use float32/float16/bfloat16");
-  JO_REQUIRE(M >= 0 && N >= 0 && N <= INT32_MAX, "fused_add_layernorm_scale_shift: bad shape");
+  JO_REQUIRE(M >= 0 && N >= 0 && N <= INT32_MAX && M <= kMaxRows,
+             "fused_add_layernorm_scale_shift: bad shape");
   JO_REQUIRE(N % 4 == 0, "N must be divisible by 4");
   JO_REQUIRE(x_stride >= N && res_stride >= N && y_stride >= N && scale_stride >= 0 &&
                  shift_stride >= 0 && gate_stride >= 0,
@@ -630,13 +632,16 @@ extern "C" int jo_norm_scale_shift_quant_fp8(
              "%s: input must be bf16 or fp16 (the quantized row is the 16-bit y)", op);
   JO_REQUIRE(norm_type == JO_NORM_LAYER || norm_type == JO_NORM_RMS,
              "norm_type must be 0 (layer) or 1 (rms)");
-  JO_REQUIRE(M >= 0 && N >= 0 && N <= INT32_MAX, "%s: bad shape", op);
+  // N == 0 is rejected: there would be scales to write but no values to
+  // take them from.
+  JO_REQUIRE(M >= 0 && N > 0 && N <= INT32_MAX && M <= kMaxRows, "%s: bad shape [%lld, %lld]",
+             op, static_cast<long long>(M), static_cast<long long>(N));
   JO_REQUIRE(N % 4 == 0, "N must be divisible by 4");
   JO_REQUIRE(x_stride >= N && q_stride >= N && scale_stride >= 0 && shift_stride >= 0 &&
                  gate_stride >= 0 && (residual == nullptr || res_stride >= N),
              "%s: bad row stride", op);
   JO_REQUIRE(residual != nullptr || gate == nullptr, "%s: a gate needs a residual", op);
-  if (M == 0 || N == 0) return JO_OK;
+  if (M == 0) return JO_OK;
   JO_REQUIRE(x && out_q && out_s && scale && shift, "%s: null pointer", op);
   NormArgs a{x, x_stride, residual, res_stride, gate, gate_stride, gamma, beta, scale,
              scale_stride, shift, shift_stride, nullptr, 0, M, static_cast<int>(N), eps,

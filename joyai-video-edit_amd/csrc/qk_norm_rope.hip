@@ -13,12 +13,15 @@
 //          and the wave redistributes them with ds_bpermute;
 //   KVC    GRID, with the rotated k written to a frame ring buffer instead
 //          of in place.
+#include <string.h>
+
 #include "jo_device.hpp"
 #include "jo_host.hpp"
 
 namespace jo {
 namespace {
 
+constexpr int kMaxPairs = 128;  // head_dim 256
 constexpr int kTable = 0;
 constexpr int kGrid = 1;
 constexpr int kKvCache = 2;
@@ -36,12 +39,16 @@ struct QKArgs {
   const void* kw;
   const void* cos;  // TABLE
   const void* sin;
-  const float* freqs;  // GRID / KVC: [2, D/2]
   int pairs_t, pairs_h;
   int grid_h, grid_w;
   int t0;
   float source_id;
   int cache_slots, slot_start;  // KVC
+  // GRID / KVC: [2, D/2] axis and source-id frequencies, carried by value in
+  // the kernel arguments (lanes index them with their own pair numbers, which
+  // compiles to loads from the kernel-argument segment). No device copy, so a
+  // grid launch needs no setup and captures into a HIP graph as it is.
+  float freqs[2 * kMaxPairs];
 };
 
 // sin and cos of an fp32 angle a. For |a| <= 65536: Cody-Waite reduction by
@@ -358,9 +365,12 @@ int check_qk(const char* op, const void* q, const void* k, int64_t batch, int64_
   JO_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
              "Unsupported head_dim for %s: %lld", op, static_cast<long long>(head_dim));
   JO_REQUIRE(batch >= 0 && seq_len >= 0 && num_heads > 0, "%s: bad shape", op);
+  // Up to 8 waves of 64 lanes per token: the launch's work-item count must
+  // stay below 2^32.
   JO_REQUIRE(seq_len <= INT32_MAX && num_heads * head_dim <= INT32_MAX &&
-                 batch * seq_len <= INT32_MAX / 8,
-             "%s: shape too large", op);
+                 batch * seq_len <= int64_t{UINT32_MAX} / (8 * kWave),
+             "%s: shape too large (batch * seq_len must not exceed %lld tokens)", op,
+             static_cast<long long>(int64_t{UINT32_MAX} / (8 * kWave)));
   JO_REQUIRE(q_ts >= num_heads * head_dim && k_ts >= num_heads * head_dim,
              "%s: token stride smaller than num_heads*head_dim", op);
   JO_REQUIRE(q_bs >= 0 && k_bs >= 0, "%s: negative batch stride", op);
@@ -376,6 +386,7 @@ int check_qk(const char* op, const void* q, const void* k, int64_t batch, int64_
 int check_grid(const char* op, int64_t seq_len, int64_t head_dim, const float* freqs,
                int32_t pairs_t, int32_t pairs_h, int32_t grid_h, int32_t grid_w) {
   JO_REQUIRE(freqs != nullptr, "%s: null freqs", op);
+  JO_REQUIRE(head_dim / 2 <= kMaxPairs, "%s: head_dim too large for the frequency table", op);
   JO_REQUIRE(grid_h > 0 && grid_w > 0, "%s: grid_h and grid_w must be positive", op);
   JO_REQUIRE(seq_len % (static_cast<int64_t>(grid_h) * grid_w) == 0,
              "%s: seq_len %lld is not a whole number of %dx%d frames", op,
@@ -435,7 +446,8 @@ extern "C" int jo_fused_qk_norm_rope_3d_grid(void* q, void* k, int64_t batch, in
   a.tokens = batch * seq_len; a.seq_len = static_cast<int>(seq_len);
   a.row_elems = static_cast<int>(num_heads * head_dim); a.eps = eps;
   a.qw = q_weight; a.kw = k_weight;
-  a.freqs = freqs; a.pairs_t = pairs_t; a.pairs_h = pairs_h;
+  memcpy(a.freqs, freqs, sizeof(float) * head_dim);
+  a.pairs_t = pairs_t; a.pairs_h = pairs_h;
   a.grid_h = grid_h; a.grid_w = grid_w; a.t0 = t0; a.source_id = source_id;
   return launch_qk<kGrid>(a, static_cast<int>(head_dim), static_cast<hipStream_t>(stream), op);
 }
@@ -470,7 +482,8 @@ extern "C" int jo_fused_qk_norm_rope_3d_kvcache(
   a.tokens = batch * seq_len; a.seq_len = static_cast<int>(seq_len);
   a.row_elems = static_cast<int>(num_heads * head_dim); a.eps = eps;
   a.qw = q_weight; a.kw = k_weight;
-  a.freqs = freqs; a.pairs_t = pairs_t; a.pairs_h = pairs_h;
+  memcpy(a.freqs, freqs, sizeof(float) * head_dim);
+  a.pairs_t = pairs_t; a.pairs_h = pairs_h;
   a.grid_h = grid_h; a.grid_w = grid_w; a.t0 = t0; a.source_id = source_id;
   a.cache_slots = static_cast<int>(cache_slots); a.slot_start = static_cast<int>(slot_start);
   return launch_qk<kKvCache>(a, static_cast<int>(head_dim), static_cast<hipStream_t>(stream), op);

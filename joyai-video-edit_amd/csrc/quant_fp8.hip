@@ -428,6 +428,8 @@ extern "C" int jo_sgl_per_token_quant_fp8(const void* input, int dtype, int64_t 
   JO_REQUIRE(hidden_dim % 4 == 0, "hidden_dim must be divisible by 4, got %lld",
              static_cast<long long>(hidden_dim));
   JO_REQUIRE(hidden_dim <= INT32_MAX, "per_token_quant_fp8: hidden_dim too large");
+  JO_REQUIRE(num_tokens <= kMaxRows, "per_token_quant_fp8: shape too large (more than %lld rows)",
+             static_cast<long long>(kMaxRows));
   JO_REQUIRE(in_stride >= hidden_dim && q_stride >= hidden_dim,
              "per_token_quant_fp8: row stride smaller than hidden_dim");
   if (num_tokens == 0) return JO_OK;
@@ -449,8 +451,9 @@ extern "C" int jo_rmsnorm_quant_fp8(const void* x, int64_t x_stride, const void*
   JO_REQUIRE(group_size == 0 || group_size == 128,
              "rmsnorm_quant_fp8: group_size must be 0 (per token) or 128, got %lld",
              static_cast<long long>(group_size));
-  JO_REQUIRE(M >= 0 && N > 0, "rmsnorm_quant_fp8: bad shape [%lld, %lld]",
-             static_cast<long long>(M), static_cast<long long>(N));
+  JO_REQUIRE(M >= 0 && N > 0 && N <= INT32_MAX && M <= kMaxRows,
+             "rmsnorm_quant_fp8: bad shape [%lld, %lld]", static_cast<long long>(M),
+             static_cast<long long>(N));
   JO_REQUIRE(N % 8 == 0, "rmsnorm_quant_fp8: N must be divisible by 8, got %lld",
              static_cast<long long>(N));
   JO_REQUIRE(group_size == 0 || N % 128 == 0,

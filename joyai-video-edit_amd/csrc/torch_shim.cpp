@@ -269,7 +269,10 @@ QKGeom check_qk_common(const torch::Tensor& q, const torch::Tensor& k, int64_t s
   JO_CHECK_DTYPE(k, torch::kBFloat16);
   JO_CHECK_INPUT(q_weight, torch::kBFloat16);
   JO_CHECK_INPUT(k_weight, torch::kBFloat16);
-  JO_CHECK_INPUT(freqs, torch::kFloat32);
+  TORCH_CHECK(freqs.device().is_cpu(),
+              "freqs must be a CPU tensor (its values are passed in the kernel arguments)");
+  JO_CHECK_CONTIGUOUS(freqs);
+  JO_CHECK_DTYPE(freqs, torch::kFloat32);
   const int64_t head_dim = q.size(q.dim() - 1);
   TORCH_CHECK(q_weight.numel() == head_dim && k_weight.numel() == head_dim,
               "weight size must match head_dim");

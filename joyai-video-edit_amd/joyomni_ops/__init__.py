@@ -99,9 +99,8 @@ _FREQ_CACHE: dict = {}
 
 
 def rope_freqs(head_dim: int, rope_dims: Sequence[int], theta: float,
-               source_theta: float = 256.0, source_dim: Optional[int] = None,
-               device=None) -> torch.Tensor:
-    """fp32 [2, head_dim/2] frequency table read by the grid RoPE ops.
+               source_theta: float = 256.0, source_dim: Optional[int] = None) -> torch.Tensor:
+    """fp32 [2, head_dim/2] frequency table of the grid RoPE ops, in host memory.
 
     Row 0 holds, per rotation pair, the frequency of its axis: the t, h and w
     axes take rope_dims[0]/2, rope_dims[1]/2 and rope_dims[2]/2 consecutive
@@ -109,15 +108,17 @@ def rope_freqs(head_dim: int, rope_dims: Sequence[int], theta: float,
     Row 1 holds the source-id frequencies 1 / source_theta^(2j/source_dim)
     for the first source_dim/2 pairs and 0 after them
     (deploy/xvideo/models/dit/dit.py:796-805; a zero frequency is the
-    identity rotation the reference uses there). The values are computed with
-    the same fp32 torch expressions as the reference and cached per device.
+    identity rotation the reference uses there). source_dim defaults to
+    head_dim. The values are computed with the same fp32 torch expressions as
+    the reference and cached. The ops take the table by value (it travels in
+    the kernel arguments), so it stays on the host: a grid op needs no device
+    copy and can be captured into a HIP graph on its first call.
     """
     dims = tuple(int(d) for d in rope_dims)
     if len(dims) != 3 or sum(dims) != head_dim or any(d % 2 for d in dims):
         raise ValueError(f"rope_dims {dims} must be 3 even sizes summing to head_dim {head_dim}")
     role = head_dim if source_dim is None else max(0, min(int(source_dim), head_dim))
-    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-    key = (dev, head_dim, dims, float(theta), float(source_theta), role)
+    key = (head_dim, dims, float(theta), float(source_theta), role)
     t = _FREQ_CACHE.get(key)
     if t is None:
         rows = []
@@ -128,7 +129,7 @@ def rope_freqs(head_dim: int, rope_dims: Sequence[int], theta: float,
         if role > 0:
             sid[: role // 2] = 1.0 / (
                 source_theta ** (torch.arange(0, role, 2, dtype=torch.float32) / role))
-        t = torch.stack([axis, sid]).to(dev)
+        t = torch.stack([axis, sid]).contiguous()
         _FREQ_CACHE[key] = t
     return t
 

@@ -92,7 +92,10 @@ def fused_qk_norm_rope_3d(
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Per-head RMSNorm + interleaved RoPE of q, k [B, L, H, D] from
     (cos, sin) tables [1, L, D] or [L, D/2] (sgl_fused_ops.py:57-99). Returns
-    new contiguous (q, k); the inputs are not modified."""
+    contiguous (q, k): copies when q / k are strided views (such as the slices
+    of a packed qkv), which leaves the inputs untouched; q / k themselves,
+    rotated in place, when they are already contiguous (.contiguous() is then
+    a no-op), as in the reference."""
     if q.dtype != torch.bfloat16:
         raise RuntimeError(f"fused_qk_norm_rope_3d requires bf16 q/k, got {q.dtype}")
     B, L, H, D = q.shape
@@ -221,19 +224,22 @@ def fused_qk_norm_rope_3d_grid_views(
     theta: float,
     source_id: float = 0.0,
     source_theta: float = 256.0,
+    source_dim: int = 128,
     eps: float = 1e-6,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """In-place RMSNorm + RoPE of q, k [B, L, H, D] that may be strided views of
     a packed qkv [B, L, 3, H, D] (heads contiguous per token). Angles come from
     the grid position (frame f of L / (H_grid * W_grid) at t0 + f), with the
-    optional source-id rotation, exactly as Transformer3DModel builds its
-    tables (dit.py:745-809, 918-933); no tables are read. Returns (q, k)."""
+    optional source-id rotation over the first min(source_dim, D) dims (the
+    model's source_id_rope_dim = 128 and source_id_rope_theta = 256,
+    dit.py:549-550,792), exactly as Transformer3DModel builds its tables
+    (dit.py:745-809, 918-933); no tables are read. Returns (q, k)."""
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
         raise RuntimeError("q/k must be bf16")
     B, L, H, D = q.shape
     if q.stride(-1) != 1 or q.stride(-2) != D or k.stride(-1) != 1 or k.stride(-2) != D:
         raise RuntimeError("heads of a token must be contiguous in q and k")
-    freqs = rope_freqs(D, rope_dims, theta, source_theta, device=q.device)
+    freqs = rope_freqs(D, rope_dims, theta, source_theta, source_dim)
     qw = q_norm_weight.to(torch.bfloat16).contiguous()
     kw = k_norm_weight.to(torch.bfloat16).contiguous()
     fused_qk_norm_rope_3d_grid(q, k, L, H, eps, qw, kw, freqs, rope_dims, grid_hw, t0, source_id)

@@ -1,8 +1,12 @@
 """Build the C part of the oracle (TEST INFRASTRUCTURE): oracle/_build/libfp8ref.so.
 
 The reference's own kernels are CUDA and cannot be compiled in this image
-(no nvcc), so there is no oracle/_ref build; the restatement in oracle/ is pinned by
-the reference's golden vectors and closed-form checks instead.
+(no nvcc), so there is no oracle/_ref build. The reference ships no golden
+vectors or known-answer tests for this path either, so the restatement in
+oracle/ is pinned by independent checks (tests/test_oracle.py): a brute-force
+e4m3fn encoder, hand-derived known-answer rows, library routines
+(F.layer_norm, F.rms_norm, complex multiplication), float64 closed forms,
+invariants, and planted mistakes that must be caught.
 """
 from __future__ import annotations
 

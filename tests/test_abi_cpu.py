@@ -55,8 +55,13 @@ def test_ctypes_signatures_match_header(abi):
 
 
 def test_abi_version(abi):
-    assert abi.lib().jo_abi_version() == 1
+    assert abi.lib().jo_abi_version() == 2
 
+
+# Launch-size bounds of the entry points (work items of one launch < 2^32).
+QK_MAX_TOKENS = (2**32 - 1) // (8 * 64)
+KV_MAX_ROWS = (2**32 - 1) // (2 * 64)
+MAX_ROWS = (2**32 - 1) // 256
 
 # Validation paths return before any HIP call, so they run without a GPU.
 BAD_CALLS = [
@@ -91,9 +96,36 @@ BAD_CALLS = [
      "divisible by 4"),
     ("jo_fused_norm_scale_shift", (16, 8, None, None, 16, 8, 16, 8, 16, 8, 4, 8, 7, 0, 1e-6, None),
      "dtype"),
+    # launch-size bounds: a launch's work-item count must stay below 2^32 (up to 8 waves of
+    # 64 lanes per QK token, 2 waves per KV-pool row, one 256-thread workgroup per row)
     ("jo_fused_qk_norm_rope_3d_paired",
      (16, 16, 2, 1 << 28, 2, 128, 256 << 28, 256, 256 << 28, 256, 1e-6, 16, 16, 16, 16, None),
      "shape too large"),
+    ("jo_fused_qk_norm_rope_3d_paired",
+     (16, 16, 1, QK_MAX_TOKENS + 1, 2, 128, 256 * (QK_MAX_TOKENS + 1), 256,
+      256 * (QK_MAX_TOKENS + 1), 256, 1e-6, 16, 16, 16, 16, None), "shape too large"),
+    ("jo_fused_qk_norm_rope_3d_paired",  # at the bound: passes the shape check, stops at the pointer
+     (None, 16, 1, QK_MAX_TOKENS, 2, 128, 256 * QK_MAX_TOKENS, 256, 256 * QK_MAX_TOKENS, 256,
+      1e-6, 16, 16, 16, 16, None), "null pointer"),
+    ("jo_kv_commit_rope",
+     (16, None, 16, None, 1, 1, KV_MAX_ROWS + 1, 2, 128, 256 * (KV_MAX_ROWS + 1),
+      256 * (KV_MAX_ROWS + 1), 256, 256 * (KV_MAX_ROWS + 1), 256 * (KV_MAX_ROWS + 1), 256,
+      KV_MAX_ROWS + 1, 0, 16, 16, 128, 0, 2, None), "too many rows"),
+    ("jo_kv_commit_rope",
+     (None, None, 16, None, 1, 1, KV_MAX_ROWS, 2, 128, 256 * KV_MAX_ROWS, 256 * KV_MAX_ROWS, 256,
+      256 * KV_MAX_ROWS, 256 * KV_MAX_ROWS, 256, KV_MAX_ROWS, 0, 16, 16, 128, 0, 2, None),
+     "null pointer"),
+    ("jo_rmsnorm", (16, 8, 16, 16, 8, MAX_ROWS + 1, 8, 2, 1e-6, None), "bad shape"),
+    ("jo_rmsnorm", (None, 8, 16, 16, 8, MAX_ROWS, 8, 2, 1e-6, None), "null pointer"),
+    ("jo_sgl_per_token_quant_fp8", (16, 2, MAX_ROWS + 1, 8, 8, 16, 8, 16, None), "shape too large"),
+    ("jo_rmsnorm_quant_fp8", (16, 256, 16, 16, 256, 16, MAX_ROWS + 1, 256, 2, 1e-6, 0, None),
+     "bad shape"),
+    ("jo_rmsnorm_heads", (16, 1152, 128, 16, 16, 128, MAX_ROWS // 3 + 1, 3, 128, 2, 1e-6, 0, None),
+     "bad shape"),
+    # zero-width rows would leave scales with nothing to take them from
+    ("jo_norm_scale_shift_quant_fp8",
+     (16, 8, None, 8, None, 0, None, None, 16, 0, 16, 0, 16, 8, 16, 4, 0, 2, 0, 1e-6, None),
+     "bad shape"),
     ("jo_rmsnorm", (16, 8, 16, None, 8, 4, 8, 2, 1e-6, None), "null pointer"),
     ("jo_rmsnorm_heads", (16, 1152, 128, 16, 16, 128, 4, 3, 128, 2, 1e-6, 2, None), "round_first"),
     ("jo_rmsnorm_heads", (16, 1152, 128, 16, 16, 128, 4, 0, 128, 2, 1e-6, 0, None), "bad shape"),
@@ -114,6 +146,16 @@ def test_validation_errors_without_gpu(abi, name, args, msg):
     status = getattr(abi.lib(), name)(*args)
     assert status == abi.JO_ERR_INVALID
     assert msg in abi.last_error()
+
+
+def test_launch_override(abi):
+    lib = abi.lib()
+    for knob in (abi.JO_KNOB_QK_SPLIT, abi.JO_KNOB_KV_SPLIT, abi.JO_KNOB_GEMM_SHAPE):
+        assert lib.jo_set_launch_override(knob, 4) == abi.JO_OK
+        assert lib.jo_set_launch_override(knob, -1) == abi.JO_OK
+    assert lib.jo_set_launch_override(3, 1) == abi.JO_ERR_INVALID
+    assert "unknown knob" in abi.last_error()
+    assert lib.jo_set_launch_override(abi.JO_KNOB_QK_SPLIT, -2) == abi.JO_ERR_INVALID
 
 
 def test_empty_inputs_are_noops(abi):

@@ -95,7 +95,7 @@ def test_golden_qk_grid(fx, dev):
     ref_q, ref_k = torch.from_numpy(fx["qkg_q_ref"]), torch.from_numpy(fx["qkg_k_ref"])
     _, L, H, D = ref_q.shape
     dims = (44, 42, 42)
-    freqs = jo.rope_freqs(D, dims, 10000.0, 256.0, device=dev)
+    freqs = jo.rope_freqs(D, dims, 10000.0, 256.0)
     jo.fused_qk_norm_rope_3d_grid(q, k, L, H, 1e-6, bf16(fx["qkg_wq"]).to(dev),
                                   bf16(fx["qkg_wk"]).to(dev), freqs, dims, (3, 5), 7, 1.0)
     torch.cuda.synchronize()

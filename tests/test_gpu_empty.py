@@ -77,9 +77,48 @@ def case_apply_rotary_emb(jo, dev):
     return [(y, (1, 0, 4, 128), BF)]
 
 
+def _qk(dev, H=4, D=128):
+    q = torch.empty(1, 0, D, dtype=BF, device=dev)
+    k = torch.empty(1, 0, D, dtype=BF, device=dev)
+    return q, k, torch.ones(D, dtype=BF, device=dev)
+
+
+def case_qk_paired(jo, dev):
+    q, k, w = _qk(dev)
+    t = torch.empty(0, 64, dtype=BF, device=dev)
+    jo.fused_qk_norm_rope_3d_paired(q, k, 0, 4, 1e-6, w, w, t, t)
+    return [(q, (1, 0, 128), BF), (k, (1, 0, 128), BF)]
+
+
+def case_qk_grid(jo, dev):
+    q, k, w = _qk(dev)
+    freqs = jo.rope_freqs(128, (44, 42, 42), 10000.0)
+    jo.fused_qk_norm_rope_3d_grid(q, k, 0, 4, 1e-6, w, w, freqs, (44, 42, 42), (3, 5), 0)
+    return [(q, (1, 0, 128), BF), (k, (1, 0, 128), BF)]
+
+
+def case_qk_kvcache(jo, dev):
+    q, k, w = _qk(dev)
+    cache = torch.zeros(1, 2 * 15 * 4, 128, dtype=BF, device=dev)  # 2 slots of 3x5-token frames
+    freqs = jo.rope_freqs(128, (44, 42, 42), 10000.0)
+    jo.fused_qk_norm_rope_3d_kvcache(q, k, cache, 0, 4, 1e-6, w, w, freqs, (44, 42, 42), (3, 5),
+                                     0, 0)
+    assert torch.count_nonzero(cache).item() == 0  # nothing written
+    return [(q, (1, 0, 128), BF), (cache, (1, 120, 128), BF)]
+
+
+def case_kv_commit(jo, dev):
+    src = torch.empty(2, 1, 0, 4, 128, dtype=BF, device=dev)
+    dst = torch.zeros(2, 1, 8, 4, 128, dtype=BF, device=dev)
+    t = torch.empty(0, 128, dtype=torch.float32, device=dev)
+    jo.kv_commit_rope(src, dst, 8, t, t, src_v=src, dst_v=dst.clone())
+    assert torch.count_nonzero(dst).item() == 0
+    return [(dst, (2, 1, 8, 4, 128), BF)]
+
+
 CASES = [case_norm_scale_shift, case_rmsnorm, case_per_token_quant, case_fp8_scaled_mm,
          case_add_layernorm, case_rmsnorm_quant, case_norm_quant, case_rmsnorm_heads,
-         case_apply_rotary_emb]
+         case_apply_rotary_emb, case_qk_paired, case_qk_grid, case_qk_kvcache, case_kv_commit]
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c.__name__[5:] for c in CASES])

@@ -148,7 +148,7 @@ def test_grid_mode(abi, dev, stream_handle, case):
     B, F, gh, gw, H, D, t0, dims, theta, sid = case
     L = F * gh * gw
     q, k, qw, kw = rand_qk(B, L, H, D, L + H + D)
-    freqs = jo.rope_freqs(D, dims, theta, 256.0, device=dev)
+    freqs = jo.rope_freqs(D, dims, theta, 256.0)
     qd, kd = q.to(dev), k.to(dev)
     grid_call(abi, stream_handle, qd, kd, B, L, H, D, qw.to(dev), kw.to(dev), freqs, dims, gh, gw, t0, sid)
     torch.cuda.synchronize()
@@ -163,7 +163,7 @@ def test_grid_mode_torch_op_c0(dev):
     d = cfg.dims
     t = W.make_inputs(cfg)
     qd, kd = t["q"].to(dev), t["k"].to(dev)
-    freqs = jo.rope_freqs(d["D"], d["rope_dims"], d["theta"], device=dev)
+    freqs = jo.rope_freqs(d["D"], d["rope_dims"], d["theta"])
     jo.fused_qk_norm_rope_3d_grid(qd, kd, d["L"], d["H"], d["eps"], t["q_weight"].to(dev),
                                   t["k_weight"].to(dev), freqs, d["rope_dims"], d["grid"], d["t0"])
     torch.cuda.synchronize()
@@ -194,7 +194,7 @@ def test_kvcache_mode(abi, dev, stream_handle, small):
     slot0 = jo.kv_ring_slot(t0, F, slots)
     cache = torch.full((B, slots * ft * H, D), 7.0, dtype=torch.bfloat16, device=dev)
     qd, kd = q.to(dev), k.to(dev)
-    freqs = jo.rope_freqs(D, dims, theta, device=dev)
+    freqs = jo.rope_freqs(D, dims, theta)
     jo.fused_qk_norm_rope_3d_kvcache(qd, kd, cache, L, H, 1e-6, qw.to(dev), kw.to(dev), freqs,
                                      dims, (gh, gw), t0, slot0)
     torch.cuda.synchronize()

@@ -4,9 +4,9 @@ Bar: bit-exact e4m3fn bytes and bit-exact fp32 scales against the CPU oracle
 (per_token_quant_fp8.cu:56-82 restated in oracle/ops.py, itself pinned by the
 C brute-force encoder), on random rows with outliers, hand known-answer rows,
 every row-shape dispatch class, strided and unaligned views, and the full C1
-shape. RMSNorm->FP8 (C4) compares scales within 2 fp32 ulps and bytes exactly
-after re-quantizing the oracle's fp32 values with the GPU's scales, except on
-provable near-ties of the fp32 sums.
+shape. RMSNorm->FP8 (C4, per token and per 1x128 block) is bit-exact too:
+fp8 bytes and fp32 scales equal to the oracle's, whose mean square is the
+exactly rounded mean of the exact squares, as the kernel's.
 """
 from __future__ import annotations
 
