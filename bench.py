@@ -18,7 +18,10 @@ reference-signature ops at the DiT block's deployment shapes (hidden 4096,
 modulation, per-token quant of [3120, 4096] and [3120, 16384], and the
 pre-RoPE K RMSNorm over [99840, 128] — on a contiguous copy (R_rms, the
 reference caller's layout) and read straight from the packed qkv (R_kn, whose
-line adds the time of the caller's copy-then-norm path). T_* are the shapes of
+line adds the time of the caller's copy-then-norm path), and the
+K-cache-before-RoPE branch in one pass (R_qks: QK norm + RoPE in place on the
+packed qkv plus the pre-RoPE K stage; its line adds the time of the two calls
+the reference makes). T_* are the shapes of
 the reference's own benchmark script (test_bench.py): rmsnorm and LayerNorm +
 modulation at [4096, 4096], table-mode QK at [1, 1560, 32, 128], the FP8 GEMM
 at 4096^3.
@@ -415,6 +418,41 @@ def copy_then_rmsnorm_us(cfg, dev, iters: int = 20):
     return round(us, 1)
 
 
+def unfused_kstage_us(cfg, dev, iters: int = 20):
+    """R_qks's branch as the reference caller takes it (dit.py:360-370 over
+    sgl_fused_ops.py:57-111): rmsnorm_qk_bf16 of the K slice (this build's op,
+    reading the slice in place), then fused_qk_norm_rope_3d with its
+    .contiguous() copies of q and k and the paired op, eager, per call."""
+    if cfg.op != "qk_kstage":
+        return None
+    import torch
+
+    from joyomni_ops import dit_ops
+    from joyomni_ops import workloads as W
+    sets = [{k: v.to(dev) for k, v in W.make_inputs(cfg).items()} for _ in range(4)]
+
+    def call(t):
+        qkv = t["qkv"]
+        kc = dit_ops.rmsnorm_qk_bf16(qkv[:, :, 1], t["k_weight"], eps=1e-6)
+        q, k = dit_ops.fused_qk_norm_rope_3d(qkv[:, :, 0], qkv[:, :, 1], t["q_weight"],
+                                             t["k_weight"], (t["cos"], t["sin"]), eps=1e-6)
+        return q, k, kc
+
+    for i in range(4):
+        call(sets[i])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(iters):
+        call(sets[i % 4])
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / iters
+    del sets
+    torch.cuda.empty_cache()
+    return round(us, 1)
+
+
 def cpu_fn(cfg):
     """The oracle's restatement of the reference formula for a config (CPU tensors)."""
     from oracle import ops
@@ -555,6 +593,9 @@ def main() -> int:
         caller_us = copy_then_rmsnorm_us(cfg, dev)
         if caller_us is not None:
             results[n]["copy_then_rmsnorm_us_per_call"] = caller_us
+        two_call_us = unfused_kstage_us(cfg, dev)
+        if two_call_us is not None:
+            results[n]["unfused_two_calls_us_per_call"] = two_call_us
         flops = W.algorithmic_flops(cfg)
         if flops is not None:
             tf = flops / (results[n]["us_per_call"] * 1e-6) / 1e12

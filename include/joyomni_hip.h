@@ -145,6 +145,42 @@ int jo_fused_qk_norm_rope_3d_grid(void* q, void* k, int64_t batch, int64_t seq_l
                                   float source_id, void* stream);
 
 /* ------------------------------------------------------------------------
+ * jo_fused_qk_norm_rope_3d_paired / _grid with a second output: the
+ * pre-RoPE normalized K, written to k_stage in the same pass that rotates q
+ * and k in place, so K is read once:
+ *   k_stage[b, n, h, :] = bf16((x * r') * k_weight),
+ *   r' = 1 / sqrt(sum(x^2) / head_dim + eps)   (separate IEEE operations)
+ * for every head vector x of k — bit for bit the row that rmsnorm_qk_bf16
+ * (jo_rmsnorm_heads with round_first = 0, or jo_rmsnorm on the rows)
+ * returns for the same k.
+ * Replaces the pair of calls of the DiT's pre-RoPE KV-cache path
+ *   (deploy/xvideo/models/dit/dit.py:360-370: rmsnorm_qk_bf16 of the K slice,
+ *    then fused_qk_norm_rope_3d; sgl_fused_ops.py:57-111), whose first call
+ *    re-reads K. The stage rows feed the graph runner's pre-RoPE K buffers
+ *    (deploy/xvideo/serving/graph_runner.py:56-59,93-95).
+ * k_stage: bf16 [batch, seq_len, num_heads, head_dim] with the given batch and
+ * token strides (heads contiguous), 16-byte aligned, not overlapping q or k.
+ * The other arguments are those of the entry point without _kstage.
+ * ------------------------------------------------------------------------ */
+int jo_fused_qk_norm_rope_3d_paired_kstage(void* q, void* k, void* k_stage, int64_t batch,
+                                           int64_t seq_len, int64_t num_heads, int64_t head_dim,
+                                           int64_t q_batch_stride, int64_t q_token_stride,
+                                           int64_t k_batch_stride, int64_t k_token_stride,
+                                           int64_t stage_batch_stride,
+                                           int64_t stage_token_stride, float eps,
+                                           const void* q_weight, const void* k_weight,
+                                           const void* cos, const void* sin, void* stream);
+int jo_fused_qk_norm_rope_3d_grid_kstage(void* q, void* k, void* k_stage, int64_t batch,
+                                         int64_t seq_len, int64_t num_heads, int64_t head_dim,
+                                         int64_t q_batch_stride, int64_t q_token_stride,
+                                         int64_t k_batch_stride, int64_t k_token_stride,
+                                         int64_t stage_batch_stride, int64_t stage_token_stride,
+                                         float eps, const void* q_weight, const void* k_weight,
+                                         const float* freqs, int32_t pairs_t, int32_t pairs_h,
+                                         int32_t grid_h, int32_t grid_w, int32_t t0,
+                                         float source_id, void* stream);
+
+/* ------------------------------------------------------------------------
  * Grid-mode QK norm + RoPE that writes the rotated K straight into a frame
  * ring buffer: q is updated in place, k is only read, and the rotated head
  * vectors of k for frame f go to cache frame slot (slot_start + f) % cache_slots,
@@ -220,7 +256,10 @@ int jo_rmsnorm_heads(const void* x, int64_t x_token_stride, int64_t x_head_strid
  * fused_norm_scale_shift LayerNorm path (fused_norm_scale_shift.cu:88-142) as
  * the DiT block uses them back to back (dit.py:447-476).
  * x: [M, N]; residual: [M, N], updated in place; y: [M, N];
- * gate, scale, shift: [M, N] row-strided, stride 0 = one [N] row for all.
+ * gate, scale, shift: row-strided, stride 0 = one [N] row for all; with a
+ * nonzero stride, modulation row r serves rows r*mod_rows .. r*mod_rows +
+ * mod_rows - 1 of x (mod_rows = 1: a row each; mod_rows = L: one row per
+ * sample of a [B, L, N] batch, as the DiT's per-sample AdaLN vectors).
  * gamma/beta as in jo_fused_norm_scale_shift. N % 4 == 0.
  * ------------------------------------------------------------------------ */
 int jo_fused_add_layernorm_scale_shift(const void* x, int64_t x_stride, void* residual,
@@ -228,9 +267,9 @@ int jo_fused_add_layernorm_scale_shift(const void* x, int64_t x_stride, void* re
                                        int64_t gate_stride, const void* gamma,
                                        const void* beta, const void* scale,
                                        int64_t scale_stride, const void* shift,
-                                       int64_t shift_stride, void* y, int64_t y_stride,
-                                       int64_t M, int64_t N, int dtype, float eps,
-                                       void* stream);
+                                       int64_t shift_stride, int64_t mod_rows, void* y,
+                                       int64_t y_stride, int64_t M, int64_t N, int dtype,
+                                       float eps, void* stream);
 
 /* ------------------------------------------------------------------------
  * RMSNorm with an FP8 e4m3 quantization epilogue.
@@ -266,16 +305,19 @@ int jo_rmsnorm_quant_fp8(const void* x, int64_t x_stride, const void* weight, vo
  * activation quantization Fp8Linear.forward runs on that y
  * (fp8_linear.py:138-169, per_token_quant_fp8.cu:56-82).
  * x: [M, N]; residual: [M, N] or NULL; gate, scale, shift: row-strided,
- * stride 0 = one [N] row for all; gamma/beta as in jo_fused_norm_scale_shift;
- * out_q: fp8 [M, N] with row stride q_stride; out_s: fp32 [M].
- * dtype bf16 or fp16; norm_type JO_NORM_LAYER or JO_NORM_RMS; N % 4 == 0.
+ * stride 0 = one [N] row for all, mod_rows consecutive rows of x per
+ * modulation row otherwise (as in jo_fused_add_layernorm_scale_shift);
+ * gamma/beta as in jo_fused_norm_scale_shift; out_q: fp8 [M, N] with row
+ * stride q_stride; out_s: fp32 [M]. dtype bf16 or fp16; norm_type
+ * JO_NORM_LAYER or JO_NORM_RMS; N % 4 == 0 and N > 0.
  * ------------------------------------------------------------------------ */
 int jo_norm_scale_shift_quant_fp8(const void* x, int64_t x_stride, void* residual,
                                   int64_t res_stride, const void* gate, int64_t gate_stride,
                                   const void* gamma, const void* beta, const void* scale,
                                   int64_t scale_stride, const void* shift, int64_t shift_stride,
-                                  void* out_q, int64_t q_stride, float* out_s, int64_t M,
-                                  int64_t N, int dtype, int norm_type, float eps, void* stream);
+                                  int64_t mod_rows, void* out_q, int64_t q_stride, float* out_s,
+                                  int64_t M, int64_t N, int dtype, int norm_type, float eps,
+                                  void* stream);
 
 /* ------------------------------------------------------------------------
  * Row-wise scaled FP8 GEMM with optional bias.

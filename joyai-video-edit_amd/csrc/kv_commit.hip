@@ -226,7 +226,6 @@ extern "C" int jo_kv_commit_rope(const void* src_k, const void* src_v, void* dst
   JO_REQUIRE(head_dim % 2 == 0, "RoPE requires an even head dimension, got %lld",
              static_cast<long long>(head_dim));
   JO_REQUIRE(num_heads * head_dim <= INT32_MAX / 2, "%s: row too long", op);
-  JO_REQUIRE((src_v == nullptr) == (dst_v == nullptr), "%s: V needs both a source and a destination", op);
   JO_REQUIRE(src_token_stride >= num_heads * head_dim && dst_token_stride >= num_heads * head_dim &&
                  src_layer_stride >= 0 && src_batch_stride >= 0 && dst_layer_stride >= 0 &&
                  dst_batch_stride >= 0 && dst_token_offset >= 0 && table_stride >= head_dim &&
@@ -237,7 +236,11 @@ extern "C" int jo_kv_commit_rope(const void* src_k, const void* src_v, void* dst
              static_cast<long long>(tokens), static_cast<long long>(dst_token_offset),
              static_cast<long long>(dst_tokens));
   const int64_t rows = layers * batch * tokens;
+  // Zero rows: nothing to read or write (an empty tensor's data pointer may be
+  // null, so the V pointer pair is checked only when there is work).
   if (rows == 0) return JO_OK;
+  JO_REQUIRE((src_v == nullptr) == (dst_v == nullptr),
+             "%s: V needs both a source and a destination", op);
   // Up to two waves of 64 lanes per row: the launch's work-item count must stay
   // below 2^32.
   JO_REQUIRE(rows <= int64_t{UINT32_MAX} / (2 * 64), "%s: too many rows (%lld, at most %lld)", op,

@@ -34,7 +34,16 @@ struct NormArgs {
   uint8_t* q = nullptr;  // FP8 epilogue: e4m3fn rows (stride qs) and fp32 scales [M]
   int64_t qs = 0;
   float* s = nullptr;
+  uint32_t mod_rows = 1;  // rows that share one gate / scale / shift row
 };
+
+// Row of the gate / scale / shift tensors that serves row `row` of x: the
+// same row, or one row per mod_rows consecutive rows (one per sample of a
+// [B, L, N] batch). M < 2^32 (checked on the host), so 32-bit division.
+__device__ __forceinline__ int64_t mod_row(const NormArgs& a, int64_t row) {
+  return a.mod_rows == 1 ? row
+                         : static_cast<int64_t>(static_cast<uint32_t>(row) / a.mod_rows);
+}
 
 constexpr int kLayer = JO_NORM_LAYER;
 constexpr int kRms = JO_NORM_RMS;
@@ -89,6 +98,7 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
   const int lane = threadIdx.x % LPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
   const bool row_ok = row < a.M;
+  const int64_t mrow = mod_row(a, row);
   const int N = a.N;
 
   // BCAST: one scale row and one shift row for all rows (stride 0, no
@@ -120,7 +130,7 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
       const int e = (i * LPR + lane) * V;
       const bool ok = row_ok && e < N;
       rc[i] = ok ? ld_row<Tag>(a.res, row * a.rs, e) : u32x4{0u, 0u, 0u, 0u};
-      gc[i] = (ok && a.gate) ? ld_mod<Tag>(a.gate, a.gs, row, e) : u32x4{0u, 0u, 0u, 0u};
+      gc[i] = (ok && a.gate) ? ld_mod<Tag>(a.gate, a.gs, mrow, e) : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
@@ -192,8 +202,8 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
       sc = bsc[i];
       sh = bsh[i];
     } else {
-      sc = ld_mod<Tag>(a.scale, a.scs, row, e);
-      sh = ld_mod<Tag>(a.shift, a.shs, row, e);
+      sc = ld_mod<Tag>(a.scale, a.scs, mrow, e);
+      sh = ld_mod<Tag>(a.shift, a.shs, mrow, e);
     }
     u32x4 gm = u32x4{0u, 0u, 0u, 0u}, bt = u32x4{0u, 0u, 0u, 0u};
     if (affine) gm = ld_chunk<Tag>(a.gamma, 0, e);
@@ -253,8 +263,9 @@ __global__ __launch_bounds__(kBlock) void norm_mod_generic_kernel(const NormArgs
   __shared__ float red[kBlock / kWave];
   const int64_t row = blockIdx.x;
   const int N = a.N;
-  const int64_t xo = row * a.xs, ro = row * a.rs, go = row * a.gs;
-  const int64_t so = row * a.scs, ho = row * a.shs, yo = row * a.ys;
+  const int64_t mrow = mod_row(a, row);
+  const int64_t xo = row * a.xs, ro = row * a.rs, go = mrow * a.gs;
+  const int64_t so = mrow * a.scs, ho = mrow * a.shs, yo = row * a.ys;
   if constexpr (ADD) {
     // Each thread later reads back exactly the elements it writes here.
     for (int i = threadIdx.x; i < N; i += kBlock) {
@@ -604,8 +615,8 @@ extern "C" int jo_rmsnorm_heads(const void* x, int64_t x_token_stride, int64_t x
 extern "C" int jo_fused_add_layernorm_scale_shift(
     const void* x, int64_t x_stride, void* residual, int64_t res_stride, const void* gate,
     int64_t gate_stride, const void* gamma, const void* beta, const void* scale,
-    int64_t scale_stride, const void* shift, int64_t shift_stride, void* y, int64_t y_stride,
-    int64_t M, int64_t N, int dtype, float eps, void* stream) {
+    int64_t scale_stride, const void* shift, int64_t shift_stride, int64_t mod_rows, void* y,
+    int64_t y_stride, int64_t M, int64_t N, int dtype, float eps, void* stream) {
   JO_REQUIRE(valid_dtype(dtype), "Unsupported dtype; use float32/float16/bfloat16");
   JO_REQUIRE(M >= 0 && N >= 0 && N <= INT32_MAX && M <= kMaxRows,
              "fused_add_layernorm_scale_shift: bad shape");
@@ -613,11 +624,14 @@ extern "C" int jo_fused_add_layernorm_scale_shift(
   JO_REQUIRE(x_stride >= N && res_stride >= N && y_stride >= N && scale_stride >= 0 &&
                  shift_stride >= 0 && gate_stride >= 0,
              "fused_add_layernorm_scale_shift: bad row stride");
+  JO_REQUIRE(mod_rows >= 1 && mod_rows <= UINT32_MAX,
+             "fused_add_layernorm_scale_shift: mod_rows must be positive");
   if (M == 0 || N == 0) return JO_OK;
   JO_REQUIRE(x && residual && y && scale && shift,
              "fused_add_layernorm_scale_shift: null pointer");
   NormArgs a{x, x_stride, residual, res_stride, gate, gate_stride, gamma, beta, scale,
              scale_stride, shift, shift_stride, y, y_stride, M, static_cast<int>(N), eps};
+  a.mod_rows = static_cast<uint32_t>(mod_rows);
   return launch_norm_mod_dt<kLayer, true>(dtype, a, static_cast<hipStream_t>(stream),
                                           "fused_add_layernorm_scale_shift");
 }
@@ -625,8 +639,9 @@ extern "C" int jo_fused_add_layernorm_scale_shift(
 extern "C" int jo_norm_scale_shift_quant_fp8(
     const void* x, int64_t x_stride, void* residual, int64_t res_stride, const void* gate,
     int64_t gate_stride, const void* gamma, const void* beta, const void* scale,
-    int64_t scale_stride, const void* shift, int64_t shift_stride, void* out_q, int64_t q_stride,
-    float* out_s, int64_t M, int64_t N, int dtype, int norm_type, float eps, void* stream) {
+    int64_t scale_stride, const void* shift, int64_t shift_stride, int64_t mod_rows, void* out_q,
+    int64_t q_stride, float* out_s, int64_t M, int64_t N, int dtype, int norm_type, float eps,
+    void* stream) {
   const char* op = "norm_scale_shift_quant_fp8";
   JO_REQUIRE(dtype == JO_DTYPE_BF16 || dtype == JO_DTYPE_F16,
              "%s: input must be bf16 or fp16 (the quantized row is the 16-bit y)", op);
@@ -641,11 +656,12 @@ extern "C" int jo_norm_scale_shift_quant_fp8(
                  gate_stride >= 0 && (residual == nullptr || res_stride >= N),
              "%s: bad row stride", op);
   JO_REQUIRE(residual != nullptr || gate == nullptr, "%s: a gate needs a residual", op);
+  JO_REQUIRE(mod_rows >= 1 && mod_rows <= UINT32_MAX, "%s: mod_rows must be positive", op);
   if (M == 0) return JO_OK;
   JO_REQUIRE(x && out_q && out_s && scale && shift, "%s: null pointer", op);
   NormArgs a{x, x_stride, residual, res_stride, gate, gate_stride, gamma, beta, scale,
              scale_stride, shift, shift_stride, nullptr, 0, M, static_cast<int>(N), eps,
-             static_cast<uint8_t*>(out_q), q_stride, out_s};
+             static_cast<uint8_t*>(out_q), q_stride, out_s, static_cast<uint32_t>(mod_rows)};
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (residual) {
     if (norm_type == JO_NORM_LAYER) return launch_norm_mod_quant_dt<kLayer, true>(dtype, a, st, op);

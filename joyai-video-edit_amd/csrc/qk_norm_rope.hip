@@ -31,6 +31,8 @@ struct QKArgs {
   const void* k;
   void* kout;  // == k for the in-place modes
   int64_t q_bs, q_ts, k_bs, k_ts, o_bs, o_ts;
+  void* kstage;  // STAGE: the pre-RoPE normalized k, [batch, seq_len, H*D] rows
+  int64_t s_bs, s_ts;
   int64_t tokens;  // batch * seq_len
   int seq_len;
   int row_elems;  // num_heads * head_dim
@@ -115,7 +117,19 @@ __device__ __forceinline__ void grid_pair_cs(float pos, float f, float source_id
 // small parameter loads (rotation table or frequencies, weights) go out
 // first, then the row loads, and only then is anything waited on — the
 // sincos then overlaps the row loads instead of delaying their issue.
-template <int HD, int G, int MODE, int SPLIT>
+// The pre-RoPE K row of rmsnorm_qk_bf16 (rmsnorm.cu:53-60 as the rmsnorm op
+// evaluates it: ms = ss / D and r = 1 / sqrt(ms + eps) as separate IEEE
+// operations, then (x * r) * w): the same per-lane sum and DPP reduction as
+// the QK normalization, so the row is bit-identical to that op's.
+__device__ __forceinline__ float kernel_rms_rstd(float ss, float n, float eps) {
+#pragma clang fp contract(off)
+  const float ms = ss / n;
+  return 1.0f / sqrtf(ms + eps);
+}
+
+// STAGE: k waves also write the pre-RoPE normalized k to a.kstage, so that a
+// forward that caches K before RoPE (dit.py:360-370) reads K once.
+template <int HD, int G, int MODE, int SPLIT, bool STAGE = false>
 __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
   constexpr int LPH = HD / 8;      // lanes per head
   constexpr int P = HD / 2;        // rotation pairs per head
@@ -166,6 +180,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
   char* qrow = static_cast<char*>(a.q) + (b * a.q_bs + n * a.q_ts) * 2;
   const char* krow = static_cast<const char*>(a.k) + (b * a.k_bs + n * a.k_ts) * 2;
   char* kdst = static_cast<char*>(a.kout) + (b * a.o_bs + kdst_tok * a.o_ts) * 2;
+  char* kstg = STAGE ? static_cast<char*>(a.kstage) + (b * a.s_bs + n * a.s_ts) * 2 : nullptr;
   const char* src[NS];
   char* dst[NS];
   const char* wsrc[NS];
@@ -275,6 +290,16 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
         for (int j = 0; j < 8; ++j) ss += xv[j] * xv[j];
         ss = allreduce<LPH, OpSum>(ss);
         const float r = rsqrtf(ss * (1.0f / HD) + a.eps);
+        if constexpr (STAGE) {
+          const bool on_k = NS == 2 ? t == 1 : (part & 1) != 0;  // wave-uniform
+          if (on_k && (g0 + g) < groups && e < a.row_elems) {
+            const float rs = kernel_rms_rstd(ss, static_cast<float>(HD), a.eps);
+            float so[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) so[j] = (xv[j] * rs) * elem<BF16>(wv[t], j);
+            st16_nt(kstg + e * 2, pack<BF16>(so));
+          }
+        }
         float o[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -315,7 +340,7 @@ int qk_split(int64_t tokens, int all_groups) {
   return (tokens < 8192 && all_groups >= 8 && all_groups % 4 == 0) ? 8 : 4;
 }
 
-template <int MODE>
+template <int MODE, bool STAGE = false>
 int launch_qk(const QKArgs& a, int head_dim, hipStream_t stream, const char* op) {
   const int all_groups = (a.row_elems + 511) / 512;
   const int split = qk_split(a.tokens, all_groups);
@@ -326,17 +351,17 @@ int launch_qk(const QKArgs& a, int head_dim, hipStream_t stream, const char* op)
     constexpr int HD = decltype(hd)::value;
     constexpr int S = decltype(sp)::value;
     if (groups <= 1)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 1, MODE, S>), grid, dim3(kBlock), 0, stream, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 1, MODE, S, STAGE>), grid, dim3(kBlock), 0, stream, a);
     else if (groups <= 2)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 2, MODE, S>), grid, dim3(kBlock), 0, stream, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 2, MODE, S, STAGE>), grid, dim3(kBlock), 0, stream, a);
     else if (groups <= 3)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 3, MODE, S>), grid, dim3(kBlock), 0, stream, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 3, MODE, S, STAGE>), grid, dim3(kBlock), 0, stream, a);
     else if (groups <= 4)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 4, MODE, S>), grid, dim3(kBlock), 0, stream, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 4, MODE, S, STAGE>), grid, dim3(kBlock), 0, stream, a);
     else if (groups <= 6)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 6, MODE, S>), grid, dim3(kBlock), 0, stream, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 6, MODE, S, STAGE>), grid, dim3(kBlock), 0, stream, a);
     else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 8, MODE, S>), grid, dim3(kBlock), 0, stream, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<HD, 8, MODE, S, STAGE>), grid, dim3(kBlock), 0, stream, a);
   };
   auto go_hd = [&](auto hd) {
     if (split == 8)
@@ -401,6 +426,77 @@ int check_grid(const char* op, int64_t seq_len, int64_t head_dim, const float* f
 
 using namespace jo;
 
+namespace jo {
+namespace {
+
+// The pre-RoPE K stage of the *_kstage entry points: [batch, seq_len, H*D]
+// rows with the given strides (elements), 16-byte aligned.
+int check_stage(const char* op, const void* k_stage, int64_t s_bs, int64_t s_ts,
+                int64_t num_heads, int64_t head_dim) {
+  JO_REQUIRE(s_ts >= num_heads * head_dim && s_bs >= 0 && s_ts % 8 == 0 && s_bs % 8 == 0,
+             "%s: bad k_stage strides", op);
+  JO_REQUIRE(k_stage && aligned(k_stage, 16), "%s: k_stage must be a 16-byte aligned pointer",
+             op);
+  return JO_OK;
+}
+
+int qk_paired(const char* op, void* q, void* k, void* k_stage, int64_t batch, int64_t seq_len,
+              int64_t num_heads, int64_t head_dim, int64_t q_bs, int64_t q_ts, int64_t k_bs,
+              int64_t k_ts, int64_t s_bs, int64_t s_ts, float eps, const void* q_weight,
+              const void* k_weight, const void* cos, const void* sin, void* stream,
+              bool stage) {
+  int st = check_qk(op, q, k, batch, seq_len, num_heads, head_dim, q_bs, q_ts, k_bs, k_ts,
+                    q_weight, k_weight);
+  if (st != JO_OK || batch * seq_len == 0) return st;
+  JO_REQUIRE(cos && sin, "%s: null cos/sin", op);
+  JO_REQUIRE(aligned(cos, 8) && aligned(sin, 8), "%s: cos/sin must be 8-byte aligned", op);
+  if (stage && (st = check_stage(op, k_stage, s_bs, s_ts, num_heads, head_dim)) != JO_OK)
+    return st;
+  QKArgs a{};
+  a.q = q; a.k = k; a.kout = k;
+  a.q_bs = q_bs; a.q_ts = q_ts;
+  a.k_bs = a.o_bs = k_bs; a.k_ts = a.o_ts = k_ts;
+  a.kstage = k_stage; a.s_bs = s_bs; a.s_ts = s_ts;
+  a.tokens = batch * seq_len; a.seq_len = static_cast<int>(seq_len);
+  a.row_elems = static_cast<int>(num_heads * head_dim); a.eps = eps;
+  a.qw = q_weight; a.kw = k_weight; a.cos = cos; a.sin = sin;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  return stage ? launch_qk<kTable, true>(a, static_cast<int>(head_dim), hs, op)
+               : launch_qk<kTable>(a, static_cast<int>(head_dim), hs, op);
+}
+
+int qk_grid(const char* op, void* q, void* k, void* k_stage, int64_t batch, int64_t seq_len,
+            int64_t num_heads, int64_t head_dim, int64_t q_bs, int64_t q_ts, int64_t k_bs,
+            int64_t k_ts, int64_t s_bs, int64_t s_ts, float eps, const void* q_weight,
+            const void* k_weight, const float* freqs, int32_t pairs_t, int32_t pairs_h,
+            int32_t grid_h, int32_t grid_w, int32_t t0, float source_id, void* stream,
+            bool stage) {
+  int st = check_qk(op, q, k, batch, seq_len, num_heads, head_dim, q_bs, q_ts, k_bs, k_ts,
+                    q_weight, k_weight);
+  if (st != JO_OK) return st;
+  st = check_grid(op, seq_len, head_dim, freqs, pairs_t, pairs_h, grid_h, grid_w);
+  if (st != JO_OK || batch * seq_len == 0) return st;
+  if (stage && (st = check_stage(op, k_stage, s_bs, s_ts, num_heads, head_dim)) != JO_OK)
+    return st;
+  QKArgs a{};
+  a.q = q; a.k = k; a.kout = k;
+  a.q_bs = q_bs; a.q_ts = q_ts;
+  a.k_bs = a.o_bs = k_bs; a.k_ts = a.o_ts = k_ts;
+  a.kstage = k_stage; a.s_bs = s_bs; a.s_ts = s_ts;
+  a.tokens = batch * seq_len; a.seq_len = static_cast<int>(seq_len);
+  a.row_elems = static_cast<int>(num_heads * head_dim); a.eps = eps;
+  a.qw = q_weight; a.kw = k_weight;
+  memcpy(a.freqs, freqs, sizeof(float) * head_dim);
+  a.pairs_t = pairs_t; a.pairs_h = pairs_h;
+  a.grid_h = grid_h; a.grid_w = grid_w; a.t0 = t0; a.source_id = source_id;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  return stage ? launch_qk<kGrid, true>(a, static_cast<int>(head_dim), hs, op)
+               : launch_qk<kGrid>(a, static_cast<int>(head_dim), hs, op);
+}
+
+}  // namespace
+}  // namespace jo
+
 extern "C" int jo_fused_qk_norm_rope_3d_paired(void* q, void* k, int64_t batch, int64_t seq_len,
                                                int64_t num_heads, int64_t head_dim,
                                                int64_t q_batch_stride, int64_t q_token_stride,
@@ -408,20 +504,20 @@ extern "C" int jo_fused_qk_norm_rope_3d_paired(void* q, void* k, int64_t batch, 
                                                float eps, const void* q_weight,
                                                const void* k_weight, const void* cos,
                                                const void* sin, void* stream) {
-  const char* op = "fused_qk_norm_rope_3d_paired";
-  int st = check_qk(op, q, k, batch, seq_len, num_heads, head_dim, q_batch_stride,
-                    q_token_stride, k_batch_stride, k_token_stride, q_weight, k_weight);
-  if (st != JO_OK || batch * seq_len == 0) return st;
-  JO_REQUIRE(cos && sin, "%s: null cos/sin", op);
-  JO_REQUIRE(aligned(cos, 8) && aligned(sin, 8), "%s: cos/sin must be 8-byte aligned", op);
-  QKArgs a{};
-  a.q = q; a.k = k; a.kout = k;
-  a.q_bs = q_batch_stride; a.q_ts = q_token_stride;
-  a.k_bs = a.o_bs = k_batch_stride; a.k_ts = a.o_ts = k_token_stride;
-  a.tokens = batch * seq_len; a.seq_len = static_cast<int>(seq_len);
-  a.row_elems = static_cast<int>(num_heads * head_dim); a.eps = eps;
-  a.qw = q_weight; a.kw = k_weight; a.cos = cos; a.sin = sin;
-  return launch_qk<kTable>(a, static_cast<int>(head_dim), static_cast<hipStream_t>(stream), op);
+  return qk_paired("fused_qk_norm_rope_3d_paired", q, k, nullptr, batch, seq_len, num_heads,
+                   head_dim, q_batch_stride, q_token_stride, k_batch_stride, k_token_stride, 0, 0,
+                   eps, q_weight, k_weight, cos, sin, stream, false);
+}
+
+extern "C" int jo_fused_qk_norm_rope_3d_paired_kstage(
+    void* q, void* k, void* k_stage, int64_t batch, int64_t seq_len, int64_t num_heads,
+    int64_t head_dim, int64_t q_batch_stride, int64_t q_token_stride, int64_t k_batch_stride,
+    int64_t k_token_stride, int64_t stage_batch_stride, int64_t stage_token_stride, float eps,
+    const void* q_weight, const void* k_weight, const void* cos, const void* sin, void* stream) {
+  return qk_paired("fused_qk_norm_rope_3d_paired_kstage", q, k, k_stage, batch, seq_len,
+                   num_heads, head_dim, q_batch_stride, q_token_stride, k_batch_stride,
+                   k_token_stride, stage_batch_stride, stage_token_stride, eps, q_weight,
+                   k_weight, cos, sin, stream, true);
 }
 
 extern "C" int jo_fused_qk_norm_rope_3d_grid(void* q, void* k, int64_t batch, int64_t seq_len,
@@ -433,23 +529,22 @@ extern "C" int jo_fused_qk_norm_rope_3d_grid(void* q, void* k, int64_t batch, in
                                              int32_t pairs_t, int32_t pairs_h, int32_t grid_h,
                                              int32_t grid_w, int32_t t0, float source_id,
                                              void* stream) {
-  const char* op = "fused_qk_norm_rope_3d_grid";
-  int st = check_qk(op, q, k, batch, seq_len, num_heads, head_dim, q_batch_stride,
-                    q_token_stride, k_batch_stride, k_token_stride, q_weight, k_weight);
-  if (st != JO_OK) return st;
-  st = check_grid(op, seq_len, head_dim, freqs, pairs_t, pairs_h, grid_h, grid_w);
-  if (st != JO_OK || batch * seq_len == 0) return st;
-  QKArgs a{};
-  a.q = q; a.k = k; a.kout = k;
-  a.q_bs = q_batch_stride; a.q_ts = q_token_stride;
-  a.k_bs = a.o_bs = k_batch_stride; a.k_ts = a.o_ts = k_token_stride;
-  a.tokens = batch * seq_len; a.seq_len = static_cast<int>(seq_len);
-  a.row_elems = static_cast<int>(num_heads * head_dim); a.eps = eps;
-  a.qw = q_weight; a.kw = k_weight;
-  memcpy(a.freqs, freqs, sizeof(float) * head_dim);
-  a.pairs_t = pairs_t; a.pairs_h = pairs_h;
-  a.grid_h = grid_h; a.grid_w = grid_w; a.t0 = t0; a.source_id = source_id;
-  return launch_qk<kGrid>(a, static_cast<int>(head_dim), static_cast<hipStream_t>(stream), op);
+  return qk_grid("fused_qk_norm_rope_3d_grid", q, k, nullptr, batch, seq_len, num_heads,
+                 head_dim, q_batch_stride, q_token_stride, k_batch_stride, k_token_stride, 0, 0,
+                 eps, q_weight, k_weight, freqs, pairs_t, pairs_h, grid_h, grid_w, t0, source_id,
+                 stream, false);
+}
+
+extern "C" int jo_fused_qk_norm_rope_3d_grid_kstage(
+    void* q, void* k, void* k_stage, int64_t batch, int64_t seq_len, int64_t num_heads,
+    int64_t head_dim, int64_t q_batch_stride, int64_t q_token_stride, int64_t k_batch_stride,
+    int64_t k_token_stride, int64_t stage_batch_stride, int64_t stage_token_stride, float eps,
+    const void* q_weight, const void* k_weight, const float* freqs, int32_t pairs_t,
+    int32_t pairs_h, int32_t grid_h, int32_t grid_w, int32_t t0, float source_id, void* stream) {
+  return qk_grid("fused_qk_norm_rope_3d_grid_kstage", q, k, k_stage, batch, seq_len, num_heads,
+                 head_dim, q_batch_stride, q_token_stride, k_batch_stride, k_token_stride,
+                 stage_batch_stride, stage_token_stride, eps, q_weight, k_weight, freqs, pairs_t,
+                 pairs_h, grid_h, grid_w, t0, source_id, stream, true);
 }
 
 extern "C" int jo_fused_qk_norm_rope_3d_kvcache(

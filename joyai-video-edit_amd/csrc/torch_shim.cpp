@@ -5,10 +5,11 @@
 // (fused_qknorm_rope_3d_kernel.cu:183-200, fused_norm_scale_shift.cu:176-196,
 // rmsnorm.cu:77-81, per_token_quant_fp8.cu:149-156, fp8_gemm.cu:1457-1485), so
 // torch.ops.joyomni_ops.* behaves as the reference does for callers. The new
-// ops (grid RoPE, K ring-cache write, add+LayerNorm, RMSNorm->FP8,
-// norm+AdaLN->FP8, KV-pool commit, apply_rotary_emb, per-head RMSNorm) have their own names. Tensors on ROCm carry the CUDA
-// device type, so the impls are
-// registered on the CUDA dispatch key like the reference's. Every op runs
+// ops (grid RoPE, K ring-cache write, QK with the pre-RoPE K stage,
+// add+LayerNorm, RMSNorm->FP8, norm+AdaLN->FP8, KV-pool commit,
+// apply_rotary_emb, per-head RMSNorm) have their own names. Tensors on ROCm
+// carry the CUDA device type, so the impls are registered on the CUDA
+// dispatch key like the reference's. Every op runs
 // on the current stream of the tensor's device and never synchronizes.
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
@@ -258,9 +259,9 @@ void qk_strides(const torch::Tensor& t, int64_t seq_len, int64_t num_heads, int6
   }
 }
 
-QKGeom check_qk_common(const torch::Tensor& q, const torch::Tensor& k, int64_t seq_len,
-                       int64_t num_heads, const torch::Tensor& q_weight,
-                       const torch::Tensor& k_weight, const torch::Tensor& freqs) {
+QKGeom check_qk_views(const torch::Tensor& q, const torch::Tensor& k, int64_t seq_len,
+                      int64_t num_heads, const torch::Tensor& q_weight,
+                      const torch::Tensor& k_weight) {
   TORCH_CHECK(q.dim() == 3 || q.dim() == 4, "q must be 3D or 4D");
   TORCH_CHECK(q.sizes() == k.sizes(), "q and k must have the same shape");
   JO_CHECK_CUDA(q);
@@ -269,20 +270,40 @@ QKGeom check_qk_common(const torch::Tensor& q, const torch::Tensor& k, int64_t s
   JO_CHECK_DTYPE(k, torch::kBFloat16);
   JO_CHECK_INPUT(q_weight, torch::kBFloat16);
   JO_CHECK_INPUT(k_weight, torch::kBFloat16);
-  TORCH_CHECK(freqs.device().is_cpu(),
-              "freqs must be a CPU tensor (its values are passed in the kernel arguments)");
-  JO_CHECK_CONTIGUOUS(freqs);
-  JO_CHECK_DTYPE(freqs, torch::kFloat32);
   const int64_t head_dim = q.size(q.dim() - 1);
   TORCH_CHECK(q_weight.numel() == head_dim && k_weight.numel() == head_dim,
               "weight size must match head_dim");
-  TORCH_CHECK(freqs.dim() == 2 && freqs.size(0) == 2 && freqs.size(1) == head_dim / 2,
-              "freqs must be [2, head_dim/2] float32");
   TORCH_CHECK(head_dim == 64 || head_dim == 128 || head_dim == 256,
               "Unsupported head_dim: ", head_dim);
   QKGeom g{q.size(0), seq_len, num_heads, head_dim, 0, 0, 0, 0};
   qk_strides(q, seq_len, num_heads, head_dim, "q", &g.q_bs, &g.q_ts);
   qk_strides(k, seq_len, num_heads, head_dim, "k", &g.k_bs, &g.k_ts);
+  return g;
+}
+
+// The pre-RoPE K output of the *_kstage ops: [B, seq_len*H, D] contiguous or
+// a [B, seq_len, H, D] view with contiguous heads; returns its strides.
+std::pair<int64_t, int64_t> stage_strides(const torch::Tensor& k_stage, const QKGeom& g) {
+  JO_CHECK_CUDA(k_stage);
+  JO_CHECK_DTYPE(k_stage, torch::kBFloat16);
+  TORCH_CHECK(k_stage.dim() >= 3 && k_stage.size(0) == g.batch &&
+                  k_stage.size(k_stage.dim() - 1) == g.head_dim,
+              "k_stage must be [B, seq_len*num_heads, D] or [B, seq_len, num_heads, D]");
+  int64_t bs = 0, ts = 0;
+  qk_strides(k_stage, g.seq_len, g.num_heads, g.head_dim, "k_stage", &bs, &ts);
+  return {bs, ts};
+}
+
+QKGeom check_qk_common(const torch::Tensor& q, const torch::Tensor& k, int64_t seq_len,
+                       int64_t num_heads, const torch::Tensor& q_weight,
+                       const torch::Tensor& k_weight, const torch::Tensor& freqs) {
+  const QKGeom g = check_qk_views(q, k, seq_len, num_heads, q_weight, k_weight);
+  TORCH_CHECK(freqs.device().is_cpu(),
+              "freqs must be a CPU tensor (its values are passed in the kernel arguments)");
+  JO_CHECK_CONTIGUOUS(freqs);
+  JO_CHECK_DTYPE(freqs, torch::kFloat32);
+  TORCH_CHECK(freqs.dim() == 2 && freqs.size(0) == 2 && freqs.size(1) == g.head_dim / 2,
+              "freqs must be [2, head_dim/2] float32");
   return g;
 }
 
@@ -303,6 +324,48 @@ void fused_qk_norm_rope_3d_grid(torch::Tensor& q, torch::Tensor& k, int64_t seq_
                    static_cast<int32_t>(grid_h), static_cast<int32_t>(grid_w),
                    static_cast<int32_t>(t0), static_cast<float>(source_id), current_stream(q)),
                "fused_qk_norm_rope_3d_grid");
+}
+
+void fused_qk_norm_rope_3d_grid_kstage(torch::Tensor& q, torch::Tensor& k, torch::Tensor& k_stage,
+                                       int64_t seq_len, int64_t num_heads, double eps,
+                                       torch::Tensor& q_weight, torch::Tensor& k_weight,
+                                       torch::Tensor& freqs, int64_t pairs_t, int64_t pairs_h,
+                                       int64_t grid_h, int64_t grid_w, int64_t t0,
+                                       double source_id) {
+  const QKGeom g = check_qk_common(q, k, seq_len, num_heads, q_weight, k_weight, freqs);
+  const auto st = stage_strides(k_stage, g);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(q.device());
+  check_status(jo_fused_qk_norm_rope_3d_grid_kstage(
+                   q.data_ptr(), k.data_ptr(), k_stage.data_ptr(), g.batch, g.seq_len,
+                   g.num_heads, g.head_dim, g.q_bs, g.q_ts, g.k_bs, g.k_ts, st.first, st.second,
+                   static_cast<float>(eps), q_weight.data_ptr(), k_weight.data_ptr(),
+                   freqs.data_ptr<float>(), static_cast<int32_t>(pairs_t),
+                   static_cast<int32_t>(pairs_h), static_cast<int32_t>(grid_h),
+                   static_cast<int32_t>(grid_w), static_cast<int32_t>(t0),
+                   static_cast<float>(source_id), current_stream(q)),
+               "fused_qk_norm_rope_3d_grid_kstage");
+}
+
+void fused_qk_norm_rope_3d_paired_kstage(torch::Tensor& q, torch::Tensor& k,
+                                         torch::Tensor& k_stage, int64_t seq_len,
+                                         int64_t num_heads, double eps, torch::Tensor& q_weight,
+                                         torch::Tensor& k_weight, torch::Tensor& cos,
+                                         torch::Tensor& sin) {
+  const QKGeom g = check_qk_views(q, k, seq_len, num_heads, q_weight, k_weight);
+  JO_CHECK_INPUT(cos, torch::kBFloat16);
+  JO_CHECK_INPUT(sin, torch::kBFloat16);
+  TORCH_CHECK(cos.dim() == 2 && sin.dim() == 2 && cos.size(0) == seq_len &&
+                  sin.size(0) == seq_len && cos.size(1) == g.head_dim / 2 &&
+                  sin.size(1) == g.head_dim / 2,
+              "cos/sin must be [seq_len, head_dim/2]");
+  const auto st = stage_strides(k_stage, g);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(q.device());
+  check_status(jo_fused_qk_norm_rope_3d_paired_kstage(
+                   q.data_ptr(), k.data_ptr(), k_stage.data_ptr(), g.batch, g.seq_len,
+                   g.num_heads, g.head_dim, g.q_bs, g.q_ts, g.k_bs, g.k_ts, st.first, st.second,
+                   static_cast<float>(eps), q_weight.data_ptr(), k_weight.data_ptr(),
+                   cos.data_ptr(), sin.data_ptr(), current_stream(q)),
+               "fused_qk_norm_rope_3d_paired_kstage");
 }
 
 void fused_qk_norm_rope_3d_kvcache(torch::Tensor& q, const torch::Tensor& k,
@@ -336,15 +399,26 @@ void fused_qk_norm_rope_3d_kvcache(torch::Tensor& q, const torch::Tensor& k,
 }
 
 namespace {
-// Row stride of an [N] vector or an [M, N] per-row tensor: 0 broadcasts.
-int64_t mod_stride(const torch::Tensor& t, int64_t M, int64_t N, const char* name) {
+// A modulation tensor (gate, scale, shift) of the fused norm ops: [N] (one
+// row for every row of x: stride 0), [M, N] (a row each) or [B, N] with B
+// dividing M (one row per sample of M / B consecutive rows). Returns its row
+// stride and records how many rows of x each of its rows serves in *group
+// (every modulation tensor with its own rows must agree).
+int64_t mod_stride(const torch::Tensor& t, int64_t M, int64_t N, const char* name,
+                   int64_t* group) {
   JO_CHECK_CUDA(t);
-  if (t.dim() == 1) {
-    TORCH_CHECK(t.size(0) == N && t.stride(0) == 1, name, " must be [N] contiguous");
+  if (t.dim() == 1 || (t.dim() == 2 && t.size(0) == 1)) {
+    TORCH_CHECK(t.size(t.dim() - 1) == N && t.stride(t.dim() - 1) == 1, name,
+                " must be [N] contiguous");
     return 0;
   }
-  TORCH_CHECK(t.dim() == 2 && t.size(0) == M && t.size(1) == N && t.stride(1) == 1, name,
-              " must be [N] or [M, N] with a contiguous last dim");
+  TORCH_CHECK(t.dim() == 2 && t.size(1) == N && t.stride(1) == 1 &&
+                  (t.size(0) == M || (t.size(0) > 0 && M % t.size(0) == 0)),
+              name, " must be [N], [M, N] or [B, N] (B dividing M) with a contiguous last dim");
+  const int64_t g = t.size(0) == M ? 1 : M / t.size(0);
+  TORCH_CHECK(*group == 0 || *group == g, name,
+              ": gate / scale / shift with rows of their own must have the same row count");
+  *group = g;
   return row_stride(t);
 }
 }  // namespace
@@ -365,13 +439,14 @@ torch::Tensor fused_add_layernorm_scale_shift(const torch::Tensor& x, torch::Ten
   TORCH_CHECK(residual.dtype() == x.dtype() && scale.dtype() == x.dtype() &&
                   shift.dtype() == x.dtype(),
               "x/residual/scale/shift dtype must match");
-  const int64_t sc_stride = mod_stride(scale, M, N, "scale");
-  const int64_t sh_stride = mod_stride(shift, M, N, "shift");
+  int64_t group = 0;
+  const int64_t sc_stride = mod_stride(scale, M, N, "scale", &group);
+  const int64_t sh_stride = mod_stride(shift, M, N, "shift", &group);
   const bool has_gate = gate_opt.has_value() && gate_opt->defined();
   int64_t g_stride = 0;
   if (has_gate) {
     TORCH_CHECK(gate_opt->dtype() == x.dtype(), "gate dtype must match x");
-    g_stride = mod_stride(*gate_opt, M, N, "gate");
+    g_stride = mod_stride(*gate_opt, M, N, "gate", &group);
   }
   const bool has_gamma = gamma_opt.has_value() && gamma_opt->defined();
   const bool has_beta = beta_opt.has_value() && beta_opt->defined();
@@ -392,7 +467,7 @@ torch::Tensor fused_add_layernorm_scale_shift(const torch::Tensor& x, torch::Ten
                    has_gate ? gate_opt->data_ptr() : nullptr, g_stride,
                    has_gamma ? gamma_opt->data_ptr() : nullptr,
                    has_beta ? beta_opt->data_ptr() : nullptr, scale.data_ptr(), sc_stride,
-                   shift.data_ptr(), sh_stride, y.data_ptr(), N, M, N, dt,
+                   shift.data_ptr(), sh_stride, group > 0 ? group : 1, y.data_ptr(), N, M, N, dt,
                    static_cast<float>(eps), current_stream(x)),
                "fused_add_layernorm_scale_shift");
   return y;
@@ -446,8 +521,9 @@ void norm_scale_shift_quant_fp8(const torch::Tensor& x,
   TORCH_CHECK(N % 4 == 0, "N must be divisible by 4");
   TORCH_CHECK(scale.dtype() == x.dtype() && shift.dtype() == x.dtype(),
               "x/scale/shift dtype must match");
-  const int64_t sc_stride = mod_stride(scale, M, N, "scale");
-  const int64_t sh_stride = mod_stride(shift, M, N, "shift");
+  int64_t group = 0;
+  const int64_t sc_stride = mod_stride(scale, M, N, "scale", &group);
+  const int64_t sh_stride = mod_stride(shift, M, N, "shift", &group);
   const bool has_res = residual_opt.has_value() && residual_opt->defined();
   if (has_res) {
     JO_CHECK_CUDA(*residual_opt);
@@ -460,7 +536,7 @@ void norm_scale_shift_quant_fp8(const torch::Tensor& x,
   int64_t g_stride = 0;
   if (has_gate) {
     TORCH_CHECK(gate_opt->dtype() == x.dtype(), "gate dtype must match x");
-    g_stride = mod_stride(*gate_opt, M, N, "gate");
+    g_stride = mod_stride(*gate_opt, M, N, "gate", &group);
   }
   const bool has_gamma = gamma_opt.has_value() && gamma_opt->defined();
   const bool has_beta = beta_opt.has_value() && beta_opt->defined();
@@ -486,7 +562,7 @@ void norm_scale_shift_quant_fp8(const torch::Tensor& x,
                    has_gate ? gate_opt->data_ptr() : nullptr, g_stride,
                    has_gamma ? gamma_opt->data_ptr() : nullptr,
                    has_beta ? beta_opt->data_ptr() : nullptr, scale.data_ptr(), sc_stride,
-                   shift.data_ptr(), sh_stride, output_q.data_ptr(), N,
+                   shift.data_ptr(), sh_stride, group > 0 ? group : 1, output_q.data_ptr(), N,
                    output_s.data_ptr<float>(), M, N, dtype_code(x),
                    static_cast<int>(norm_type), static_cast<float>(eps), current_stream(x)),
                "norm_scale_shift_quant_fp8");
@@ -645,6 +721,13 @@ TORCH_LIBRARY(joyomni_ops, m) {
       "Tensor q_weight, Tensor k_weight, Tensor freqs, int pairs_t, int pairs_h, int grid_h, "
       "int grid_w, int t0, float source_id) -> ()");
   m.def(
+      "fused_qk_norm_rope_3d_paired_kstage(Tensor! q, Tensor! k, Tensor! k_stage, int seq_len, "
+      "int num_heads, float eps, Tensor q_weight, Tensor k_weight, Tensor cos, Tensor sin) -> ()");
+  m.def(
+      "fused_qk_norm_rope_3d_grid_kstage(Tensor! q, Tensor! k, Tensor! k_stage, int seq_len, "
+      "int num_heads, float eps, Tensor q_weight, Tensor k_weight, Tensor freqs, int pairs_t, "
+      "int pairs_h, int grid_h, int grid_w, int t0, float source_id) -> ()");
+  m.def(
       "fused_qk_norm_rope_3d_kvcache(Tensor! q, Tensor k, Tensor! k_cache, int seq_len, "
       "int num_heads, float eps, Tensor q_weight, Tensor k_weight, Tensor freqs, int pairs_t, "
       "int pairs_h, int grid_h, int grid_w, int t0, float source_id, int slot_start) -> ()");
@@ -673,6 +756,9 @@ TORCH_LIBRARY_IMPL(joyomni_ops, CUDA, m) {
   m.impl("fp8_scaled_mm", &joyomni_ops::fp8_scaled_mm);
   m.impl("fused_qk_norm_rope_3d_grid", &joyomni_ops::fused_qk_norm_rope_3d_grid);
   m.impl("fused_qk_norm_rope_3d_kvcache", &joyomni_ops::fused_qk_norm_rope_3d_kvcache);
+  m.impl("fused_qk_norm_rope_3d_paired_kstage",
+         &joyomni_ops::fused_qk_norm_rope_3d_paired_kstage);
+  m.impl("fused_qk_norm_rope_3d_grid_kstage", &joyomni_ops::fused_qk_norm_rope_3d_grid_kstage);
   m.impl("fused_add_layernorm_scale_shift", &joyomni_ops::fused_add_layernorm_scale_shift);
   m.impl("rmsnorm_quant_fp8", &joyomni_ops::rmsnorm_quant_fp8);
   m.impl("norm_scale_shift_quant_fp8", &joyomni_ops::norm_scale_shift_quant_fp8);

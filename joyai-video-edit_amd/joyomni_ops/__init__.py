@@ -9,7 +9,8 @@ below keep the reference's names, argument order, defaults and the
 for device tensors only, and importing fails if the libraries are missing.
 
 New ops (no reference signature): fused_qk_norm_rope_3d_grid,
-fused_qk_norm_rope_3d_kvcache, fused_add_layernorm_scale_shift,
+fused_qk_norm_rope_3d_kvcache, fused_qk_norm_rope_3d_paired_kstage,
+fused_qk_norm_rope_3d_grid_kstage, fused_add_layernorm_scale_shift,
 rmsnorm_quant_fp8, norm_scale_shift_quant_fp8, kv_commit_rope,
 apply_rotary_emb, rmsnorm_heads, plus rope_freqs() to build the
 [2, head_dim/2] frequency table the grid ops read.
@@ -49,6 +50,8 @@ __all__ = [
     "apply_rotary_emb",
     "norm_scale_shift_quant_fp8",
     "rmsnorm_heads",
+    "fused_qk_norm_rope_3d_paired_kstage",
+    "fused_qk_norm_rope_3d_grid_kstage",
 ]
 
 _ops = torch.ops.joyomni_ops
@@ -148,6 +151,30 @@ def fused_qk_norm_rope_3d_grid(q, k, seq_len, num_heads, eps, q_weight, k_weight
                                     float(source_id))
 
 
+def fused_qk_norm_rope_3d_paired_kstage(q, k, k_stage, seq_len, num_heads, eps, q_weight,
+                                        k_weight, cos, sin):
+    """fused_qk_norm_rope_3d_paired that also writes the pre-RoPE normalized k
+    (rmsnorm_qk_bf16's rows, bit for bit) to k_stage in the same pass.
+
+    q/k: [B, seq_len*num_heads, D] contiguous or [B, seq_len, num_heads, D]
+    views with contiguous heads (e.g. slices of a packed qkv), rotated in
+    place; k_stage: bf16 of the same geometry (any batch / token strides),
+    not overlapping q or k; cos/sin bf16 [seq_len, D/2].
+    """
+    _ops.fused_qk_norm_rope_3d_paired_kstage(q, k, k_stage, seq_len, num_heads, eps, q_weight,
+                                             k_weight, cos, sin)
+
+
+def fused_qk_norm_rope_3d_grid_kstage(q, k, k_stage, seq_len, num_heads, eps, q_weight, k_weight,
+                                      freqs, rope_dims, grid_hw, t0=0, source_id=0.0):
+    """fused_qk_norm_rope_3d_grid that also writes the pre-RoPE normalized k
+    (rmsnorm_qk_bf16's rows, bit for bit) to k_stage in the same pass."""
+    gh, gw = grid_hw
+    _ops.fused_qk_norm_rope_3d_grid_kstage(q, k, k_stage, seq_len, num_heads, eps, q_weight,
+                                           k_weight, freqs, rope_dims[0] // 2, rope_dims[1] // 2,
+                                           gh, gw, t0, float(source_id))
+
+
 def kv_ring_slot(t0: int, frames_per_chunk: int, cache_slots: int) -> int:
     """First ring slot of a chunk starting at temporal position t0: (t0 / frames) mod slots."""
     return (t0 // frames_per_chunk) % cache_slots
@@ -171,7 +198,8 @@ def fused_add_layernorm_scale_shift(x, residual, scale, shift, gate=None, gamma=
     """residual <- residual + x (* gate); returns LayerNorm(residual) * (1 + scale) + shift.
 
     x, residual: [M, N]; residual is updated in place. scale/shift/gate:
-    [N] (broadcast) or [M, N].
+    [N] (broadcast), [M, N] (a row each) or [B, N] with B dividing M (one row
+    per sample of M / B consecutive rows, the DiT's per-sample AdaLN vectors).
     """
     return _ops.fused_add_layernorm_scale_shift(x, residual, gate, gamma, beta, scale, shift, eps)
 
@@ -187,7 +215,9 @@ def norm_scale_shift_quant_fp8(x, scale, shift, output_q, output_s, residual=Non
     fused_norm_scale_shift (residual None) or fused_add_layernorm_scale_shift
     (residual given, updated in place with residual + x (* gate)) would return;
     y itself is never written. output_q: float8_e4m3fn [M, N]; output_s:
-    float32 [M] or [M, 1]. norm_type "layer" or "rms".
+    float32 [M] or [M, 1]. scale/shift/gate: [N], [M, N] or [B, N] (B
+    dividing M), as for fused_add_layernorm_scale_shift. norm_type "layer"
+    or "rms".
     """
     nt = 0 if norm_type == "layer" else 1 if norm_type == "rms" else -1
     _ops.norm_scale_shift_quant_fp8(x, residual, gate, gamma, beta, scale, shift, nt, eps,

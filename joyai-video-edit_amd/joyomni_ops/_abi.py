@@ -43,6 +43,12 @@ SIGNATURES: dict[str, list] = {
     "jo_fused_qk_norm_rope_3d_grid": [
         _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P,
         c_int32, c_int32, c_int32, c_int32, c_int32, _F, _P],
+    "jo_fused_qk_norm_rope_3d_paired_kstage": [
+        _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P,
+        _P, _P],
+    "jo_fused_qk_norm_rope_3d_grid_kstage": [
+        _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P,
+        c_int32, c_int32, c_int32, c_int32, c_int32, _F, _P],
     "jo_fused_qk_norm_rope_3d_kvcache": [
         _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
         _F, _P, _P, _P, c_int32, c_int32, c_int32, c_int32, c_int32, _F, _P],
@@ -51,11 +57,11 @@ SIGNATURES: dict[str, list] = {
     "jo_rmsnorm": [_P, _I64, _P, _P, _I64, _I64, _I64, c_int, _F, _P],
     "jo_rmsnorm_heads": [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, c_int, _F, c_int, _P],
     "jo_fused_add_layernorm_scale_shift": [
-        _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, c_int,
-        _F, _P],
+        _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64,
+        c_int, _F, _P],
     "jo_rmsnorm_quant_fp8": [_P, _I64, _P, _P, _I64, _P, _I64, _I64, c_int, _F, _I64, _P],
     "jo_norm_scale_shift_quant_fp8": [
-        _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64,
+        _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _I64,
         c_int, c_int, _F, _P],
     "jo_fp8_scaled_mm": [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, c_int, _P],
     "jo_kv_commit_rope": [

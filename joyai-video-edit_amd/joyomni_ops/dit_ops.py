@@ -18,6 +18,10 @@ Additional entry points for callers that can use the new fused ops:
   fused_qk_norm_rope_3d_grid_views  RMSNorm + RoPE in place on q/k views of the
                             packed qkv [B, L, 3, H, D] with angles computed from
                             grid positions (no tables, no .contiguous() copies).
+  fused_qk_norm_rope_3d_kstage  the pre-RoPE K-cache path of dit.py:360-370
+                            (rmsnorm_qk_bf16 of K, then fused_qk_norm_rope_3d) in one
+                            pass that reads K once; q / k rotated in place on their
+                            packed-qkv views (no .contiguous() copies).
   fused_add_gate_layernorm_modulate residual + x * gate and the following
                             fused_layernorm_modulate in one pass (dit.py:447-457).
   quantize_activation_fp8   x_q, x_scale of Fp8Linear.forward (fp8_linear.py:140-166).
@@ -40,7 +44,8 @@ from typing import Optional, Sequence, Tuple
 import torch
 
 from . import (fp8_scaled_mm, fused_add_layernorm_scale_shift, fused_norm_scale_shift,
-               fused_qk_norm_rope_3d_grid, fused_qk_norm_rope_3d_paired,
+               fused_qk_norm_rope_3d_grid, fused_qk_norm_rope_3d_grid_kstage,
+               fused_qk_norm_rope_3d_paired, fused_qk_norm_rope_3d_paired_kstage,
                kv_commit_rope, norm_scale_shift_quant_fp8, rmsnorm, rmsnorm_heads,
                rope_freqs, sgl_per_token_quant_fp8)
 
@@ -103,9 +108,19 @@ def fused_qk_norm_rope_3d(
     k = k.contiguous()
     q_r = q.view(B, L * H, D)
     k_r = k.view(B, L * H, D)
+    cos_bf16, sin_bf16 = _half_tables_bf16(freqs_cis, L, D, q.device)
+    qw = q_norm_weight.to(torch.bfloat16)
+    kw = k_norm_weight.to(torch.bfloat16)
+    fused_qk_norm_rope_3d_paired(q_r, k_r, L, H, eps, qw, kw, cos_bf16, sin_bf16)
+    return q, k
+
+
+def _half_tables_bf16(freqs_cis, L: int, D: int, device):
+    """cos/sin as the paired op takes them: [L, D/2] bf16, from [1, L, D] or
+    [L, D/2] tables, squeezed, halved and cast as sgl_fused_ops.py:80-94 does."""
     cos, sin = freqs_cis
-    cos = cos.to(q.device)
-    sin = sin.to(q.device)
+    cos = cos.to(device)
+    sin = sin.to(device)
     while cos.dim() > 2:
         if cos.shape[0] != 1:
             raise RuntimeError(f"freqs_cis cos has non-singleton leading dim: {cos.shape}")
@@ -114,12 +129,42 @@ def fused_qk_norm_rope_3d(
     if cos.shape[-1] == D:
         cos = cos[..., ::2]
         sin = sin[..., ::2]
-    cos_bf16 = cos.contiguous().to(torch.bfloat16)
-    sin_bf16 = sin.contiguous().to(torch.bfloat16)
-    qw = q_norm_weight.to(torch.bfloat16)
-    kw = k_norm_weight.to(torch.bfloat16)
-    fused_qk_norm_rope_3d_paired(q_r, k_r, L, H, eps, qw, kw, cos_bf16, sin_bf16)
-    return q, k
+    return cos.contiguous().to(torch.bfloat16), sin.contiguous().to(torch.bfloat16)
+
+
+def fused_qk_norm_rope_3d_kstage(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    q_norm_weight: torch.Tensor,
+    k_norm_weight: torch.Tensor,
+    freqs_cis: Tuple[torch.Tensor, torch.Tensor],
+    *,
+    eps: float = 1e-6,
+    k_stage: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The K-cache-before-RoPE branch of MMDoubleStreamBlock.forward
+    (dit.py:360-370): k_for_cache = rmsnorm_qk_bf16(k, k_norm_weight) and
+    q, k = fused_qk_norm_rope_3d(q, k, ...), in one pass that reads K once.
+
+    q, k: bf16 [B, L, H, D], typically the q / k slices of the packed qkv
+    [B, L, 3, H, D] (heads contiguous per token); they are normalized and
+    rotated IN PLACE and returned (the reference returns rotated contiguous
+    copies and leaves the qkv slices as they were; the DiT forward reads only
+    the returned q, k and the v slice afterwards). freqs_cis: (cos, sin) of
+    [1, L, D] or [L, D/2]. k_stage: bf16 [B, L, H, D] destination of the
+    pre-RoPE normalized K (e.g. a layer's slice of the graph runner's stage
+    buffer), allocated when None. Returns (q, k, k_stage); k_stage equals
+    rmsnorm_qk_bf16(k) of the input k bit for bit."""
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+        raise RuntimeError(f"fused_qk_norm_rope_3d_kstage requires bf16 q/k, got {q.dtype}")
+    B, L, H, D = q.shape
+    if k_stage is None:
+        k_stage = torch.empty((B, L, H, D), dtype=torch.bfloat16, device=q.device)
+    cos, sin = _half_tables_bf16(freqs_cis, L, D, q.device)
+    fused_qk_norm_rope_3d_paired_kstage(q, k, k_stage, L, H, eps,
+                                        q_norm_weight.to(torch.bfloat16).contiguous(),
+                                        k_norm_weight.to(torch.bfloat16).contiguous(), cos, sin)
+    return q, k, k_stage
 
 
 def _heads_view(x: torch.Tensor) -> bool:
@@ -198,18 +243,12 @@ def fused_add_gate_layernorm_modulate(
     B, L, D = x.shape
     if not residual.is_contiguous():
         raise RuntimeError("residual must be contiguous (it is updated in place)")
-    x_2d = x.reshape(B * L, D)
-    r_2d = residual.view(B * L, D)
-    if B == 1:
-        out = fused_add_layernorm_scale_shift(x_2d, r_2d, scale.reshape(D), shift.reshape(D),
-                                              gate=gate.reshape(D), gamma=weight, beta=bias, eps=eps)
-        return residual, out.reshape(B, L, D)
-    out = torch.empty_like(x)
-    for b in range(B):
-        out[b] = fused_add_layernorm_scale_shift(x[b], residual[b], scale.reshape(B, D)[b],
-                                                 shift.reshape(B, D)[b], gate=gate.reshape(B, D)[b],
-                                                 gamma=weight, beta=bias, eps=eps)
-    return residual, out
+    out = fused_add_layernorm_scale_shift(x.reshape(B * L, D), residual.view(B * L, D),
+                                          _mod_per_sample(scale, B, L, D),
+                                          _mod_per_sample(shift, B, L, D),
+                                          gate=_mod_per_sample(gate, B, L, D), gamma=weight,
+                                          beta=bias, eps=eps)
+    return residual, out.reshape(B, L, D)
 
 
 def fused_qk_norm_rope_3d_grid_views(
@@ -257,11 +296,13 @@ def quantize_activation_fp8(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor
     return x_q, x_scale
 
 
-def _mod_of(t: torch.Tensor, B: int, L: int, D: int, b: int) -> torch.Tensor:
-    """Sample b's modulation: [D] from [B, D] / [B, 1, D], or [L, D] from [B, L, D]."""
+def _mod_per_sample(t: torch.Tensor, B: int, L: int, D: int) -> torch.Tensor:
+    """A modulation vector as the fused norm ops take it, without copies: [B, D]
+    or [B, 1, D] -> [B, D] (one row per sample of L rows; [D] when B == 1),
+    [B, L, D] -> [B*L, D] (a row per token)."""
     if t.numel() == B * D:
-        return t.reshape(B, D)[b]
-    return t.reshape(B, L, D)[b]
+        return t.reshape(D) if B == 1 else t.reshape(B, D)
+    return t.reshape(B * L, D)
 
 
 def _fp8_outputs(M: int, D: int, device) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -284,10 +325,9 @@ def layernorm_modulate_fp8(
     (x_q [B*L, D], x_scale [B*L, 1]), byte-identical to the two calls."""
     B, L, D = x.shape
     x_q, x_scale = _fp8_outputs(B * L, D, x.device)
-    for b in range(B):
-        rows = slice(b * L, (b + 1) * L)
-        norm_scale_shift_quant_fp8(x[b], _mod_of(scale, B, L, D, b), _mod_of(shift, B, L, D, b),
-                                   x_q[rows], x_scale[rows], gamma=weight, beta=bias, eps=eps)
+    norm_scale_shift_quant_fp8(x.reshape(B * L, D), _mod_per_sample(scale, B, L, D),
+                               _mod_per_sample(shift, B, L, D), x_q, x_scale, gamma=weight,
+                               beta=bias, eps=eps)
     return x_q, x_scale
 
 
@@ -309,12 +349,11 @@ def fused_add_gate_layernorm_modulate_fp8(
     if not residual.is_contiguous():
         raise RuntimeError("residual must be contiguous (it is updated in place)")
     x_q, x_scale = _fp8_outputs(B * L, D, x.device)
-    for b in range(B):
-        rows = slice(b * L, (b + 1) * L)
-        norm_scale_shift_quant_fp8(x[b], _mod_of(scale, B, L, D, b), _mod_of(shift, B, L, D, b),
-                                   x_q[rows], x_scale[rows], residual=residual[b],
-                                   gate=_mod_of(gate, B, L, D, b), gamma=weight, beta=bias,
-                                   eps=eps)
+    norm_scale_shift_quant_fp8(x.reshape(B * L, D), _mod_per_sample(scale, B, L, D),
+                               _mod_per_sample(shift, B, L, D), x_q, x_scale,
+                               residual=residual.view(B * L, D),
+                               gate=_mod_per_sample(gate, B, L, D), gamma=weight, beta=bias,
+                               eps=eps)
     return residual, x_q, x_scale
 
 

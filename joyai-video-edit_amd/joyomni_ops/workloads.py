@@ -30,6 +30,10 @@ Deployment shapes through the reference-signature entry points (reported):
   R_kn    rmsnorm_qk_bf16's per-head norm read straight from the K slice of the
           packed qkv [1, 3120, 3, 32, 128] (jo_rmsnorm_heads; the reference
           first copies that slice with .contiguous())
+  R_qks   the K-cache-before-RoPE branch (dit.py:360-370) in one pass:
+          fused_qk_norm_rope_3d_paired_kstage on the q / k slices of the packed
+          qkv [1, 3120, 3, 32, 128], bf16 [3120, 64] tables, pre-RoPE K to a
+          [1, 3120, 32, 128] stage
 
 The shapes of the reference's own benchmark script (test_bench.py; reported):
   T_rms   rmsnorm, x [4096, 4096]
@@ -85,6 +89,7 @@ CONFIGS: dict[str, Config] = {
     "R_q16k": Config("R_q16k", "quant", 13, dict(M=3120, K=16384)),
     "R_rms": Config("R_rms", "rmsnorm", 14, dict(M=99840, N=128, eps=1e-6)),
     "R_kn": Config("R_kn", "rms_heads", 16, dict(B=1, L=3120, H=32, D=128, eps=1e-6)),
+    "R_qks": Config("R_qks", "qk_kstage", 21, dict(B=1, L=3120, H=32, D=128, eps=1e-6)),
     # The shapes of the reference's own benchmark script
     # (deploy/joyomni_ops/tests/test_bench.py:59-200); reported, not gated.
     "T_rms": Config("T_rms", "rmsnorm", 17, dict(M=4096, N=4096, eps=1e-6)),
@@ -162,6 +167,13 @@ def make_inputs(cfg: Config, device="cpu") -> dict:
     elif cfg.op == "rms_heads":
         out["qkv"] = torch.randn(d["B"], d["L"], 3, d["H"], d["D"], generator=g).to(torch.bfloat16)
         out["weight"] = (1 + 0.1 * torch.randn(d["D"], generator=g)).to(torch.bfloat16)
+    elif cfg.op == "qk_kstage":
+        out["qkv"] = torch.randn(d["B"], d["L"], 3, d["H"], d["D"], generator=g).to(torch.bfloat16)
+        out["q_weight"] = (1 + 0.1 * torch.randn(d["D"], generator=g)).to(torch.bfloat16)
+        out["k_weight"] = (1 + 0.1 * torch.randn(d["D"], generator=g)).to(torch.bfloat16)
+        ang = torch.rand(d["L"], d["D"] // 2, generator=g) * 100
+        out["cos"] = ang.cos().to(torch.bfloat16)
+        out["sin"] = ang.sin().to(torch.bfloat16)
     else:
         raise ValueError(cfg.op)
     return {k: v.to(device) for k, v in out.items()}
@@ -179,6 +191,10 @@ def algorithmic_bytes(cfg: Config) -> int:
     if cfg.op == "qk_table":
         n = d["B"] * d["L"] * d["H"] * d["D"] * 2
         return 4 * n + 2 * d["D"] * 2 + 2 * d["L"] * (d["D"] // 2) * 2   # + cos/sin tables
+    if cfg.op == "qk_kstage":
+        n = d["B"] * d["L"] * d["H"] * d["D"] * 2
+        # q, k read + written, pre-RoPE k written; weights; cos/sin tables
+        return 5 * n + 2 * d["D"] * 2 + 2 * d["L"] * (d["D"] // 2) * 2
     if cfg.op == "ln_rows":
         return 4 * d["M"] * d["N"] * 2                     # x, scale, shift in; y out
     if cfg.op == "rmsnorm":
@@ -224,7 +240,7 @@ def alloc_outputs(cfg: Config, inputs: dict) -> dict:
         return {"y": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev)}
     if cfg.op == "rmsnorm":
         return {"out": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev)}
-    if cfg.op == "rms_heads":
+    if cfg.op in ("rms_heads", "qk_kstage"):
         return {"out": torch.empty(d["B"], d["L"], d["H"], d["D"], dtype=torch.bfloat16,
                                    device=dev)}
     if cfg.op == "gemm":
@@ -252,7 +268,7 @@ def launch(cfg: Config, t: dict, stream_handle: int, freqs: torch.Tensor | None 
                   stream_handle)
     elif cfg.op == "add_ln":
         _abi.call("jo_fused_add_layernorm_scale_shift", p(t["x"]), d["N"], p(t["residual"]),
-                  d["N"], None, 0, None, None, p(t["scale"]), 0, p(t["shift"]), 0, p(t["y"]),
+                  d["N"], None, 0, None, None, p(t["scale"]), 0, p(t["shift"]), 0, 1, p(t["y"]),
                   d["N"], d["M"], d["N"], _abi.JO_DTYPE_BF16, d["eps"], stream_handle)
     elif cfg.op == "ln_rows":
         _abi.call("jo_fused_norm_scale_shift", p(t["x"]), d["N"], None, None, p(t["scale"]),
@@ -266,6 +282,13 @@ def launch(cfg: Config, t: dict, stream_handle: int, freqs: torch.Tensor | None 
         k = t["qkv"][:, :, 1]
         _abi.call("jo_rmsnorm_heads", p(k), 3 * H * D, D, p(t["weight"]), p(t["out"]), D, B * L,
                   H, D, _abi.JO_DTYPE_BF16, d["eps"], 0, stream_handle)
+    elif cfg.op == "qk_kstage":
+        B, L, H, D = d["B"], d["L"], d["H"], d["D"]
+        qkv = t["qkv"]
+        tok = 3 * H * D
+        _abi.call("jo_fused_qk_norm_rope_3d_paired_kstage", p(qkv[:, :, 0]), p(qkv[:, :, 1]),
+                  p(t["out"]), B, L, H, D, L * tok, tok, L * tok, tok, L * H * D, H * D, d["eps"],
+                  p(t["q_weight"]), p(t["k_weight"]), p(t["cos"]), p(t["sin"]), stream_handle)
     elif cfg.op == "qk_table":
         B, L, H, D = d["B"], d["L"], d["H"], d["D"]
         tok = H * D
@@ -274,7 +297,7 @@ def launch(cfg: Config, t: dict, stream_handle: int, freqs: torch.Tensor | None 
                   p(t["sin"]), stream_handle)
     elif cfg.op == "add_ln_quant":
         _abi.call("jo_norm_scale_shift_quant_fp8", p(t["x"]), d["N"], p(t["residual"]), d["N"],
-                  p(t["gate"]), 0, None, None, p(t["scale"]), 0, p(t["shift"]), 0, p(t["q"]),
+                  p(t["gate"]), 0, None, None, p(t["scale"]), 0, p(t["shift"]), 0, 1, p(t["q"]),
                   d["N"], p(t["s"]), d["M"], d["N"], _abi.JO_DTYPE_BF16, _abi.JO_NORM_LAYER,
                   d["eps"], stream_handle)
     elif cfg.op == "gemm":

@@ -124,8 +124,14 @@ BAD_CALLS = [
      "bad shape"),
     # zero-width rows would leave scales with nothing to take them from
     ("jo_norm_scale_shift_quant_fp8",
-     (16, 8, None, 8, None, 0, None, None, 16, 0, 16, 0, 16, 8, 16, 4, 0, 2, 0, 1e-6, None),
+     (16, 8, None, 8, None, 0, None, None, 16, 0, 16, 0, 1, 16, 8, 16, 4, 0, 2, 0, 1e-6, None),
      "bad shape"),
+    ("jo_norm_scale_shift_quant_fp8",
+     (16, 8, None, 8, None, 0, None, None, 16, 8, 16, 8, 0, 16, 8, 16, 4, 8, 2, 0, 1e-6, None),
+     "mod_rows"),
+    ("jo_fused_add_layernorm_scale_shift",
+     (16, 8, 16, 8, None, 0, None, None, 16, 8, 16, 8, 0, 16, 8, 4, 8, 2, 1e-6, None),
+     "mod_rows"),
     ("jo_rmsnorm", (16, 8, 16, None, 8, 4, 8, 2, 1e-6, None), "null pointer"),
     ("jo_rmsnorm_heads", (16, 1152, 128, 16, 16, 128, 4, 3, 128, 2, 1e-6, 2, None), "round_first"),
     ("jo_rmsnorm_heads", (16, 1152, 128, 16, 16, 128, 4, 0, 128, 2, 1e-6, 0, None), "bad shape"),
@@ -133,7 +139,7 @@ BAD_CALLS = [
     ("jo_rmsnorm_heads", (16, 1152, 128, None, 16, 128, 4, 3, 128, 2, 1e-6, 1, None), "null pointer"),
     ("jo_rmsnorm_heads", (16, 1152, 128, 16, 16, 128, 4, 3, 128, 9, 1e-6, 1, None), "dtype"),
     ("jo_fused_add_layernorm_scale_shift",
-     (16, 12, 16, 12, None, 0, None, None, 16, 0, 16, 0, 16, 8, 4, 12, 2, 1e-6, None),
+     (16, 12, 16, 12, None, 0, None, None, 16, 0, 16, 0, 1, 16, 8, 4, 12, 2, 1e-6, None),
      "bad row stride"),
     ("jo_rmsnorm_quant_fp8", (16, 256, 16, 16, 256, 16, 4, 256, 2, 1e-6, 64, None), "group_size"),
     ("jo_rmsnorm_quant_fp8", (16, 200, 16, 16, 200, 16, 4, 200, 2, 1e-6, 128, None), "divisible by 128"),
@@ -170,12 +176,12 @@ def test_empty_inputs_are_noops(abi):
     assert lib.jo_fused_qk_norm_rope_3d_paired(None, None, 1, 0, 2, 128, 0, 256, 0, 256, 1e-6,
                                                None, None, None, None, None) == abi.JO_OK
     assert lib.jo_fused_add_layernorm_scale_shift(None, 8, None, 8, None, 0, None, None, None, 0,
-                                                  None, 0, None, 8, 0, 8, 2, 1e-6,
+                                                  None, 0, 1, None, 8, 0, 8, 2, 1e-6,
                                                   None) == abi.JO_OK
     assert lib.jo_rmsnorm_quant_fp8(None, 8, None, None, 8, None, 0, 8, 2, 1e-6, 0,
                                     None) == abi.JO_OK
     assert lib.jo_norm_scale_shift_quant_fp8(None, 8, None, 8, None, 0, None, None, None, 0, None,
-                                             0, None, 8, None, 0, 8, 2, 0, 1e-6,
+                                             0, 1, None, 8, None, 0, 8, 2, 0, 1e-6,
                                              None) == abi.JO_OK
     assert lib.jo_fp8_scaled_mm(None, 16, None, 16, None, None, None, None, 8, 0, 8, 16, 2,
                                 None) == abi.JO_OK

@@ -57,7 +57,7 @@ def run_fused(abi, stream, d, M, N, dtype, norm, eps, x_stride=None, q_stride=No
     rs = N if d["scale"].dim() == 2 else 0
     abi.call("jo_norm_scale_shift_quant_fp8", d["x"].data_ptr(), xs, ptr(d["residual"]), N,
              ptr(d["gate"]), rs, ptr(d["gamma"]), ptr(d["beta"]), d["scale"].data_ptr(), rs,
-             d["shift"].data_ptr(), rs, q.data_ptr(), qs, s.data_ptr(), M, N,
+             d["shift"].data_ptr(), rs, 1, q.data_ptr(), qs, s.data_ptr(), M, N,
              abi.dtype_code(dtype), NORM[norm], eps, stream)
     return q, s
 
@@ -172,13 +172,47 @@ def test_norm_quant_rejects(abi, dev, stream_handle):
     s = torch.empty(4, dtype=torch.float32, device=dev)
     with pytest.raises(RuntimeError, match="bf16 or fp16"):
         abi.call("jo_norm_scale_shift_quant_fp8", x.data_ptr(), 64, None, 0, None, 0, None, None,
-                 x.data_ptr(), 0, x.data_ptr(), 0, q.data_ptr(), 64, s.data_ptr(), 4, 64,
+                 x.data_ptr(), 0, x.data_ptr(), 0, 1, q.data_ptr(), 64, s.data_ptr(), 4, 64,
                  abi.dtype_code(torch.float32), 0, 1e-6, stream_handle)
     xb = x.to(torch.bfloat16)
     with pytest.raises(RuntimeError, match="gate needs a residual"):
         abi.call("jo_norm_scale_shift_quant_fp8", xb.data_ptr(), 64, None, 0, xb.data_ptr(), 0,
-                 None, None, xb.data_ptr(), 0, xb.data_ptr(), 0, q.data_ptr(), 64, s.data_ptr(),
+                 None, None, xb.data_ptr(), 0, xb.data_ptr(), 0, 1, q.data_ptr(), 64, s.data_ptr(),
                  4, 64, abi.dtype_code(torch.bfloat16), 0, 1e-6, stream_handle)
+
+
+@pytest.mark.parametrize("B,L,N", [(2, 300, 3072), (3, 17, 512)])
+def test_norm_quant_per_sample_modulation(abi, dev, stream_handle, B, L, N):
+    """One call for a batch (mod_rows = L, gate / scale / shift [B, N]): the
+    residual bit-exact against the oracle, the fp8 bytes and scales bit-exact
+    against the C quantizer applied to the y the unfused device op stores for
+    the same rows, and that y within 1 ulp of the oracle."""
+    import joyomni_ops as jo
+    dtype = torch.bfloat16
+    M = B * L
+    g = torch.Generator().manual_seed(B * 10 + L + N)
+    x = torch.randn(M, N, generator=g).to(dtype)
+    res = torch.randn(M, N, generator=g).to(dtype)
+    gate = torch.randn(B, N, generator=g).to(dtype)
+    sc = (0.2 * torch.randn(B, N, generator=g)).to(dtype)
+    sh = (0.2 * torch.randn(B, N, generator=g)).to(dtype)
+    xd, rd, gd, scd, shd = (t.to(dev) for t in (x, res, gate, sc, sh))
+    r2 = rd.clone()
+    q = torch.full((M, N), 0x55, dtype=torch.uint8, device=dev)
+    s = torch.full((M,), -1.0, dtype=torch.float32, device=dev)
+    abi.call("jo_norm_scale_shift_quant_fp8", xd.data_ptr(), N, rd.data_ptr(), N, gd.data_ptr(),
+             N, None, None, scd.data_ptr(), N, shd.data_ptr(), N, L, q.data_ptr(), N,
+             s.data_ptr(), M, N, abi.dtype_code(dtype), 0, 1e-6, stream_handle)
+    ex = lambda t: t.repeat_interleave(L, dim=0)  # noqa: E731
+    y_dev = jo.fused_add_layernorm_scale_shift(xd, r2, ex(scd), ex(shd), gate=ex(gd), eps=1e-6)
+    torch.cuda.synchronize()
+    new_res, qo, so, yo = ops.norm_scale_shift_quant_fp8(x, res, ex(gate), None, None, ex(sc),
+                                                         ex(sh), 0, 1e-6, y=y_dev.cpu())
+    assert torch.equal(rd.cpu(), new_res) and torch.equal(r2.cpu(), new_res), "residual"
+    assert torch.equal(q.cpu(), qo), "fp8 bytes"
+    assert torch.equal(s.cpu(), so), "scales"
+    ref = ops.norm_scale_shift_f32(new_res, None, None, ex(sc), ex(sh), 0, 1e-6)
+    assert_within_ulp(yo, ref, dtype, ref.abs().amax(-1, keepdim=True), what="y per sample")
 
 
 def test_torch_op_and_dit_shims(dev):

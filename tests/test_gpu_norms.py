@@ -154,10 +154,34 @@ def test_add_layernorm(abi, dev, stream_handle, dtype, M, N, gated, per_row):
     rs = N if per_row else 0
     abi.call("jo_fused_add_layernorm_scale_shift", xd.data_ptr(), N, rd.data_ptr(), N,
              gd.data_ptr() if gated else None, rs, None, None, scd.data_ptr(), rs, shd.data_ptr(),
-             rs, y.data_ptr(), N, M, N, abi.dtype_code(dtype), 1e-6, stream_handle)
+             rs, 1, y.data_ptr(), N, M, N, abi.dtype_code(dtype), 1e-6, stream_handle)
     torch.cuda.synchronize()
     check_add_ln(rd.cpu(), y.cpu(), x, res, gate, None, None, sc, sh, 1e-6, dtype,
                  f"add_ln {dtype} [{M},{N}] gated={gated} per_row={per_row}")
+
+
+@pytest.mark.parametrize("B,L,N", [(2, 300, 3072), (3, 17, 512), (4, 5, 100)])
+def test_add_layernorm_per_sample_modulation(abi, dev, stream_handle, B, L, N):
+    """One call for a batch: gate / scale / shift [B, N], each row serving the L
+    rows of its sample (mod_rows = L), against the oracle with the rows expanded
+    (what the reference caller materialises, sgl_fused_ops.py:44-51)."""
+    dtype = torch.bfloat16
+    M = B * L
+    g = torch.Generator().manual_seed(B * 100 + L + N)
+    x = torch.randn(M, N, generator=g).to(dtype)
+    res = torch.randn(M, N, generator=g).to(dtype)
+    gate = torch.randn(B, N, generator=g).to(dtype)
+    sc = (0.2 * torch.randn(B, N, generator=g)).to(dtype)
+    sh = (0.2 * torch.randn(B, N, generator=g)).to(dtype)
+    xd, rd, gd, scd, shd = (t.to(dev) for t in (x, res, gate, sc, sh))
+    y = torch.empty(M, N, dtype=dtype, device=dev)
+    abi.call("jo_fused_add_layernorm_scale_shift", xd.data_ptr(), N, rd.data_ptr(), N,
+             gd.data_ptr(), N, None, None, scd.data_ptr(), N, shd.data_ptr(), N, L, y.data_ptr(),
+             N, M, N, abi.dtype_code(dtype), 1e-6, stream_handle)
+    torch.cuda.synchronize()
+    ex = lambda t: t.repeat_interleave(L, dim=0)  # noqa: E731
+    check_add_ln(rd.cpu(), y.cpu(), x, res, ex(gate), None, None, ex(sc), ex(sh), 1e-6, dtype,
+                 f"add_ln per sample B={B} L={L} N={N}")
 
 
 def test_add_layernorm_full_c2_and_torch_op(dev):
