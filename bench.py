@@ -26,11 +26,13 @@ the reference's own benchmark script (test_bench.py): rmsnorm and LayerNorm +
 modulation at [4096, 4096], table-mode QK at [1, 1560, 32, 128], the FP8 GEMM
 at 4096^3.
 
-Timing: max(W, 20) eager warmup calls, then K calls captured into one HIP
-graph, replayed once untimed and then ceil(100 / K) times between HIP events
-recorded on the replay stream (the stream the kernels run on), so that at
-least 100 calls are timed whatever K is (`timed_calls` in each line);
-per-call time = elapsed / timed calls. The calls rotate over >= 4
+Timing: max(W, 20) eager warmup calls, K eager calls (eager_us_per_call),
+then max(K, 100) calls captured into one HIP graph, replayed once untimed and
+then five times, each replay between HIP events recorded on the replay stream
+(the stream the kernels run on); per-call time = the median over the five
+replays of elapsed / calls (min and max beside it), so that at least 500
+calls are timed whatever K is (`timed_calls` in each line). Each config's
+stream ceilings (S_*) are timed right after it. The calls rotate over >= 4
 input/output buffer sets totalling > 640 MB so the 256 MB Infinity Cache
 cannot hold the working set. Inputs are resident in HBM before the timed
 region. achieved GB/s = algorithmic bytes (compulsory reads + writes,
@@ -103,7 +105,8 @@ def copy_probe(mb: int, steps: int, dev) -> dict:
     return {"bytes_each_way": n, "us_per_call": round(us, 3), "gbps": round(2 * n / (us * 1e-6) / 1e9, 1)}
 
 
-MIN_TIMED = 100   # timed calls per line, whatever --steps is
+MIN_TIMED = 100   # calls per timed graph replay, whatever --steps is
+TIMED_REPLAYS = 5  # timed replays per line; the line reports their median
 MIN_WARMUP = 20   # eager warmup calls per line, whatever --warmup is
 
 
@@ -112,9 +115,11 @@ def time_launches(launch, n_sets: int, steps: int, warmup: int, dev,
     """Times launch(i, stream_handle) (call i uses buffer set i % n_sets).
 
     max(warmup, MIN_WARMUP) eager warmups; `steps` eager launches timed for
-    eager_us_per_call; then `steps` launches captured into one HIP graph,
-    replayed once untimed and ceil(MIN_TIMED / steps) times between HIP events
-    on the replay stream. Returns per-call times and the timed call count."""
+    eager_us_per_call; then max(steps, MIN_TIMED) launches captured into one
+    HIP graph, replayed once untimed and once between HIP events on the replay
+    stream. (One long graph rather than a short one replayed several times:
+    the residual + LayerNorm kernels measured 1.5-2 us per call slower as 20-call
+    graphs replayed five times than as one 100-call graph.)"""
     import torch
     warmup = max(warmup, MIN_WARMUP)
     stream = torch.cuda.Stream(dev)
@@ -137,32 +142,35 @@ def time_launches(launch, n_sets: int, steps: int, warmup: int, dev,
         return {"us_per_call": eager_us, "eager_us_per_call": eager_us, "timed_calls": steps,
                 "warmup_calls": warmup, "timing": "eager"}
 
-    # HIP graph of `steps` launches, replayed until >= MIN_TIMED calls are timed
+    calls = max(steps, MIN_TIMED)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         h = torch.cuda.current_stream().cuda_stream
-        for i in range(steps):
+        for i in range(calls):
             launch(i, h)
     graph.replay()
     torch.cuda.synchronize()
-    replays = max(1, math.ceil(MIN_TIMED / steps))
     cur = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(cur)
-    for _ in range(replays):
+    per_call = []
+    for _ in range(TIMED_REPLAYS):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
         graph.replay()
-    e1.record(cur)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / (steps * replays)
+        e1.record(cur)
+        torch.cuda.synchronize()
+        per_call.append(e0.elapsed_time(e1) * 1000.0 / calls)
     del graph
-    return {"us_per_call": us, "eager_us_per_call": eager_us, "timed_calls": steps * replays,
-            "warmup_calls": warmup, "timing": "hip-graph"}
+    return {"us_per_call": statistics.median(per_call), "eager_us_per_call": eager_us,
+            "min_us_per_call": min(per_call), "max_us_per_call": max(per_call),
+            "timed_calls": calls * TIMED_REPLAYS, "warmup_calls": warmup, "timing": "hip-graph"}
 
 
 def _finish(res: dict, alg: int, n_sets: int, set_bytes: int) -> dict:
     us = res["us_per_call"]
     gbps = alg / (us * 1e-6) / 1e9
     out = {"us_per_call": round(us, 3), "eager_us_per_call": round(res["eager_us_per_call"], 3),
+           "min_us_per_call": round(res.get("min_us_per_call", us), 3),
+           "max_us_per_call": round(res.get("max_us_per_call", us), 3),
            "gbps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_GBPS, 4),
            "algorithmic_bytes": alg, "buffer_sets": n_sets,
            "rotated_mb": round(n_sets * set_bytes / 1e6, 1),
@@ -574,7 +582,11 @@ def main() -> int:
     if args.only:
         names = [n for n in args.only.split(",") if n]
     else:
-        names = list(W.CONFIGS) + ([] if args.no_streams else list(STREAMS))
+        names = []
+        for c in W.CONFIGS:
+            names.append(c)
+            if not args.no_streams:
+                names += [sn for sn, spec in STREAMS.items() if spec[0] == c]
     if HEADLINE not in names:
         names.insert(0, HEADLINE)
     results = {}

@@ -273,7 +273,7 @@ void rmsnorm_quant_tok_kernel(
 // Per 1x128 block: each 16-lane DPP row of a chunk holds one block. Same
 // fast / exact paths as per token, decided per block; the vote for the
 // NaN-skipping maxima is wave-wide (workgroup-wide for rows wider than a wave).
-template <class Tag, int LPR, int CH, bool EXACT>
+template <class Tag, int LPR, int CH, bool EXACT, bool KEEPX>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kC4WavesPerSimd)))
 void rmsnorm_quant_blk_kernel(
     const void* __restrict__ x, int64_t xs, const void* __restrict__ w, uint8_t* __restrict__ q,
@@ -286,9 +286,9 @@ void rmsnorm_quant_blk_kernel(
   const bool row_ok = row < M;
   u32x4 c[CH], wc[CH];
   load_row_weight<Tag, LPR, CH, EXACT>(x, xs, w, row_ok ? row : M - 1, lane, N, c, wc);
-  float xf[1][8];
+  float xf[KEEPX ? CH : 1][8];
   const float r =
-      rms_rstd(row_reduce_sum64<LPR>(lane_sum_squares<Tag, CH, false>(c, xf), red_ss), N, eps);
+      rms_rstd(row_reduce_sum64<LPR>(lane_sum_squares<Tag, CH, KEEPX>(c, xf), red_ss), N, eps);
 
   float v[CH][8];
   float gmax[CH];
@@ -298,7 +298,7 @@ void rmsnorm_quant_blk_kernel(
     float m = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      v[i][j] = (elem<Tag>(c[i], j) * r) * elem<Tag>(wc[i], j);
+      v[i][j] = (x_at<Tag, CH, KEEPX>(c, xf, i, j) * r) * elem<Tag>(wc[i], j);
       m = nan_max_abs(m, v[i][j]);
     }
     gmax[i] = allreduce_amax<16>(m);
@@ -396,12 +396,22 @@ int launch_rmsnorm_quant(const void* x, int64_t xs, const void* w, void* q, int6
       constexpr int LPR = decltype(lpr)::value < 16 ? 16 : decltype(lpr)::value;
       constexpr int CH = decltype(ch)::value;
       const dim3 grid(static_cast<unsigned>(row_blocks(M, LPR)));
-      if (int64_t{LPR} * CH * 8 == N)
-        hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, true>), grid, dim3(kBlock), 0,
-                           stream, x, xs, w, q8, qs, s, M, n, eps);
-      else
-        hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, false>), grid, dim3(kBlock), 0,
-                           stream, x, xs, w, q8, qs, s, M, n, eps);
+      const bool exact = int64_t{LPR} * CH * 8 == N;
+      if (M >= kFewRows) {
+        if (exact)
+          hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, true, true>), grid,
+                             dim3(kBlock), 0, stream, x, xs, w, q8, qs, s, M, n, eps);
+        else
+          hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, false, true>), grid,
+                             dim3(kBlock), 0, stream, x, xs, w, q8, qs, s, M, n, eps);
+      } else {
+        if (exact)
+          hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, true, false>), grid,
+                             dim3(kBlock), 0, stream, x, xs, w, q8, qs, s, M, n, eps);
+        else
+          hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, false, false>), grid,
+                             dim3(kBlock), 0, stream, x, xs, w, q8, qs, s, M, n, eps);
+      }
     });
   }
   if (!launched) {

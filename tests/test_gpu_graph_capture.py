@@ -49,15 +49,26 @@ def prepare(host: dict, dev) -> dict:
     return s
 
 
-def block(s: dict) -> dict:
+def block(s: dict, qk: str = "views") -> dict:
+    """qk = "views": the pre-RoPE K norm, then grid RoPE in place on the qkv
+    views (two ops); "kstage": both in one pass (the *_kstage op)."""
+    import joyomni_ops as jo
     from joyomni_ops import dit_ops
     x_q, x_s = dit_ops.layernorm_modulate_fp8(s["img"], s["shift1"], s["scale1"])
     qkv = dit_ops.fp8_linear_quantized(x_q, x_s, s["wq_qkv"], s["ws_qkv"], s["b_qkv"])
     iv = qkv.view(B, L, 3, H, D)
-    k_pre = dit_ops.rmsnorm_qk_bf16(iv[:, :, 1], s["kw"])
-    q, k = dit_ops.fused_qk_norm_rope_3d_grid_views(
-        iv[:, :, 0], iv[:, :, 1], s["qw"], s["kw"], grid_hw=(GH, GW), t0=3,
-        rope_dims=(16, 56, 56), theta=256.0, source_id=1.0)
+    if qk == "views":
+        k_pre = dit_ops.rmsnorm_qk_bf16(iv[:, :, 1], s["kw"])
+        q, k = dit_ops.fused_qk_norm_rope_3d_grid_views(
+            iv[:, :, 0], iv[:, :, 1], s["qw"], s["kw"], grid_hw=(GH, GW), t0=3,
+            rope_dims=(16, 56, 56), theta=256.0, source_id=1.0)
+    else:
+        k_pre = torch.empty(B, L, H, D, dtype=torch.bfloat16, device=qkv.device)
+        freqs = jo.rope_freqs(D, (16, 56, 56), 256.0, 256.0, 128)
+        jo.fused_qk_norm_rope_3d_grid_kstage(iv[:, :, 0], iv[:, :, 1], k_pre, L, H, 1e-6,
+                                             s["qw"], s["kw"], freqs, (16, 56, 56), (GH, GW), 3,
+                                             1.0)
+        q = iv[:, :, 0]
     attn = q.reshape(B, L, HID)  # stands in for the attention output
     res, x_q2, x_s2 = dit_ops.fused_add_gate_layernorm_modulate_fp8(
         s["res"], attn, s["gate"], s["shift2"], s["scale2"])
@@ -92,3 +103,29 @@ def test_dit_block_graph_replays_match_eager(dev):
         for k in want:
             assert torch.equal(as_bits(got[k]), as_bits(want[k])), f"replay {rep}: {k} differs"
         assert bool(got["up"].float().abs().sum() > 0), "graph produced nothing"
+
+
+def test_graph_captured_on_first_use_with_kstage(dev):
+    """Nothing runs eagerly before the capture (the grid RoPE frequencies travel
+    in the kernel arguments, so the first call needs no device setup): the
+    block with the one-pass K stage is captured cold, replayed three times with
+    new inputs, and every replay equals, bit for bit, the eager two-op block."""
+    import joyomni_ops as jo
+    jo._FREQ_CACHE.clear()
+    static = prepare(make_inputs(10), dev)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = block(static, "kstage")
+    torch.cuda.synchronize()
+    for rep in range(11, 14):
+        fresh = prepare(make_inputs(rep), dev)
+        for k, v in fresh.items():
+            static[k].copy_(v)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = {k: v.clone() for k, v in outs.items()}
+        want = block(prepare(make_inputs(rep), dev), "views")
+        torch.cuda.synchronize()
+        for k in want:
+            assert torch.equal(as_bits(got[k]), as_bits(want[k])), f"replay {rep}: {k} differs"
