@@ -27,12 +27,13 @@ modulation at [4096, 4096], table-mode QK at [1, 1560, 32, 128], the FP8 GEMM
 at 4096^3.
 
 Timing: max(W, 20) eager warmup calls, K eager calls (eager_us_per_call),
-then max(K, 100) calls captured into one HIP graph, replayed once untimed and
-then five times, each replay between HIP events recorded on the replay stream
-(the stream the kernels run on); per-call time = the median over the five
-replays of elapsed / calls (min and max beside it), so that at least 500
-calls are timed whatever K is (`timed_calls` in each line). Each config's
-stream ceilings (S_*) are timed right after it. The calls rotate over >= 4
+then max(K, 100) calls captured into one HIP graph. Five times: the graph is
+replayed untimed and, enqueued right behind it (the GPU kept busy), replayed
+again between HIP events recorded on the replay stream (the stream the kernels
+run on). Per-call time = the median over the five timed replays of elapsed /
+calls (min and max beside it), so that at least 500 calls are timed whatever
+K is (`timed_calls` in each line). Each config's stream ceilings (S_*) are
+timed right after it. The calls rotate over >= 4
 input/output buffer sets totalling > 640 MB so the 256 MB Infinity Cache
 cannot hold the working set. Inputs are resident in HBM before the timed
 region. achieved GB/s = algorithmic bytes (compulsory reads + writes,
@@ -153,6 +154,10 @@ def time_launches(launch, n_sets: int, steps: int, warmup: int, dev,
     cur = torch.cuda.current_stream(dev)
     per_call = []
     for _ in range(TIMED_REPLAYS):
+        # An untimed replay is enqueued right before each timed one, so that the
+        # timed calls run on a GPU that is already busy (steady state) rather
+        # than one that has just idled through the host's synchronization.
+        graph.replay()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(cur)
         graph.replay()
