@@ -561,6 +561,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", default="", help="comma-separated config names (C*, S_*, ...)")
     ap.add_argument("--no-streams", action="store_true", help="skip the S_* stream ceilings")
+    ap.add_argument("--no-compare", action="store_true",
+                    help="skip the reference-path timings (hipBLASLt, the torch commit loop, "
+                         "the reference callers' unfused calls), e.g. for profiler runs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--cpu-iters", type=int, default=10, help="minimum timed CPU calls per config")
     ap.add_argument("--cpu-seconds", type=float, default=2.0,
@@ -604,13 +607,13 @@ def main() -> int:
         cfg = W.CONFIGS[n]
         log(f"{n}: timing {'eager' if args.no_graph else 'graph-replayed'} calls")
         results[n] = time_gpu(cfg, args.steps, args.warmup, dev, use_graph=not args.no_graph)
-        ref_us = torch_reference_us(cfg, dev)
+        ref_us = None if args.no_compare else torch_reference_us(cfg, dev)
         if ref_us is not None:
             results[n]["torch_reference_us_per_call"] = ref_us
-        caller_us = copy_then_rmsnorm_us(cfg, dev)
+        caller_us = None if args.no_compare else copy_then_rmsnorm_us(cfg, dev)
         if caller_us is not None:
             results[n]["copy_then_rmsnorm_us_per_call"] = caller_us
-        two_call_us = unfused_kstage_us(cfg, dev)
+        two_call_us = None if args.no_compare else unfused_kstage_us(cfg, dev)
         if two_call_us is not None:
             results[n]["unfused_two_calls_us_per_call"] = two_call_us
         flops = W.algorithmic_flops(cfg)
@@ -620,7 +623,7 @@ def main() -> int:
             results[n].pop("frac_of_peak", None)
             results[n].update(bound="mfma", algorithmic_flops=flops, tflops=round(tf, 1),
                               frac_of_fp8_peak=round(tf / PEAK_FP8_TFLOPS, 4))
-            ab = gemm_vs_hipblaslt(cfg, dev)
+            ab = None if args.no_compare else gemm_vs_hipblaslt(cfg, dev)
             if ab is not None:
                 results[n]["ab_eager_us_per_call"] = ab[0]
                 results[n]["hipblaslt_us_per_call"] = ab[1]
