@@ -59,6 +59,7 @@ Prints ONE JSON line on stdout; progress goes to stderr.
 from __future__ import annotations
 
 import argparse
+import collections
 import json
 import math
 import os
@@ -210,36 +211,55 @@ def time_gpu(cfg, steps: int, warmup: int, dev, use_graph: bool = True) -> dict:
 
 
 # ---------------------------------------------------------------------------
-# Stream ceilings: (config it bounds, rows, lanes per row, chunks per lane,
-# input streams, output streams, bytes stored per 16 read, fp32 scalars per
-# row, in place). The first entry of a config is its kernel's launch shape;
-# entries named S_<cfg>@<LPR>x<CH> are other shapes of the same bytes.
+# Stream ceilings. Each entry: the config it bounds, rows, lanes per row,
+# chunks per lane, input streams, output streams, bytes stored per 16 read,
+# fp32 scalars per row, in place, row-invariant inputs (the weight row a
+# kernel reads, through the cache, for every row), and for input rows that
+# come in groups (per-head rows of a strided view) the rows per group, the
+# bytes between groups and the offset of the first row. The entry named
+# S_<cfg> is the kernel's own access shape; entries named S_<cfg>@<what> are
+# other shapes of the same bytes (@LPRxCH) or the shape without the cached
+# weight reads (@no-weight) or without the stride (@contiguous).
 # ---------------------------------------------------------------------------
+Stream = collections.namedtuple(
+    "Stream", "cfg rows lpr ch nin nout outb nscal inplace nconst group gstride goff",
+    defaults=(0, 0, 0, 0))
+
+_S = Stream
 STREAMS = {
-    "S_C0": ("C0", 3510 * 4, 64, 3, 1, 1, 16, 0, True),
-    "S_C0@64x1": ("C0", 3510 * 12, 64, 1, 1, 1, 16, 0, True),
-    "S_C0@64x2": ("C0", 3510 * 6, 64, 2, 1, 1, 16, 0, True),
-    "S_C1": ("C1", 10530, 64, 6, 1, 1, 8, 1, False),
-    "S_C1@128x3": ("C1", 10530, 128, 3, 1, 1, 8, 1, False),
-    "S_C2": ("C2", 10530, 128, 3, 2, 2, 16, 0, False),
-    "S_C2@64x6": ("C2", 10530, 64, 6, 2, 2, 16, 0, False),
-    "S_C3": ("C3", 10530 * 4, 64, 3, 1, 1, 16, 0, True),
-    "S_C4_4725_tok": ("C4_4725_tok", 4725, 64, 6, 1, 1, 8, 1, False),
-    "S_C4_4725_tok@128x3": ("C4_4725_tok", 4725, 128, 3, 1, 1, 8, 1, False),
-    "S_C4_4725_tok@256x2": ("C4_4725_tok", 4725, 256, 2, 1, 1, 8, 1, False),
-    "S_C4_4725_blk": ("C4_4725_blk", 4725, 64, 6, 1, 1, 8, 24, False),
-    "S_C4_10530_tok": ("C4_10530_tok", 10530, 64, 6, 1, 1, 8, 1, False),
-    "S_C4_10530_blk": ("C4_10530_blk", 10530, 64, 6, 1, 1, 8, 24, False),
-    "S_R_q4k": ("R_q4k", 3120, 128, 4, 1, 1, 8, 1, False),
-    "S_R_q4k@64x8": ("R_q4k", 3120, 64, 8, 1, 1, 8, 1, False),
-    "S_R_q16k": ("R_q16k", 3120, 256, 8, 1, 1, 8, 1, False),
-    "S_R_rms": ("R_rms", 99840, 16, 1, 1, 1, 16, 0, False),
-    "S_R_ln": ("R_ln", 3120, 256, 2, 3, 1, 16, 0, False),
-    "S_R_ln@64x8": ("R_ln", 3120, 64, 8, 3, 1, 16, 0, False),
-    "S_R_qk": ("R_qk", 3120 * 8, 64, 2, 1, 1, 16, 0, True),
-    "S_T_rms": ("T_rms", 4096, 64, 8, 1, 1, 16, 0, False),
-    "S_T_ln": ("T_ln", 4096, 256, 2, 3, 1, 16, 0, False),
-    "S_T_qk": ("T_qk", 1560 * 8, 64, 2, 1, 1, 16, 0, True),
+    "S_C0": _S("C0", 3510 * 4, 64, 3, 1, 1, 16, 0, True),
+    "S_C0@64x1": _S("C0", 3510 * 12, 64, 1, 1, 1, 16, 0, True),
+    "S_C0@64x2": _S("C0", 3510 * 6, 64, 2, 1, 1, 16, 0, True),
+    "S_C1": _S("C1", 10530, 64, 6, 1, 1, 8, 1, False),
+    "S_C1@128x3": _S("C1", 10530, 128, 3, 1, 1, 8, 1, False),
+    "S_C2": _S("C2", 10530, 128, 3, 2, 2, 16, 0, False),
+    "S_C2@64x6": _S("C2", 10530, 64, 6, 2, 2, 16, 0, False),
+    "S_C3": _S("C3", 10530 * 4, 64, 3, 1, 1, 16, 0, True),
+    "S_C4_4725_tok": _S("C4_4725_tok", 4725, 64, 6, 1, 1, 8, 1, False, 1),
+    "S_C4_4725_tok@no-weight": _S("C4_4725_tok", 4725, 64, 6, 1, 1, 8, 1, False),
+    "S_C4_4725_tok@128x3": _S("C4_4725_tok", 4725, 128, 3, 1, 1, 8, 1, False),
+    "S_C4_4725_blk": _S("C4_4725_blk", 4725, 64, 6, 1, 1, 8, 24, False, 1),
+    "S_C4_4725_blk@no-weight": _S("C4_4725_blk", 4725, 64, 6, 1, 1, 8, 24, False),
+    "S_C4_10530_tok": _S("C4_10530_tok", 10530, 64, 6, 1, 1, 8, 1, False, 1),
+    "S_C4_10530_tok@no-weight": _S("C4_10530_tok", 10530, 64, 6, 1, 1, 8, 1, False),
+    "S_C4_10530_blk": _S("C4_10530_blk", 10530, 64, 6, 1, 1, 8, 24, False, 1),
+    "S_C4_10530_blk@no-weight": _S("C4_10530_blk", 10530, 64, 6, 1, 1, 8, 24, False),
+    "S_R_q4k": _S("R_q4k", 3120, 128, 4, 1, 1, 8, 1, False),
+    "S_R_q4k@64x8": _S("R_q4k", 3120, 64, 8, 1, 1, 8, 1, False),
+    "S_R_q16k": _S("R_q16k", 3120, 256, 8, 1, 1, 8, 1, False),
+    "S_R_rms": _S("R_rms", 99840, 16, 1, 1, 1, 16, 0, False, 1),
+    "S_R_rms@no-weight": _S("R_rms", 99840, 16, 1, 1, 1, 16, 0, False),
+    # K slice of the packed qkv [1, 3120, 3, 32, 128]: 32 head rows of 256 B
+    # per token, tokens 24576 B apart, starting 8192 B into the buffer
+    "S_R_kn": _S("R_kn", 99840, 16, 1, 1, 1, 16, 0, False, 1, 32, 24576, 8192),
+    "S_R_kn@contiguous": _S("R_kn", 99840, 16, 1, 1, 1, 16, 0, False, 1),
+    "S_R_ln": _S("R_ln", 3120, 256, 2, 3, 1, 16, 0, False),
+    "S_R_ln@64x8": _S("R_ln", 3120, 64, 8, 3, 1, 16, 0, False),
+    "S_R_qk": _S("R_qk", 3120 * 8, 64, 2, 1, 1, 16, 0, True),
+    "S_T_rms": _S("T_rms", 4096, 64, 8, 1, 1, 16, 0, False, 1),
+    "S_T_rms@no-weight": _S("T_rms", 4096, 64, 8, 1, 1, 16, 0, False),
+    "S_T_ln": _S("T_ln", 4096, 256, 2, 3, 1, 16, 0, False),
+    "S_T_qk": _S("T_qk", 1560 * 8, 64, 2, 1, 1, 16, 0, True),
 }
 
 _STREAM_LIB = None
@@ -252,47 +272,67 @@ def stream_lib():
         path = ROOT / "joyai-video-edit_amd" / "joyomni_ops" / "libjoyomni_stream.so"
         lib = ctypes.CDLL(str(path))
         P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
-        lib.jo_stream_rows.argtypes = [P, P, P, P, P, P, I64, I, I, I, I, I, I, P]
+        lib.jo_stream_rows.argtypes = [P, P, P, P, P, P, I64, I, I, I, I, I, I, I, I64, I64, P]
         lib.jo_stream_rows.restype = I
         _STREAM_LIB = lib
     return _STREAM_LIB
 
 
 def stream_bytes(spec) -> int:
-    _, rows, lpr, ch, nin, nout, outb, nscal, _ = spec
-    return rows * (nin * lpr * ch * 16 + nout * lpr * ch * outb + nscal * 4)
+    """Bytes a stream moves per call: its rows in and out, the per-row
+    scalars, and each row-invariant input once (as the kernels' algorithmic
+    bytes count their weight row)."""
+    row_in, row_out = spec.lpr * spec.ch * 16, spec.lpr * spec.ch * spec.outb
+    return (spec.rows * (spec.nin * row_in + spec.nout * row_out + spec.nscal * 4)
+            + spec.nconst * row_in)
 
 
 def time_stream(spec, steps: int, warmup: int, dev) -> dict:
     import torch
-    _, rows, lpr, ch, nin, nout, outb, nscal, inplace = spec
-    rin, rout = rows * lpr * ch * 16, rows * lpr * ch * outb
-    set_bytes = stream_bytes(spec)
+    row_in = spec.lpr * spec.ch * 16
+    if spec.group:
+        rin = spec.goff + (spec.rows // spec.group) * spec.gstride
+    else:
+        rin = spec.rows * row_in
+    rout = spec.rows * spec.lpr * spec.ch * spec.outb
+    set_bytes = (spec.nin * rin + (0 if spec.inplace else spec.nout * rout)
+                 + spec.nconst * row_in + spec.rows * spec.nscal * 4)
     n_sets = max(4, math.ceil(ROT_BYTES / set_bytes))
     sets = []
     for _ in range(n_sets):
-        ins = [torch.randint(0, 255, (rin,), dtype=torch.uint8, device=dev) for _ in range(nin)]
-        outs = ins[:1] if inplace else [torch.empty(rout, dtype=torch.uint8, device=dev)
-                                        for _ in range(nout)]
-        scal = torch.empty(max(1, rows * nscal), dtype=torch.float32, device=dev)
-        sets.append((ins, outs, scal))
+        ins = [torch.randint(0, 255, (rin,), dtype=torch.uint8, device=dev)
+               for _ in range(spec.nin)]
+        consts = [torch.randint(0, 255, (row_in,), dtype=torch.uint8, device=dev)
+                  for _ in range(spec.nconst)]
+        outs = ins[:1] if spec.inplace else [torch.empty(rout, dtype=torch.uint8, device=dev)
+                                             for _ in range(spec.nout)]
+        scal = torch.empty(max(1, spec.rows * spec.nscal), dtype=torch.float32, device=dev)
+        sets.append((ins, consts, outs, scal))
     lib = stream_lib()
 
     def launch(i, h):
-        ins, outs, scal = sets[i % n_sets]
-        p = [t.data_ptr() for t in ins] + [None] * (3 - len(ins))
+        ins, consts, outs, scal = sets[i % n_sets]
+        p = [t.data_ptr() + spec.goff for t in ins] + [t.data_ptr() for t in consts]
+        p += [None] * (3 - len(p))
         o = [t.data_ptr() for t in outs] + [None] * (2 - len(outs))
-        rc = lib.jo_stream_rows(p[0], p[1], p[2], o[0], o[1], scal.data_ptr() if nscal else None,
-                                rows, lpr, ch, nin, nout, outb, nscal, h)
+        rc = lib.jo_stream_rows(p[0], p[1], p[2], o[0], o[1],
+                                scal.data_ptr() if spec.nscal else None, spec.rows, spec.lpr,
+                                spec.ch, spec.nin, spec.nout, spec.outb, spec.nscal, spec.nconst,
+                                spec.group, spec.gstride, h)
         if rc != 0:
             raise RuntimeError(f"jo_stream_rows failed ({rc}) for {spec}")
 
     res = time_launches(launch, n_sets, steps, warmup, dev)
     del sets
     torch.cuda.empty_cache()
-    out = _finish(res, set_bytes, n_sets, set_bytes)
-    out.update(shape=f"{rows} rows, {lpr} lanes x {ch} chunks, {nin} in / {nout} out",
-               kind="stream-ceiling")
+    out = _finish(res, stream_bytes(spec), n_sets, set_bytes)
+    shape = (f"{spec.rows} rows, {spec.lpr} lanes x {spec.ch} chunks, "
+             f"{spec.nin} in / {spec.nout} out")
+    if spec.nconst:
+        shape += f", {spec.nconst} cached weight row read per row"
+    if spec.group:
+        shape += f", rows in groups of {spec.group} every {spec.gstride} B"
+    out.update(shape=shape, kind="stream-ceiling")
     return out
 
 
@@ -594,7 +634,7 @@ def main() -> int:
         for c in W.CONFIGS:
             names.append(c)
             if not args.no_streams:
-                names += [sn for sn, spec in STREAMS.items() if spec[0] == c]
+                names += [sn for sn, spec in STREAMS.items() if spec.cfg == c]
     if HEADLINE not in names:
         names.insert(0, HEADLINE)
     results = {}
@@ -633,7 +673,7 @@ def main() -> int:
 
     # Each config's stream ceiling: its kernel's own shape, and the fastest shape.
     for sname, spec in STREAMS.items():
-        cname = spec[0]
+        cname = spec.cfg
         if sname not in results or cname not in results:
             continue
         r, s_us = results[cname], results[sname]["us_per_call"]

@@ -11,9 +11,14 @@
 // lane, and rows that span several waves meet at a workgroup barrier, as the
 // kernels' cross-wave reductions do.
 //
-// Row r of input stream t starts at in[t] + r * LPR*CH*16 bytes, row r of
-// output stream o at out[o] + r * LPR*CH*OUTB bytes; with in[0] == out[0] and
-// OUTB == 16 the stream is in place (the QK kernels' layout).
+// Row r of input stream t starts at in[t] + r * LPR*CH*16 bytes (or, for
+// input rows that come in groups of G contiguous rows GS bytes apart — the
+// per-head rows of a strided [T, H, D] view — at in[t] + (r / G) * GS +
+// (r % G) * LPR*CH*16), row r of output stream o at out[o] + r * LPR*CH*OUTB
+// bytes; with in[0] == out[0] and OUTB == 16 the stream is in place (the QK
+// kernels' layout). NCONST row-invariant inputs (a weight row every row is
+// multiplied by, read through the cache by every row as the kernels do) follow
+// the row inputs in in[].
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -29,26 +34,42 @@ struct StreamArgs {
   char* out[2];
   float* scal;       // nscal fp32 per row, or null
   int64_t rows;
+  uint32_t group_rows;    // input rows per contiguous group (0: all rows contiguous)
+  int64_t group_stride;   // bytes between groups
   int nscal;
   uint32_t mask;     // 0 at run time; keeps the dependency opaque to the compiler
 };
 
-template <int LPR, int CH, int NIN, int NOUT, int OUTB>
+template <int LPR, int CH, int NIN, int NOUT, int OUTB, int NCONST>
 __global__ __launch_bounds__(256) void stream_rows_kernel(const StreamArgs a) {
+  static_assert(NIN + NCONST <= 3, "three input streams");
   constexpr int RPB = 256 / LPR;
   constexpr int64_t kIn = int64_t(LPR) * CH * 16;
   constexpr int64_t kOut = int64_t(LPR) * CH * OUTB;
   const int lane = threadIdx.x % LPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
   const bool ok = row < a.rows;
+  u32x4 w[NCONST > 0 ? NCONST : 1][CH];
+#pragma unroll
+  for (int t = 0; t < NCONST; ++t)
+#pragma unroll
+    for (int i = 0; i < CH; ++i) w[t][i] = jo::ld16(a.in[NIN + t] + (i * LPR + lane) * 16);
+  int64_t ro = row * kIn;
+  if (a.group_rows) {
+    const uint32_t g = static_cast<uint32_t>(row) / a.group_rows;
+    ro = static_cast<int64_t>(g) * a.group_stride + (row - int64_t{g} * a.group_rows) * kIn;
+  }
   u32x4 c[NIN][CH];
 #pragma unroll
   for (int t = 0; t < NIN; ++t)
 #pragma unroll
     for (int i = 0; i < CH; ++i)
-      c[t][i] = ok ? jo::ld16_nt(a.in[t] + row * kIn + (i * LPR + lane) * 16)
-                   : u32x4{0u, 0u, 0u, 0u};
+      c[t][i] = ok ? jo::ld16_nt(a.in[t] + ro + (i * LPR + lane) * 16) : u32x4{0u, 0u, 0u, 0u};
   uint32_t x = 0;
+#pragma unroll
+  for (int t = 0; t < NCONST; ++t)
+#pragma unroll
+    for (int i = 0; i < CH; ++i) x ^= w[t][i].x ^ w[t][i].y ^ w[t][i].z ^ w[t][i].w;
 #pragma unroll
   for (int t = 0; t < NIN; ++t)
 #pragma unroll
@@ -72,12 +93,13 @@ __global__ __launch_bounds__(256) void stream_rows_kernel(const StreamArgs a) {
   if (a.scal && lane < a.nscal) a.scal[row * a.nscal + lane] = static_cast<float>(x & 0xffu);
 }
 
-template <int LPR, int CH, int NIN, int NOUT, int OUTB>
-bool try_launch(int lpr, int ch, int nin, int nout, int outb, const StreamArgs& a,
+template <int LPR, int CH, int NIN, int NOUT, int OUTB, int NCONST = 0>
+bool try_launch(int lpr, int ch, int nin, int nout, int outb, int nconst, const StreamArgs& a,
                 hipStream_t st) {
-  if (lpr != LPR || ch != CH || nin != NIN || nout != NOUT || outb != OUTB) return false;
+  if (lpr != LPR || ch != CH || nin != NIN || nout != NOUT || outb != OUTB || nconst != NCONST)
+    return false;
   constexpr int RPB = 256 / LPR;
-  hipLaunchKernelGGL((stream_rows_kernel<LPR, CH, NIN, NOUT, OUTB>),
+  hipLaunchKernelGGL((stream_rows_kernel<LPR, CH, NIN, NOUT, OUTB, NCONST>),
                      dim3(static_cast<unsigned>((a.rows + RPB - 1) / RPB)), dim3(256), 0, st, a);
   return true;
 }
@@ -85,40 +107,50 @@ bool try_launch(int lpr, int ch, int nin, int nout, int outb, const StreamArgs& 
 }  // namespace
 
 // Shapes measured by bench.py: (lanes per row, chunks per lane, input
-// streams, output streams, bytes stored per 16 bytes read). Returns 0 on
-// success, 1 for a shape that is not instantiated, 3 for a launch error.
+// streams, output streams, bytes stored per 16 bytes read, row-invariant
+// inputs). Returns 0 on success, 1 for a shape that is not instantiated or
+// bad sizes, 3 for a launch error.
 extern "C" int jo_stream_rows(const void* in0, const void* in1, const void* in2, void* out0,
                               void* out1, float* scal, int64_t rows, int lpr, int ch, int nin,
-                              int nout, int outb, int nscal, void* stream) {
+                              int nout, int outb, int nscal, int nconst, int64_t group_rows,
+                              int64_t group_stride, void* stream) {
   if (rows <= 0 || rows > (int64_t{1} << 30)) return 1;
+  if (group_rows < 0 || group_rows > (int64_t{1} << 30) || (group_rows && group_stride <= 0))
+    return 1;
   StreamArgs a{{static_cast<const char*>(in0), static_cast<const char*>(in1),
                 static_cast<const char*>(in2)},
                {static_cast<char*>(out0), static_cast<char*>(out1)},
-               scal, rows, nscal, 0u};
+               scal, rows, static_cast<uint32_t>(group_rows), group_stride, nscal, 0u};
   hipStream_t st = static_cast<hipStream_t>(stream);
+#define TRY(...) try_launch<__VA_ARGS__>(lpr, ch, nin, nout, outb, nconst, a, st)
   const bool done =
       // QK units: 1, 2 or 3 head groups of 512 elements per wave, in place or to a cache
-      try_launch<64, 1, 1, 1, 16>(lpr, ch, nin, nout, outb, a, st) ||
-      try_launch<64, 2, 1, 1, 16>(lpr, ch, nin, nout, outb, a, st) ||
-      try_launch<64, 3, 1, 1, 16>(lpr, ch, nin, nout, outb, a, st) ||
-      try_launch<64, 4, 1, 1, 16>(lpr, ch, nin, nout, outb, a, st) ||
+      TRY(64, 1, 1, 1, 16) ||
+      TRY(64, 2, 1, 1, 16) ||
+      TRY(64, 3, 1, 1, 16) ||
+      TRY(64, 4, 1, 1, 16) ||
       // bf16 rows -> fp8 rows (+ scales): hidden 3072 / 4096 / 16384
-      try_launch<64, 6, 1, 1, 8>(lpr, ch, nin, nout, outb, a, st) ||
-      try_launch<128, 3, 1, 1, 8>(lpr, ch, nin, nout, outb, a, st) ||
-      try_launch<256, 2, 1, 1, 8>(lpr, ch, nin, nout, outb, a, st) ||
-      try_launch<128, 4, 1, 1, 8>(lpr, ch, nin, nout, outb, a, st) ||
-      try_launch<64, 8, 1, 1, 8>(lpr, ch, nin, nout, outb, a, st) ||
-      try_launch<256, 8, 1, 1, 8>(lpr, ch, nin, nout, outb, a, st) ||
+      TRY(64, 6, 1, 1, 8) ||
+      TRY(128, 3, 1, 1, 8) ||
+      TRY(256, 2, 1, 1, 8) ||
+      TRY(128, 4, 1, 1, 8) ||
+      TRY(64, 8, 1, 1, 8) ||
+      TRY(256, 8, 1, 1, 8) ||
       // two rows in, two rows out (residual add + norm): hidden 3072
-      try_launch<128, 3, 2, 2, 16>(lpr, ch, nin, nout, outb, a, st) ||
-      try_launch<64, 6, 2, 2, 16>(lpr, ch, nin, nout, outb, a, st) ||
-      try_launch<256, 2, 2, 2, 16>(lpr, ch, nin, nout, outb, a, st) ||
+      TRY(128, 3, 2, 2, 16) ||
+      TRY(64, 6, 2, 2, 16) ||
+      TRY(256, 2, 2, 2, 16) ||
       // three rows in (x, scale, shift), one out: hidden 4096
-      try_launch<256, 2, 3, 1, 16>(lpr, ch, nin, nout, outb, a, st) ||
-      try_launch<64, 8, 3, 1, 16>(lpr, ch, nin, nout, outb, a, st) ||
+      TRY(256, 2, 3, 1, 16) ||
+      TRY(64, 8, 3, 1, 16) ||
       // one row in, one out, 16 bytes each: rmsnorm rows of 128 and 4096
-      try_launch<16, 1, 1, 1, 16>(lpr, ch, nin, nout, outb, a, st) ||
-      try_launch<64, 8, 1, 1, 16>(lpr, ch, nin, nout, outb, a, st);
+      TRY(16, 1, 1, 1, 16) ||
+      TRY(64, 8, 1, 1, 16) ||
+      // the same with the row-invariant weight row the kernels read per row
+      TRY(64, 6, 1, 1, 8, 1) ||    // RMSNorm -> FP8, hidden 3072
+      TRY(16, 1, 1, 1, 16, 1) ||   // rmsnorm rows of 128 (also per-head rows of a strided view)
+      TRY(64, 8, 1, 1, 16, 1);     // rmsnorm rows of 4096
+#undef TRY
   if (!done) return 1;
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }

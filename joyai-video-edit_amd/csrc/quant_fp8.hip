@@ -143,20 +143,58 @@ constexpr int kC4WavesPerSimd = 5;
 // Weight chunks first (cached: they arrive before the row), then the row's.
 // A row past M reads row M - 1 and a lane past N reads chunk 0 of its row;
 // their values are cleared (EXACT == false) and never stored.
-template <class Tag, int LPR, int CH, bool EXACT>
+//
+// SHARED (one row per wave): the workgroup's four waves share one copy of
+// the weight row through LDS, each loading a quarter of its chunks, which cuts
+// the weight traffic through L2 fourfold ([4725, 3072] per 1x128 block:
+// 10.2 -> 9.9 us on MI355X). The meeting point is a bare s_barrier behind an
+// LDS-only wait: a fenced barrier would also wait for the row loads in flight.
+template <class Tag, int LPR, int CH, bool EXACT, bool SHARED>
 __device__ __forceinline__ void load_row_weight(const void* x, int64_t xs, const void* w,
                                                 int64_t row, int lane, int N, u32x4 (&c)[CH],
                                                 u32x4 (&wc)[CH]) {
   const void* xr = byte_off(x, row * xs * Tag::kBytes);
+  if constexpr (SHARED) {
+    static_assert(LPR == kWave, "one row per wave");
+    constexpr int kWaves = kBlock / kWave;
+    constexpr int kMine = (CH + kWaves - 1) / kWaves;
+    __shared__ u32x4 wl[CH * LPR];
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+    u32x4 wt[kMine];
 #pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const int e = (i * LPR + lane) * 8;
-    wc[i] = ld16(byte_off(w, static_cast<int64_t>((EXACT || e < N) ? e : 0) * Tag::kBytes));
-  }
+    for (int k = 0; k < kMine; ++k) {
+      const int i = wave + kWaves * k;
+      const int e = (i * LPR + lane) * 8;
+      if (i < CH)
+        wt[k] = ld16(byte_off(w, static_cast<int64_t>((EXACT || e < N) ? e : 0) * Tag::kBytes));
+    }
 #pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const int e = (i * LPR + lane) * 8;
-    c[i] = ld16_nt(byte_off(xr, static_cast<int64_t>((EXACT || e < N) ? e : 0) * Tag::kBytes));
+    for (int i = 0; i < CH; ++i) {
+      const int e = (i * LPR + lane) * 8;
+      c[i] = ld16_nt(byte_off(xr, static_cast<int64_t>((EXACT || e < N) ? e : 0) * Tag::kBytes));
+    }
+#pragma unroll
+    for (int k = 0; k < kMine; ++k) {
+      const int i = wave + kWaves * k;
+      if (i < CH) wl[i * LPR + lane] = wt[k];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < CH; ++i) wc[i] = wl[i * LPR + lane];
+  } else {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int e = (i * LPR + lane) * 8;
+      wc[i] = ld16(byte_off(w, static_cast<int64_t>((EXACT || e < N) ? e : 0) * Tag::kBytes));
+    }
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int e = (i * LPR + lane) * 8;
+      c[i] = ld16_nt(byte_off(xr, static_cast<int64_t>((EXACT || e < N) ? e : 0) * Tag::kBytes));
+    }
   }
   if constexpr (!EXACT) {
 #pragma unroll
@@ -232,7 +270,7 @@ void rmsnorm_quant_tok_kernel(
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
   const bool row_ok = row < M;
   u32x4 c[CH], wc[CH];
-  load_row_weight<Tag, LPR, CH, EXACT>(x, xs, w, row_ok ? row : M - 1, lane, N, c, wc);
+  load_row_weight<Tag, LPR, CH, EXACT, false>(x, xs, w, row_ok ? row : M - 1, lane, N, c, wc);
   float xf[KEEPX ? CH : 1][8];
   const float r =
       rms_rstd(row_reduce_sum64<LPR>(lane_sum_squares<Tag, CH, KEEPX>(c, xf), red_ss), N, eps);
@@ -273,7 +311,7 @@ void rmsnorm_quant_tok_kernel(
 // Per 1x128 block: each 16-lane DPP row of a chunk holds one block. Same
 // fast / exact paths as per token, decided per block; the vote for the
 // NaN-skipping maxima is wave-wide (workgroup-wide for rows wider than a wave).
-template <class Tag, int LPR, int CH, bool EXACT, bool KEEPX>
+template <class Tag, int LPR, int CH, bool EXACT, bool KEEPX, bool SHARED>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kC4WavesPerSimd)))
 void rmsnorm_quant_blk_kernel(
     const void* __restrict__ x, int64_t xs, const void* __restrict__ w, uint8_t* __restrict__ q,
@@ -285,7 +323,7 @@ void rmsnorm_quant_blk_kernel(
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
   const bool row_ok = row < M;
   u32x4 c[CH], wc[CH];
-  load_row_weight<Tag, LPR, CH, EXACT>(x, xs, w, row_ok ? row : M - 1, lane, N, c, wc);
+  load_row_weight<Tag, LPR, CH, EXACT, SHARED>(x, xs, w, row_ok ? row : M - 1, lane, N, c, wc);
   float xf[KEEPX ? CH : 1][8];
   const float r =
       rms_rstd(row_reduce_sum64<LPR>(lane_sum_squares<Tag, CH, KEEPX>(c, xf), red_ss), N, eps);
@@ -362,7 +400,10 @@ void rmsnorm_quant_blk_kernel(
 // kernels): per token, fewer rows than wave slots keeps 74 registers so all
 // rows are resident in one round (T = 4725: 10.3 -> 9.7 us), more rows keeps
 // x in fp32 (T = 10530: 18.5 -> 17.8 us); per block (T = 10530: 19.7 -> 18.6
-// us, T = 4725 level).
+// us), and with fewer rows than wave slots the weight row is shared through
+// LDS (T = 4725: 10.2 -> 9.9 us; per token and with more rows it measured no
+// gain). Two or three rows per wave, each row's arithmetic overlapping the
+// next row's arrival, measured slower (T = 4725 per token 9.6 -> 10.4 us).
 template <class Tag>
 int launch_rmsnorm_quant(const void* x, int64_t xs, const void* w, void* q, int64_t qs, float* s,
                          int64_t M, int64_t N, float eps, int64_t group, hipStream_t stream) {
@@ -399,17 +440,17 @@ int launch_rmsnorm_quant(const void* x, int64_t xs, const void* w, void* q, int6
       const bool exact = int64_t{LPR} * CH * 8 == N;
       if (M >= kFewRows) {
         if (exact)
-          hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, true, true>), grid,
+          hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, true, true, false>), grid,
                              dim3(kBlock), 0, stream, x, xs, w, q8, qs, s, M, n, eps);
         else
-          hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, false, true>), grid,
+          hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, false, true, false>), grid,
                              dim3(kBlock), 0, stream, x, xs, w, q8, qs, s, M, n, eps);
       } else {
         if (exact)
-          hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, true, false>), grid,
+          hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, true, false, LPR == kWave>), grid,
                              dim3(kBlock), 0, stream, x, xs, w, q8, qs, s, M, n, eps);
         else
-          hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, false, false>), grid,
+          hipLaunchKernelGGL((rmsnorm_quant_blk_kernel<Tag, LPR, CH, false, false, LPR == kWave>), grid,
                              dim3(kBlock), 0, stream, x, xs, w, q8, qs, s, M, n, eps);
       }
     });
