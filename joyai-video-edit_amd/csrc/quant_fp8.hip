@@ -387,12 +387,25 @@ void rmsnorm_quant_blk_kernel(
     }
   }
   if (!row_ok) return;
+  // One wave-uniform branch when every block of the wave takes the clamp-free
+  // path (a per-block select would run both conversions).
+  bool lane_fast = true;
 #pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const int e = (i * LPR + lane) * 8;
-    if (EXACT || e < N)
-      st8_nt(q + row * qs + e, (fast[i] && finite_bits(ginv[i])) ? quant8<false>(v[i], ginv[i])
-                                                                : quant8<true>(v[i], ginv[i]));
+  for (int i = 0; i < CH; ++i) lane_fast = lane_fast && fast[i] && finite_bits(ginv[i]);
+  if (__builtin_amdgcn_ballot_w64(!lane_fast) == 0) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int e = (i * LPR + lane) * 8;
+      if (EXACT || e < N) st8_nt(q + row * qs + e, quant8<false>(v[i], ginv[i]));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int e = (i * LPR + lane) * 8;
+      if (EXACT || e < N)
+        st8_nt(q + row * qs + e, (fast[i] && finite_bits(ginv[i])) ? quant8<false>(v[i], ginv[i])
+                                                                  : quant8<true>(v[i], ginv[i]));
+    }
   }
 }
 
