@@ -1,0 +1,95 @@
+"""CPU tests of bench.py's measurement tables: every stream ceiling (S_*) line
+names a real config, uses a launch shape that csrc/bench/stream_ceiling.hip
+instantiates, and — for the line that stands for a kernel's own access shape —
+moves the config's algorithmic bytes; the stream library loads and rejects bad
+sizes without touching a GPU."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+STREAM_SRC = ROOT / "joyai-video-edit_amd" / "csrc" / "bench" / "stream_ceiling.hip"
+
+
+@pytest.fixture(scope="module")
+def bench():
+    import bench as b
+    return b
+
+
+def instantiated_shapes() -> set[tuple[int, ...]]:
+    """(lpr, ch, nin, nout, outb, nconst) of every TRY(...) in the dispatch list."""
+    shapes = set()
+    for m in re.finditer(r"TRY\(([\d,\s]+)\)", STREAM_SRC.read_text()):
+        v = [int(t) for t in m.group(1).split(",")]
+        shapes.add(tuple(v + [0] * (6 - len(v))))
+    return shapes
+
+
+def test_stream_shapes_are_instantiated(bench):
+    shapes = instantiated_shapes()
+    assert shapes, "no TRY(...) lines found"
+    for name, s in bench.STREAMS.items():
+        key = (s.lpr, s.ch, s.nin, s.nout, s.outb, s.nconst)
+        assert key in shapes, f"{name}: shape {key} is not instantiated in {STREAM_SRC.name}"
+        assert s.nin + s.nconst <= 3 and s.nout <= 2, name
+        assert not (s.inplace and s.nout != 1), name
+
+
+def test_streams_name_configs_and_one_own_shape(bench):
+    from joyomni_ops import workloads as W
+    own = {}
+    for name, s in bench.STREAMS.items():
+        assert s.cfg in W.CONFIGS, name
+        assert name.startswith("S_" + s.cfg), name
+        if "@" not in name:
+            assert s.cfg not in own, f"{s.cfg} has two own-shape streams"
+            own[s.cfg] = name
+    for cfg in ("C0", "C1", "C2", "C3", "C4_4725_tok", "C4_4725_blk", "C4_10530_tok",
+                "C4_10530_blk"):
+        assert cfg in own, f"BASELINE config {cfg} has no stream ceiling"
+
+
+def test_own_shape_streams_move_the_config_bytes(bench):
+    """The S_<cfg> line moves the config's algorithmic bytes: exactly for the
+    row ops (rows, scales and the weight row once), within 1% where the kernel
+    also reads small per-token tables (QK: rotation tables, weights)."""
+    from joyomni_ops import workloads as W
+    for name, s in bench.STREAMS.items():
+        if "@" in name:
+            continue
+        alg = W.algorithmic_bytes(W.CONFIGS[s.cfg])
+        got = bench.stream_bytes(s)
+        if s.cfg.startswith("C4") or s.cfg in ("C1", "R_q4k", "R_q16k", "R_rms", "R_kn", "T_rms"):
+            assert got == alg, (name, got, alg)
+        else:
+            assert abs(got - alg) <= 0.01 * alg, (name, got, alg)
+
+
+def test_grouped_stream_covers_the_strided_view(bench):
+    """S_R_kn reads the K slice of a packed [1, 3120, 3, 32, 128] bf16 qkv: 32
+    head rows of 256 bytes per token, tokens 3 * 32 * 128 * 2 bytes apart,
+    starting one q slice (32 * 128 * 2 bytes) in."""
+    s = bench.STREAMS["S_R_kn"]
+    assert (s.group, s.gstride, s.goff) == (32, 3 * 32 * 128 * 2, 32 * 128 * 2)
+    assert s.rows == 3120 * 32 and s.lpr * s.ch * 16 == 128 * 2
+
+
+def test_stream_library_rejects_bad_sizes_without_a_gpu(bench):
+    path = ROOT / "joyai-video-edit_amd" / "joyomni_ops" / "libjoyomni_stream.so"
+    if not path.exists():
+        pytest.skip("stream library not built (python joyai-video-edit_amd/build.py)")
+    import torch  # noqa: F401  (shares torch's HIP runtime, as bench.py does)
+    lib = bench.stream_lib()
+    null = None
+    # rows <= 0, a group with no stride, and a shape that is not instantiated
+    assert lib.jo_stream_rows(null, null, null, null, null, null, 0, 64, 6, 1, 1, 8, 1, 0, 0, 0,
+                              null) == 1
+    assert lib.jo_stream_rows(null, null, null, null, null, null, 10, 16, 1, 1, 1, 16, 0, 1, 32,
+                              0, null) == 1
+    assert lib.jo_stream_rows(null, null, null, null, null, null, 10, 64, 5, 1, 1, 8, 1, 0, 0, 0,
+                              null) == 1
