@@ -25,6 +25,15 @@ constexpr int kWave = 64;
 constexpr int kBlock = 256;  // threads per workgroup for every row kernel
 constexpr float kFp8Max = 448.0f;
 
+// x / n for a row length n > 0, rounded as the IEEE division: when n is a
+// power of two the quotient is x scaled by an exact 2^-k, one rounding either
+// way (the branch is uniform: n is a kernel argument).
+__device__ __forceinline__ float div_by_len(float x, int n) {
+  if (n > 0 && (n & (n - 1)) == 0)
+    return x * __builtin_bit_cast(float, static_cast<uint32_t>(127 - __builtin_ctz(n)) << 23);
+  return x / static_cast<float>(n);
+}
+
 // ---------------------------------------------------------------------------
 // Element types. kVec = elements carried by one 16-byte chunk.
 // ---------------------------------------------------------------------------

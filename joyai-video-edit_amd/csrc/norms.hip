@@ -159,11 +159,10 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
     }
   }
   sum = row_reduce<LPR, OpSum>(sum, red_a);
-  const float nf = static_cast<float>(N);
   float mean = 0.f;
   float r;
   if constexpr (NT == kLayer) {
-    mean = sum / nf;
+    mean = div_by_len(sum, N);
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
@@ -177,9 +176,9 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
       }
     }
     ss = row_reduce<LPR, OpSum>(ss, red_b);
-    r = 1.0f / sqrtf(ss / nf + a.eps);
+    r = 1.0f / sqrtf(div_by_len(ss, N) + a.eps);
   } else {
-    r = 1.0f / sqrtf(sum / nf + a.eps);
+    r = 1.0f / sqrtf(div_by_len(sum, N) + a.eps);
   }
 
   // Output.
@@ -283,19 +282,18 @@ __global__ __launch_bounds__(kBlock) void norm_mod_generic_kernel(const NormArgs
     sum += (NT == kLayer) ? v : v * v;
   }
   sum = block_reduce<OpSum>(sum, red);
-  const float nf = static_cast<float>(N);
   float mean = 0.f, r;
   if constexpr (NT == kLayer) {
-    mean = sum / nf;
+    mean = div_by_len(sum, N);
     float ss = 0.f;
     for (int i = threadIdx.x; i < N; i += kBlock) {
       const float t = load_elem<Tag>(src, so_src + i) - mean;
       ss += t * t;
     }
     ss = block_reduce<OpSum>(ss, red);
-    r = 1.0f / sqrtf(ss / nf + a.eps);
+    r = 1.0f / sqrtf(div_by_len(ss, N) + a.eps);
   } else {
-    r = 1.0f / sqrtf(sum / nf + a.eps);
+    r = 1.0f / sqrtf(div_by_len(sum, N) + a.eps);
   }
   const bool affine = a.gamma != nullptr;
   const bool has_beta = affine && a.beta != nullptr && NT == kLayer;
@@ -464,7 +462,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const RmsArgs a) {
       }
     }
     ss = row_reduce<LPR, OpSum>(ss, red);
-    ms = ss / static_cast<float>(N);
+    ms = div_by_len(ss, N);
   }
   const float r = 1.0f / sqrtf(ms + a.eps);
 #pragma unroll
@@ -505,7 +503,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_generic_kernel(const RmsArgs a
       ss += v * v;
     }
     ss = block_reduce<OpSum>(ss, red);
-    ms = ss / static_cast<float>(a.N);
+    ms = div_by_len(ss, a.N);
   }
   const float r = 1.0f / sqrtf(ms + a.eps);
   for (int i = threadIdx.x; i < a.N; i += kBlock) {
