@@ -213,17 +213,19 @@ def time_gpu(cfg, steps: int, warmup: int, dev, use_graph: bool = True) -> dict:
 # ---------------------------------------------------------------------------
 # Stream ceilings. Each entry: the config it bounds, rows, lanes per row,
 # chunks per lane, input streams, output streams, bytes stored per 16 read,
-# fp32 scalars per row, in place, row-invariant inputs (the weight row a
-# kernel reads, through the cache, for every row), and for input rows that
-# come in groups (per-head rows of a strided view) the rows per group, the
-# bytes between groups and the offset of the first row. The entry named
-# S_<cfg> is the kernel's own access shape; entries named S_<cfg>@<what> are
-# other shapes of the same bytes (@LPRxCH) or the shape without the cached
-# weight reads (@no-weight) or without the stride (@contiguous).
+# fp32 scalars per row, in place, row-invariant inputs (the weight or
+# modulation rows a kernel reads, through the cache, for every row), for input
+# rows that come in groups (per-head rows of a strided view) the rows per
+# group, the bytes between groups and the offset of the first row, and an
+# extra output of 8 bytes per 16 read (an fp8 row next to a bf16 one). The
+# entry named S_<cfg> is the kernel's own access shape; entries named
+# S_<cfg>@<what> are other shapes of the same bytes (@LPRxCH) or the shape
+# without the cached row reads (@no-weight, @no-mod) or without the stride
+# (@contiguous).
 # ---------------------------------------------------------------------------
 Stream = collections.namedtuple(
-    "Stream", "cfg rows lpr ch nin nout outb nscal inplace nconst group gstride goff",
-    defaults=(0, 0, 0, 0))
+    "Stream", "cfg rows lpr ch nin nout outb nscal inplace nconst group gstride goff out8",
+    defaults=(0, 0, 0, 0, 0))
 
 _S = Stream
 STREAMS = {
@@ -232,9 +234,13 @@ STREAMS = {
     "S_C0@64x2": _S("C0", 3510 * 6, 64, 2, 1, 1, 16, 0, True),
     "S_C1": _S("C1", 10530, 64, 6, 1, 1, 8, 1, False),
     "S_C1@128x3": _S("C1", 10530, 128, 3, 1, 1, 8, 1, False),
-    "S_C2": _S("C2", 10530, 128, 3, 2, 2, 16, 0, False),
+    "S_C2": _S("C2", 10530, 128, 3, 2, 2, 16, 0, False, 2),
+    "S_C2@no-mod": _S("C2", 10530, 128, 3, 2, 2, 16, 0, False),
     "S_C2@64x6": _S("C2", 10530, 64, 6, 2, 2, 16, 0, False),
     "S_C3": _S("C3", 10530 * 4, 64, 3, 1, 1, 16, 0, True),
+    # x and residual in; residual and the fp8 row out, one scale per row;
+    # broadcast gate, scale and shift rows
+    "S_N3": _S("N3", 10530, 128, 3, 2, 1, 16, 1, False, 3, out8=1),
     "S_C4_4725_tok": _S("C4_4725_tok", 4725, 64, 6, 1, 1, 8, 1, False, 1),
     "S_C4_4725_tok@no-weight": _S("C4_4725_tok", 4725, 64, 6, 1, 1, 8, 1, False),
     "S_C4_4725_tok@128x3": _S("C4_4725_tok", 4725, 128, 3, 1, 1, 8, 1, False),
@@ -272,7 +278,7 @@ def stream_lib():
         path = ROOT / "joyai-video-edit_amd" / "joyomni_ops" / "libjoyomni_stream.so"
         lib = ctypes.CDLL(str(path))
         P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
-        lib.jo_stream_rows.argtypes = [P, P, P, P, P, P, I64, I, I, I, I, I, I, I, I64, I64, P]
+        lib.jo_stream_rows.argtypes = [P, P, P, I64, I, I, I, I, I, I, I, I, I64, I64, P]
         lib.jo_stream_rows.restype = I
         _STREAM_LIB = lib
     return _STREAM_LIB
@@ -283,8 +289,8 @@ def stream_bytes(spec) -> int:
     scalars, and each row-invariant input once (as the kernels' algorithmic
     bytes count their weight row)."""
     row_in, row_out = spec.lpr * spec.ch * 16, spec.lpr * spec.ch * spec.outb
-    return (spec.rows * (spec.nin * row_in + spec.nout * row_out + spec.nscal * 4)
-            + spec.nconst * row_in)
+    return (spec.rows * (spec.nin * row_in + spec.nout * row_out + spec.out8 * row_in // 2
+                         + spec.nscal * 4) + spec.nconst * row_in)
 
 
 def time_stream(spec, steps: int, warmup: int, dev) -> dict:
@@ -295,8 +301,9 @@ def time_stream(spec, steps: int, warmup: int, dev) -> dict:
     else:
         rin = spec.rows * row_in
     rout = spec.rows * spec.lpr * spec.ch * spec.outb
+    rout8 = spec.rows * row_in // 2
     set_bytes = (spec.nin * rin + (0 if spec.inplace else spec.nout * rout)
-                 + spec.nconst * row_in + spec.rows * spec.nscal * 4)
+                 + spec.out8 * rout8 + spec.nconst * row_in + spec.rows * spec.nscal * 4)
     n_sets = max(4, math.ceil(ROT_BYTES / set_bytes))
     sets = []
     for _ in range(n_sets):
@@ -306,19 +313,23 @@ def time_stream(spec, steps: int, warmup: int, dev) -> dict:
                   for _ in range(spec.nconst)]
         outs = ins[:1] if spec.inplace else [torch.empty(rout, dtype=torch.uint8, device=dev)
                                              for _ in range(spec.nout)]
+        outs += [torch.empty(rout8, dtype=torch.uint8, device=dev) for _ in range(spec.out8)]
         scal = torch.empty(max(1, spec.rows * spec.nscal), dtype=torch.float32, device=dev)
         sets.append((ins, consts, outs, scal))
     lib = stream_lib()
 
-    def launch(i, h):
-        ins, consts, outs, scal = sets[i % n_sets]
+    import ctypes
+    ptrs = []
+    for ins, consts, outs, _ in sets:
         p = [t.data_ptr() + spec.goff for t in ins] + [t.data_ptr() for t in consts]
-        p += [None] * (3 - len(p))
-        o = [t.data_ptr() for t in outs] + [None] * (2 - len(outs))
-        rc = lib.jo_stream_rows(p[0], p[1], p[2], o[0], o[1],
-                                scal.data_ptr() if spec.nscal else None, spec.rows, spec.lpr,
-                                spec.ch, spec.nin, spec.nout, spec.outb, spec.nscal, spec.nconst,
-                                spec.group, spec.gstride, h)
+        ptrs.append(((ctypes.c_void_p * 5)(*p), (ctypes.c_void_p * 3)(*[t.data_ptr() for t in outs])))
+
+    def launch(i, h):
+        scal = sets[i % n_sets][3]
+        pin, pout = ptrs[i % n_sets]
+        rc = lib.jo_stream_rows(pin, pout, scal.data_ptr() if spec.nscal else None, spec.rows,
+                                spec.lpr, spec.ch, spec.nin, spec.nout, spec.outb, spec.nscal,
+                                spec.nconst, spec.out8, spec.group, spec.gstride, h)
         if rc != 0:
             raise RuntimeError(f"jo_stream_rows failed ({rc}) for {spec}")
 
@@ -328,8 +339,10 @@ def time_stream(spec, steps: int, warmup: int, dev) -> dict:
     out = _finish(res, stream_bytes(spec), n_sets, set_bytes)
     shape = (f"{spec.rows} rows, {spec.lpr} lanes x {spec.ch} chunks, "
              f"{spec.nin} in / {spec.nout} out")
+    if spec.out8:
+        shape += f" + an 8-byte-per-16 output"
     if spec.nconst:
-        shape += f", {spec.nconst} cached weight row read per row"
+        shape += f", {spec.nconst} cached row(s) read per row"
     if spec.group:
         shape += f", rows in groups of {spec.group} every {spec.gstride} B"
     out.update(shape=shape, kind="stream-ceiling")

@@ -16,9 +16,10 @@
 // per-head rows of a strided [T, H, D] view — at in[t] + (r / G) * GS +
 // (r % G) * LPR*CH*16), row r of output stream o at out[o] + r * LPR*CH*OUTB
 // bytes; with in[0] == out[0] and OUTB == 16 the stream is in place (the QK
-// kernels' layout). NCONST row-invariant inputs (a weight row every row is
-// multiplied by, read through the cache by every row as the kernels do) follow
-// the row inputs in in[].
+// kernels' layout). NCONST row-invariant inputs (a weight or modulation row
+// every row uses, read through the cache by every row as the kernels do)
+// follow the row inputs in in[]; OUT8 adds an output stream of 8 bytes per 16
+// read (an fp8 row next to a bf16 one) after the NOUT outputs in out[].
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -30,8 +31,8 @@ using jo::u32x2;
 using jo::u32x4;
 
 struct StreamArgs {
-  const char* in[3];
-  char* out[2];
+  const char* in[5];
+  char* out[3];
   float* scal;       // nscal fp32 per row, or null
   int64_t rows;
   uint32_t group_rows;    // input rows per contiguous group (0: all rows contiguous)
@@ -40,9 +41,9 @@ struct StreamArgs {
   uint32_t mask;     // 0 at run time; keeps the dependency opaque to the compiler
 };
 
-template <int LPR, int CH, int NIN, int NOUT, int OUTB, int NCONST>
+template <int LPR, int CH, int NIN, int NOUT, int OUTB, int NCONST, int OUT8>
 __global__ __launch_bounds__(256) void stream_rows_kernel(const StreamArgs a) {
-  static_assert(NIN + NCONST <= 3, "three input streams");
+  static_assert(NIN + NCONST <= 5 && NOUT + OUT8 <= 3, "stream counts");
   constexpr int RPB = 256 / LPR;
   constexpr int64_t kIn = int64_t(LPR) * CH * 16;
   constexpr int64_t kOut = int64_t(LPR) * CH * OUTB;
@@ -90,39 +91,56 @@ __global__ __launch_bounds__(256) void stream_rows_kernel(const StreamArgs a) {
                    u32x2{v.x ^ v.y ^ dep, v.z ^ v.w ^ dep});
     }
   }
+  if constexpr (OUT8) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const u32x4 v = c[NIN - 1][i];
+      jo::st8_nt(a.out[NOUT] + row * (kIn / 2) + (i * LPR + lane) * 8,
+                 u32x2{v.x ^ v.z ^ dep, v.y ^ v.w ^ dep});
+    }
+  }
   if (a.scal && lane < a.nscal) a.scal[row * a.nscal + lane] = static_cast<float>(x & 0xffu);
 }
 
-template <int LPR, int CH, int NIN, int NOUT, int OUTB, int NCONST = 0>
-bool try_launch(int lpr, int ch, int nin, int nout, int outb, int nconst, const StreamArgs& a,
-                hipStream_t st) {
-  if (lpr != LPR || ch != CH || nin != NIN || nout != NOUT || outb != OUTB || nconst != NCONST)
+template <int LPR, int CH, int NIN, int NOUT, int OUTB, int NCONST = 0, int OUT8 = 0>
+bool try_launch(int lpr, int ch, int nin, int nout, int outb, int nconst, int out8,
+                const StreamArgs& a, hipStream_t st) {
+  if (lpr != LPR || ch != CH || nin != NIN || nout != NOUT || outb != OUTB || nconst != NCONST ||
+      out8 != OUT8)
     return false;
   constexpr int RPB = 256 / LPR;
-  hipLaunchKernelGGL((stream_rows_kernel<LPR, CH, NIN, NOUT, OUTB, NCONST>),
+  hipLaunchKernelGGL((stream_rows_kernel<LPR, CH, NIN, NOUT, OUTB, NCONST, OUT8>),
                      dim3(static_cast<unsigned>((a.rows + RPB - 1) / RPB)), dim3(256), 0, st, a);
   return true;
 }
 
 }  // namespace
 
-// Shapes measured by bench.py: (lanes per row, chunks per lane, input
+// Shapes measured by bench.py: (lanes per row, chunks per lane, row input
 // streams, output streams, bytes stored per 16 bytes read, row-invariant
-// inputs). Returns 0 on success, 1 for a shape that is not instantiated or
+// inputs, extra 8-byte output). in[] holds nin + nconst pointers, out[]
+// nout + out8. Returns 0 on success, 1 for a shape that is not instantiated or
 // bad sizes, 3 for a launch error.
-extern "C" int jo_stream_rows(const void* in0, const void* in1, const void* in2, void* out0,
-                              void* out1, float* scal, int64_t rows, int lpr, int ch, int nin,
-                              int nout, int outb, int nscal, int nconst, int64_t group_rows,
-                              int64_t group_stride, void* stream) {
+extern "C" int jo_stream_rows(const void* const* in, void* const* out, float* scal, int64_t rows,
+                              int lpr, int ch, int nin, int nout, int outb, int nscal, int nconst,
+                              int out8, int64_t group_rows, int64_t group_stride, void* stream) {
   if (rows <= 0 || rows > (int64_t{1} << 30)) return 1;
   if (group_rows < 0 || group_rows > (int64_t{1} << 30) || (group_rows && group_stride <= 0))
     return 1;
-  StreamArgs a{{static_cast<const char*>(in0), static_cast<const char*>(in1),
-                static_cast<const char*>(in2)},
-               {static_cast<char*>(out0), static_cast<char*>(out1)},
-               scal, rows, static_cast<uint32_t>(group_rows), group_stride, nscal, 0u};
+  if (nin < 1 || nconst < 0 || nin + nconst > 5 || nout < 0 || out8 < 0 || out8 > 1 ||
+      nout + out8 > 3 || !in || !out)
+    return 1;
+  StreamArgs a{};
+  for (int t = 0; t < nin + nconst; ++t) a.in[t] = static_cast<const char*>(in[t]);
+  for (int o = 0; o < nout + out8; ++o) a.out[o] = static_cast<char*>(out[o]);
+  a.scal = scal;
+  a.rows = rows;
+  a.group_rows = static_cast<uint32_t>(group_rows);
+  a.group_stride = group_stride;
+  a.nscal = nscal;
+  a.mask = 0u;
   hipStream_t st = static_cast<hipStream_t>(stream);
-#define TRY(...) try_launch<__VA_ARGS__>(lpr, ch, nin, nout, outb, nconst, a, st)
+#define TRY(...) try_launch<__VA_ARGS__>(lpr, ch, nin, nout, outb, nconst, out8, a, st)
   const bool done =
       // QK units: 1, 2 or 3 head groups of 512 elements per wave, in place or to a cache
       TRY(64, 1, 1, 1, 16) ||
@@ -136,8 +154,12 @@ extern "C" int jo_stream_rows(const void* in0, const void* in1, const void* in2,
       TRY(128, 4, 1, 1, 8) ||
       TRY(64, 8, 1, 1, 8) ||
       TRY(256, 8, 1, 1, 8) ||
-      // two rows in, two rows out (residual add + norm): hidden 3072
+      // two rows in, two rows out (residual add + norm): hidden 3072, with
+      // the broadcast scale and shift rows, and the FP8 epilogue's shape
+      // (residual out, fp8 row out, gate / scale / shift rows)
       TRY(128, 3, 2, 2, 16) ||
+      TRY(128, 3, 2, 2, 16, 2) ||
+      TRY(128, 3, 2, 1, 16, 3, 1) ||
       TRY(64, 6, 2, 2, 16) ||
       TRY(256, 2, 2, 2, 16) ||
       // three rows in (x, scale, shift), one out: hidden 4096

@@ -22,11 +22,11 @@ def bench():
 
 
 def instantiated_shapes() -> set[tuple[int, ...]]:
-    """(lpr, ch, nin, nout, outb, nconst) of every TRY(...) in the dispatch list."""
+    """(lpr, ch, nin, nout, outb, nconst, out8) of every TRY(...) in the dispatch list."""
     shapes = set()
     for m in re.finditer(r"TRY\(([\d,\s]+)\)", STREAM_SRC.read_text()):
         v = [int(t) for t in m.group(1).split(",")]
-        shapes.add(tuple(v + [0] * (6 - len(v))))
+        shapes.add(tuple(v + [0] * (7 - len(v))))
     return shapes
 
 
@@ -34,9 +34,9 @@ def test_stream_shapes_are_instantiated(bench):
     shapes = instantiated_shapes()
     assert shapes, "no TRY(...) lines found"
     for name, s in bench.STREAMS.items():
-        key = (s.lpr, s.ch, s.nin, s.nout, s.outb, s.nconst)
+        key = (s.lpr, s.ch, s.nin, s.nout, s.outb, s.nconst, s.out8)
         assert key in shapes, f"{name}: shape {key} is not instantiated in {STREAM_SRC.name}"
-        assert s.nin + s.nconst <= 3 and s.nout <= 2, name
+        assert s.nin + s.nconst <= 5 and s.nout + s.out8 <= 3, name
         assert not (s.inplace and s.nout != 1), name
 
 
@@ -64,7 +64,8 @@ def test_own_shape_streams_move_the_config_bytes(bench):
             continue
         alg = W.algorithmic_bytes(W.CONFIGS[s.cfg])
         got = bench.stream_bytes(s)
-        if s.cfg.startswith("C4") or s.cfg in ("C1", "R_q4k", "R_q16k", "R_rms", "R_kn", "T_rms"):
+        if s.cfg.startswith("C4") or s.cfg in ("C1", "C2", "N3", "R_q4k", "R_q16k", "R_rms", "R_kn",
+                                               "T_rms"):
             assert got == alg, (name, got, alg)
         else:
             assert abs(got - alg) <= 0.01 * alg, (name, got, alg)
@@ -85,11 +86,11 @@ def test_stream_library_rejects_bad_sizes_without_a_gpu(bench):
         pytest.skip("stream library not built (python joyai-video-edit_amd/build.py)")
     import torch  # noqa: F401  (shares torch's HIP runtime, as bench.py does)
     lib = bench.stream_lib()
-    null = None
-    # rows <= 0, a group with no stride, and a shape that is not instantiated
-    assert lib.jo_stream_rows(null, null, null, null, null, null, 0, 64, 6, 1, 1, 8, 1, 0, 0, 0,
-                              null) == 1
-    assert lib.jo_stream_rows(null, null, null, null, null, null, 10, 16, 1, 1, 1, 16, 0, 1, 32,
-                              0, null) == 1
-    assert lib.jo_stream_rows(null, null, null, null, null, null, 10, 64, 5, 1, 1, 8, 1, 0, 0, 0,
-                              null) == 1
+    pin = (ctypes.c_void_p * 5)()
+    pout = (ctypes.c_void_p * 3)()
+    # rows <= 0, a group with no stride, too many streams, a shape that is not
+    # instantiated
+    assert lib.jo_stream_rows(pin, pout, None, 0, 64, 6, 1, 1, 8, 1, 0, 0, 0, 0, None) == 1
+    assert lib.jo_stream_rows(pin, pout, None, 10, 16, 1, 1, 1, 16, 0, 1, 0, 32, 0, None) == 1
+    assert lib.jo_stream_rows(pin, pout, None, 10, 64, 6, 3, 1, 8, 1, 3, 0, 0, 0, None) == 1
+    assert lib.jo_stream_rows(pin, pout, None, 10, 64, 5, 1, 1, 8, 1, 0, 0, 0, 0, None) == 1
