@@ -130,9 +130,16 @@ extern "C" int jo_stream_rows(const void* const* in, void* const* out, float* sc
   if (nin < 1 || nconst < 0 || nin + nconst > 5 || nout < 0 || out8 < 0 || out8 > 1 ||
       nout + out8 > 3 || !in || !out)
     return 1;
+  if (nscal < 0 || nscal > 64 || (nscal > 0 && !scal)) return 1;
   StreamArgs a{};
-  for (int t = 0; t < nin + nconst; ++t) a.in[t] = static_cast<const char*>(in[t]);
-  for (int o = 0; o < nout + out8; ++o) a.out[o] = static_cast<char*>(out[o]);
+  for (int t = 0; t < nin + nconst; ++t) {
+    if (!in[t]) return 1;
+    a.in[t] = static_cast<const char*>(in[t]);
+  }
+  for (int o = 0; o < nout + out8; ++o) {
+    if (!out[o]) return 1;
+    a.out[o] = static_cast<char*>(out[o]);
+  }
   a.scal = scal;
   a.rows = rows;
   a.group_rows = static_cast<uint32_t>(group_rows);
