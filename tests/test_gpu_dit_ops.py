@@ -87,6 +87,38 @@ def test_grid_views_on_packed_qkv(dev, sid):
         assert_bf16_within_ulp(out[:, :, j], ref, rowmax(ref), what=f"grid views sid={sid}")
 
 
+@pytest.mark.parametrize("sid,source_dim", [(1.0, None), (3.0, None), (3.0, 256)])
+def test_grid_views_head_dim_256_source_rotation(dev, sid, source_dim):
+    """head_dim 256 with a source id: the source rotation covers the first
+    min(source_dim, D) dims, source_dim 128 by default (the model's
+    source_id_rope_dim, dit.py:792, config.py:35), against the oracle's tables
+    built with the same split."""
+    from joyomni_ops import dit_ops
+    B, L, H, D = 1, 96, 4, 256
+    dims = (32, 112, 112)
+    g = torch.Generator().manual_seed(60 + int(sid))
+    qkv = torch.randn(B, L, 3, H, D, generator=g).to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    d = qkv.to(dev)
+    kwargs = {} if source_dim is None else {"source_dim": source_dim}
+    dit_ops.fused_qk_norm_rope_3d_grid_views(d[:, :, 0], d[:, :, 1], qw.to(dev), kw.to(dev),
+                                             grid_hw=(8, 12), t0=5, rope_dims=dims,
+                                             theta=256.0, source_id=sid, **kwargs)
+    torch.cuda.synchronize()
+    out = d.cpu()
+    sd = 128 if source_dim is None else source_dim
+    cos, sin = ops.half_tables(*ops.rope_grid_tables(1, 8, 12, 5, dims, 256.0, sid, 256.0, sd))
+    for j, w in ((0, qw), (1, kw)):
+        ref = ops.qk_norm_rope_f32(qkv[:, :, j].contiguous(), w, cos, sin, 1e-6)
+        assert_bf16_within_ulp(out[:, :, j], ref, rowmax(ref),
+                               what=f"D=256 sid={sid} source_dim={source_dim}")
+    if source_dim is None:
+        # the full-width source rotation is a different table: the split matters
+        c2, s2 = ops.half_tables(*ops.rope_grid_tables(1, 8, 12, 5, dims, 256.0, sid, 256.0, D))
+        assert not torch.equal(c2, cos)
+
+
 def test_rmsnorm_qk_bf16_strided(dev):
     from joyomni_ops import dit_ops
     B, L, H, D = 1, 200, 8, 128
