@@ -99,3 +99,14 @@ def test_stream_library_rejects_bad_sizes_without_a_gpu(bench):
     fake = (ctypes.c_void_p * 5)(*([16] * 5))
     fake_out = (ctypes.c_void_p * 3)(*([16] * 3))
     assert lib.jo_stream_rows(fake, fake_out, None, 10, 64, 6, 1, 1, 8, 1, 0, 0, 0, 0, None) == 1
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """One GPU is what this build measures: --gpus 2 exits with a message
+    naming the reason, before touching a GPU."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=300)
+    out = r.stdout + r.stderr
+    assert "one GPU" in out and "--gpus 2" in out, out
