@@ -231,9 +231,10 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
     // reference's amax and lets the clamp go; waves (workgroups, for rows
     // wider than a wave) with a non-finite row take the NaN-skipping maximum
     // and clamp.
-    float amax = row_reduce<LPR, OpAmax>(ymax, red_c);
+    bool any_nonfinite;
+    float amax = row_amax_vote<LPR>(ymax, red_c, any_nonfinite);
     const bool finite_row = finite_bits(amax);
-    if (rows_any<LPR>(!finite_row)) {
+    if (any_nonfinite) {
       float m = 0.f;
 #pragma unroll
       for (int i = 0; i < CH; ++i)

@@ -47,9 +47,10 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restri
 #pragma unroll
     for (int j = 0; j < 8; ++j) amax = nan_max_abs(amax, elem<Tag>(c[i], j));
   }
-  amax = row_reduce<LPR, OpAmax>(amax, red);
+  bool any_nonfinite;
+  amax = row_amax_vote<LPR>(amax, red, any_nonfinite);
   const bool finite_row = finite_bits(amax);
-  if (rows_any<LPR>(!finite_row)) {
+  if (any_nonfinite) {
     // Reference amax: NaNs skipped (fmaxf from 0).
     float m = 0.f;
 #pragma unroll
@@ -285,9 +286,10 @@ void rmsnorm_quant_tok_kernel(
       amax = nan_max_abs(amax, v[i][j]);
     }
   }
-  amax = row_reduce<LPR, OpAmax>(amax, red_max);
+  bool any_nonfinite;
+  amax = row_amax_vote<LPR>(amax, red_max, any_nonfinite);
   const bool finite_row = finite_bits(amax);
-  if (rows_any<LPR>(!finite_row)) {
+  if (any_nonfinite) {
     float m = 0.f;
 #pragma unroll
     for (int i = 0; i < CH; ++i)
