@@ -76,7 +76,21 @@ __global__ __launch_bounds__(256) void stream_rows_kernel(const StreamArgs a) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) x ^= c[t][i].x ^ c[t][i].y ^ c[t][i].z ^ c[t][i].w;
   uint32_t dep = x & a.mask;
-  if constexpr (LPR > jo::kWave) dep = __syncthreads_or(dep) ? a.mask : 0u;
+  if constexpr (LPR > jo::kWave) {
+    // The rows' waves meet once, through LDS, as the kernels' cross-wave
+    // reductions do: each wave's lane 0 posts its part, one barrier, and every
+    // wave reads the parts of its row.
+    __shared__ uint32_t part[256 / jo::kWave];
+    const int wave = threadIdx.x / jo::kWave;
+    dep = __ballot(dep != 0u) ? a.mask : 0u;
+    if ((threadIdx.x & (jo::kWave - 1)) == 0) part[wave] = dep;
+    __syncthreads();
+    constexpr int kWpr = LPR / jo::kWave;
+    const int first = (wave / kWpr) * kWpr;
+    dep = 0u;
+#pragma unroll
+    for (int k = 0; k < kWpr; ++k) dep |= part[first + k];
+  }
   if (!ok) return;
 #pragma unroll
   for (int o = 0; o < NOUT; ++o) {

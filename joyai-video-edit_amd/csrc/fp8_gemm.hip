@@ -18,6 +18,7 @@
 // reads with one ds_read_b128 fall in 16 distinct 16-byte bank groups.
 
 #include <atomic>
+#include <type_traits>
 
 #include "jo_device.hpp"
 #include "jo_host.hpp"
@@ -217,6 +218,82 @@ struct PipeLoads {
   bool last;                      // the wave owns a slot kPerWave - 1 (always when kEven)
 };
 
+// Epilogue of a wave's K loop, shared by the pipelined kernels. The LDS of
+// the K loop's ring (at least 128 padded output rows) is free once every wave
+// has passed the first barrier below.
+template <class OutTag, int BM, int BN, int NW, int MI>
+__device__ __forceinline__ void store_tile(const GemmArgs& g, uint8_t* smem,
+                                           const f32x16 (&acc)[MI][BN / (NW / 2) / 32], int wm,
+                                           int wn, int m0, int n0) {
+  constexpr int WCOLS = BN / (NW / 2);
+  constexpr int J = WCOLS / 32;
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int fr = lane & 31, fh = lane >> 5;
+  // Subtile (i, j) element e of a lane is row
+  // m = m0 + wm*128 + i*32 + lane%32, column n = n0 + wn*WCOLS + j*32 +
+  // (e/4)*8 + (lane/32)*4 + e%4. The finished values go through LDS (free
+  // after the K loop) one 128-row half at a time, so that every row leaves
+  // as whole lines of 16-byte lane stores: stored straight from the MFMA
+  // layout (8 bytes per lane, 32 rows per wave store) the lines were written
+  // back part-filled, measured 2.4-4.5x the output bytes in WRITE_SIZE.
+  constexpr int kRowBytes = BN * 2 + 16;  // padded LDS row: 8-byte writes of 32 rows spread over the banks
+  float sam[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) sam[i] = g.sa[min(m0 + wm * 128 + i * 32 + fr, g.M - 1)];
+  float sbq[J][4][4], bq[J][4][4];
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = min(n0 + wn * WCOLS + j * 32 + q * 8 + fh * 4, g.N - 4);  // N % 8 == 0
+      const u32x4 sbv = ld16(g.sb + n);
+      u32x4 b4{0u, 0u, 0u, 0u};
+      if (g.bias) {
+        const u32x2 braw = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(g.bias) + n);
+        b4 = u32x4{braw.x, braw.y, 0u, 0u};
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        sbq[j][q][t] = elem<F32>(sbv, t);
+        bq[j][q][t] = g.bias ? elem<OutTag>(b4, t) : 0.f;
+      }
+    }
+  constexpr int kT = NW * 64;
+  constexpr int kChunksPerRow = BN * 2 / 16;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    __syncthreads();  // the ring (or the previous half) is no longer read
+    if (wm == half) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float o[8];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              o[t] = __builtin_fmaf(sam[i], acc[i][j][q * 4 + t] * sbq[j][q][t], bq[j][q][t]);
+              o[t + 4] = 0.f;
+            }
+            const u32x4 pk = pack<OutTag>(o);
+            const int rl = i * 32 + fr, cl = wn * WCOLS + j * 32 + q * 8 + fh * 4;
+            *reinterpret_cast<u32x2*>(smem + rl * kRowBytes + cl * 2) = u32x2{pk.x, pk.y};
+          }
+    }
+    __syncthreads();
+    const int rows = half == 0 ? 128 : BM - 128;
+    for (int c = tid; c < rows * kChunksPerRow; c += kT) {
+      const int rl = c / kChunksPerRow, ch = c % kChunksPerRow;
+      const int m = m0 + half * 128 + rl, n = n0 + ch * 8;
+      if (m < g.M && n < g.N)
+        st16_nt(static_cast<uint16_t*>(g.out) + static_cast<int64_t>(m) * g.ldo + n,
+                *reinterpret_cast<const u32x4*>(smem + rl * kRowBytes + ch * 16));
+    }
+  }
+}
+
 // One output tile's K loop and epilogue for a wave holding MI row blocks of 32
 // (rows wm*128 .. wm*128 + 32*MI - 1 of the tile) and WCOLS columns.
 template <class OutTag, int BM, int BN, int NW, int NST, int MI>
@@ -372,69 +449,8 @@ __device__ __forceinline__ void fp8_gemm_pipe_tile(const GemmArgs& g, uint8_t* s
     if (s + 1 < stages) drain(s + 1, af1, bf1, af0, bf0);
   }
 
-  // Epilogue: subtile (i, j) element e of a lane is row
-  // m = m0 + wm*128 + i*32 + lane%32, column n = n0 + wn*WCOLS + j*32 +
-  // (e/4)*8 + (lane/32)*4 + e%4. The finished values go through LDS (free
-  // after the K loop) one 128-row half at a time, so that every row leaves
-  // as whole lines of 16-byte lane stores: stored straight from the MFMA
-  // layout (8 bytes per lane, 32 rows per wave store) the lines were written
-  // back part-filled, measured 2.4-4.5x the output bytes in WRITE_SIZE.
-  constexpr int kRowBytes = BN * 2 + 16;  // padded LDS row: 8-byte writes of 32 rows spread over the banks
-  static_assert(128 * kRowBytes <= NST * kStage, "epilogue staging fits the ring");
-  float sam[MI];
-#pragma unroll
-  for (int i = 0; i < MI; ++i) sam[i] = g.sa[min(m0 + wm * 128 + i * 32 + fr, g.M - 1)];
-  float sbq[J][4][4], bq[J][4][4];
-#pragma unroll
-  for (int j = 0; j < J; ++j)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int n = min(n0 + wn * WCOLS + j * 32 + q * 8 + fh * 4, g.N - 4);  // N % 8 == 0
-      const u32x4 sbv = ld16(g.sb + n);
-      u32x4 b4{0u, 0u, 0u, 0u};
-      if (g.bias) {
-        const u32x2 braw = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(g.bias) + n);
-        b4 = u32x4{braw.x, braw.y, 0u, 0u};
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        sbq[j][q][t] = elem<F32>(sbv, t);
-        bq[j][q][t] = g.bias ? elem<OutTag>(b4, t) : 0.f;
-      }
-    }
-  constexpr int kT = NW * 64;
-  constexpr int kChunksPerRow = BN * 2 / 16;
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    __syncthreads();  // the ring (or the previous half) is no longer read
-    if (wm == half) {
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < J; ++j)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            float o[8];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              o[t] = __builtin_fmaf(sam[i], acc[i][j][q * 4 + t] * sbq[j][q][t], bq[j][q][t]);
-              o[t + 4] = 0.f;
-            }
-            const u32x4 pk = pack<OutTag>(o);
-            const int rl = i * 32 + fr, cl = wn * WCOLS + j * 32 + q * 8 + fh * 4;
-            *reinterpret_cast<u32x2*>(smem + rl * kRowBytes + cl * 2) = u32x2{pk.x, pk.y};
-          }
-    }
-    __syncthreads();
-    const int rows = half == 0 ? 128 : BM - 128;
-    for (int c = tid; c < rows * kChunksPerRow; c += kT) {
-      const int rl = c / kChunksPerRow, ch = c % kChunksPerRow;
-      const int m = m0 + half * 128 + rl, n = n0 + ch * 8;
-      if (m < g.M && n < g.N)
-        st16_nt(static_cast<uint16_t*>(g.out) + static_cast<int64_t>(m) * g.ldo + n,
-                *reinterpret_cast<const u32x4*>(smem + rl * kRowBytes + ch * 16));
-    }
-  }
+  static_assert(128 * (BN * 2 + 16) <= NST * kStage, "epilogue staging fits the ring");
+  store_tile<OutTag, BM, BN, NW, MI>(g, smem, acc, wm, wn, m0, n0);
 }
 
 template <class OutTag, int BM, int BN, int NW, int NST>
@@ -495,6 +511,224 @@ void launch_pipe(const GemmArgs& g, hipStream_t stream) {
                      dim3((g.N + BN - 1) / BN, (g.M + BM - 1) / BM), dim3(NW * 64), 0, stream, g);
 }
 
+// ---------------------------------------------------------------------------
+// 128-byte-stage kernel (K % 128 == 0), the default for 8-wave tiles: the
+// tile and wave layout of the pipelined kernel, but K advances in 128-byte
+// stages through two LDS slots of (BM + BN) x 128 bytes. A wave's 1 KB direct
+// load then covers eight whole 128-byte rows (eight lanes per row) where a
+// 64-byte stage covers sixteen half lines: the vector L1 keeps one entry per
+// missed line, so whole lines bring twice the bytes per entry, and the loads
+// of the 64-byte stages were what held that kernel back (4096^3 without its
+// loads, a timing-only copy: 65 -> 48 us). Per stage s, one barrier:
+//   MFMAs of the first 64-byte half    | reads of the second half's fragments
+//   wait for those reads and for this wave's loads of stage s+1; barrier
+//   loads of stage s+2 into the slot of stage s (every wave holds its
+//   fragments now); MFMAs of the second half | reads of stage s+1's first half.
+// LDS rows are 128 bytes; chunk c of row r sits at chunk position
+// c ^ ((r >> 1) & 7): the sixteen consecutive rows a 16-lane group reads with
+// one ds_read_b128 then fall in sixteen distinct 16-byte bank groups.
+// ---------------------------------------------------------------------------
+constexpr int kQBK = 128;  // bytes of K per stage
+
+__device__ __forceinline__ int qswz(int r) { return (r >> 1) & 7; }
+
+// Direct loads of one stage: BM rows of A then BN rows of B^T, 128 bytes
+// each, written by (BM + BN) / 8 wave instructions of 1 KB (8 rows, eight
+// lanes per row); slot L fills stage bytes L * 1024 .. +1024 and belongs to
+// wave L % NW.
+template <int BM, int BN, int NW>
+struct PairLoads {
+  static constexpr int kSlots = (BM + BN) / 8;
+  static constexpr int kPerWave = (kSlots + NW - 1) / NW;
+  static constexpr bool kEven = kSlots % NW == 0;
+  const uint8_t* base[kPerWave];  // wave-uniform: the tile's first row of A or B^T
+  uint32_t off[kPerWave];         // this lane's 16-byte chunk of each slot at K offset 0
+  bool last;                      // the wave owns a slot kPerWave - 1 (always when kEven)
+};
+
+template <class OutTag, int BM, int BN, int NW, int MI>
+__device__ __forceinline__ void fp8_gemm_pair_tile(const GemmArgs& g, uint8_t* smem,
+                                                   const PairLoads<BM, BN, NW>& ld, int wave,
+                                                   int wm, int wn, int m0, int n0) {
+  using Loads = PairLoads<BM, BN, NW>;
+  constexpr int WCOLS = BN / (NW / 2);  // wave tile columns
+  constexpr int J = WCOLS / 32;         // n-subtiles of 32 per wave
+  constexpr int kSlot = (BM + BN) * kQBK;
+  constexpr int PER = Loads::kPerWave;
+  static_assert(J >= 1 && MI >= 2 && MI <= 4, "tile shape");
+  static_assert(128 * (BN * 2 + 16) <= 2 * kSlot, "epilogue staging fits the slots");
+  const int lane = threadIdx.x % kWave;
+  const int stages = g.K / kQBK;
+  auto issue = [&](int s) {
+    uint8_t* base = smem + (s & 1) * kSlot;
+    const int kb = s * kQBK;
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (Loads::kEven || i + 1 < PER || ld.last)
+        __builtin_amdgcn_global_load_lds(ld.base[i] + (ld.off[i] + kb), (__attribute__((address_space(3))) void*)(base + (wave + i * NW) * 1024), 16, 0, 0);
+  };
+
+  f32x16 acc[MI][J];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Fragment rows are wm*128 + i*32 + lane%32 (A) and wn*WCOLS + j*32 +
+  // lane%32 (B): all differ from lane%32 by multiples of 16, so they share
+  // its swizzle, and row block i (j) sits i*32 (j*32) rows after block 0.
+  const int fr = lane & 31, fh = lane >> 5;
+  const int q = qswz(fr);
+  int offa[2][2], offb[2][2];  // [half of the stage][chunk of the pair]
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int pos = ((k * 4 + fh * 2 + h) ^ q) << 4;
+      offa[k][h] = (wm * 128 + fr) * kQBK + pos;
+      offb[k][h] = BM * kQBK + (wn * WCOLS + fr) * kQBK + pos;
+    }
+  auto read_frags = [&](int s, int k, i32x8 (&af)[MI], i32x8 (&bf)[J]) {
+    const uint8_t* st = smem + (s & 1) * kSlot;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(st + offb[k][0] + j * 32 * kQBK);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(st + offb[k][1] + j * 32 * kQBK);
+      bf[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    }
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(st + offa[k][0] + i * 32 * kQBK);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(st + offa[k][1] + i * 32 * kQBK);
+      af[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    }
+  };
+  // Wait for this wave's LDS reads and for all but `later` stages of its
+  // loads (PER instructions a stage; waves without a slot kPerWave - 1 issue
+  // one fewer).
+  auto wait_own = [&](int later) {
+    JO_WAIT_LDS0();
+    if (Loads::kEven || ld.last)
+      wait_loads<PER>(later);
+    else
+      wait_loads<PER - 1>(later);
+  };
+  auto bare_barrier = [&]() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // B first: the accumulator is the transposed tile (a lane holds one output
+  // row and, per group of four registers, four consecutive columns).
+  auto mfma_q = [&](int qi, i32x8 (&af)[MI], i32x8 (&bf)[J]) {
+    acc[qi / J][qi % J] = mfma32(bf[qi % J], af[qi / J], acc[qi / J][qi % J]);
+  };
+
+  i32x8 a0[MI], b0[J], a1[MI], b1[J];  // fragments of the first / second half of a stage
+  // With 256-row tiles the first KB MFMAs of the second half go out before
+  // the barrier (their fragments are this wave's own), so the matrix cores
+  // are busy while the waves meet.
+  constexpr int KB = BM == 256 ? 2 : 0;
+  // Stage s with stage s+1 present (NEXT) and stage s+2 present (MORE).
+  auto stage = [&](int s, auto next, auto more) {
+    constexpr bool kNext = decltype(next)::value, kMore = decltype(more)::value;
+    // First half: MFMAs on a0/b0 while the second half's fragments arrive.
+    read_frags(s, 1, a1, b1);
+#pragma unroll
+    for (int qi = 0; qi < MI * J; ++qi) mfma_q(qi, a0, b0);
+#pragma unroll
+    for (int qi = 0; qi < MI * J; ++qi) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Stage s+1's loads are this wave's only ones in flight.
+    wait_own(0);
+#pragma unroll
+    for (int qi = 0; qi < KB; ++qi) mfma_q(qi, a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kNext) bare_barrier();
+    if constexpr (kMore) issue(s + 2);
+    if constexpr (kNext) read_frags(s + 1, 0, a0, b0);
+#pragma unroll
+    for (int qi = KB; qi < MI * J; ++qi) mfma_q(qi, a1, b1);
+    if constexpr (kNext) {
+#pragma unroll
+      for (int qi = KB; qi < MI * J; ++qi) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  using T = std::true_type;
+  using F = std::false_type;
+  issue(0);
+  if (stages > 1) issue(1);
+  wait_own(stages > 1 ? 1 : 0);
+  bare_barrier();
+  read_frags(0, 0, a0, b0);
+  int s = 0;
+  for (; s + 2 < stages; ++s) stage(s, T{}, T{});
+  if (s + 1 < stages) stage(s++, T{}, F{});
+  stage(s, F{}, F{});
+
+  store_tile<OutTag, BM, BN, NW, MI>(g, smem, acc, wm, wn, m0, n0);
+}
+
+template <class OutTag, int BM, int BN, int NW>
+__device__ __forceinline__ void fp8_gemm_pair_body(const GemmArgs& g) {
+  using Loads = PairLoads<BM, BN, NW>;
+  static_assert(BM == 256 || BM == 224, "tile rows");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * (BM + BN) * kQBK];
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  // Wave tiles as in fp8_gemm_pipe_body.
+  const int wm = BM == 256 ? (wave & 1) : wave / (NW / 2);
+  const int wn = BM == 256 ? (wave >> 1) : wave % (NW / 2);
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+  // Lane p of a slot fills row +p/8, chunk position p%8 with the global chunk
+  // that belongs there. Rows beyond M (N) read row M-1 (N-1); they are never
+  // stored. Wave-uniform 64-bit tile bases plus 32-bit lane offsets (the host
+  // keeps 256 rows of A and B^T under 4 GB).
+  Loads ld;
+#pragma unroll
+  for (int i = 0; i < Loads::kPerWave; ++i) {
+    const int slot = wave + i * NW;
+    const bool is_a = slot < BM / 8;
+    const int r = (is_a ? slot : slot - BM / 8) * 8 + lane / 8;
+    const int row = is_a ? min(m0 + r, g.M - 1) - m0 : min(n0 + r, g.N - 1) - n0;
+    ld.base[i] = is_a ? g.a + static_cast<int64_t>(m0) * g.lda : g.b + static_cast<int64_t>(n0) * g.ldb;
+    ld.off[i] = static_cast<uint32_t>(row) * static_cast<uint32_t>(is_a ? g.lda : g.ldb) +
+                (((lane & 7) ^ qswz(r)) * 16);
+  }
+  ld.last = Loads::kEven || wave + (Loads::kPerWave - 1) * NW < Loads::kSlots;
+  if constexpr (BM == 256) {
+    fp8_gemm_pair_tile<OutTag, BM, BN, NW, 4>(g, smem, ld, wave, wm, wn, m0, n0);
+  } else {
+    if (wm == 0)
+      fp8_gemm_pair_tile<OutTag, BM, BN, NW, 4>(g, smem, ld, wave, wm, wn, m0, n0);
+    else
+      fp8_gemm_pair_tile<OutTag, BM, BN, NW, 3>(g, smem, ld, wave, wm, wn, m0, n0);
+  }
+}
+
+template <class OutTag, int BM, int BN, int NW>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void fp8_gemm_pair_kernel(const GemmArgs g) {
+  fp8_gemm_pair_body<OutTag, BM, BN, NW>(g);
+}
+
+template <class OutTag, int BM, int BN, int NW>
+void launch_pair(const GemmArgs& g, hipStream_t stream) {
+  hipLaunchKernelGGL((fp8_gemm_pair_kernel<OutTag, BM, BN, NW>),
+                     dim3((g.N + BN - 1) / BN, (g.M + BM - 1) / BM), dim3(NW * 64), 0, stream, g);
+}
+
 // CUs of the current device (queried once per device; 256, MI355X's count,
 // if the query fails).
 int cu_count() {
@@ -534,8 +768,13 @@ int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   // the matrix cores).
   const int forced = launch_knob(JO_KNOB_GEMM_SHAPE);
   const int shape = forced >= 0 ? forced : (pick_tile_rows(g.M, g.N) == 224 ? 3 : 0);
+  const bool pair_ok = pipe_ok && g.K % kQBK == 0;
   if (pipe_ok && shape == 1)
     launch_pipe<OutTag, 256, 128, 4, 3>(g, stream);
+  else if (pair_ok && shape == 0)
+    launch_pair<OutTag, 256, 256, 8>(g, stream);
+  else if (pair_ok && shape == 3)
+    launch_pair<OutTag, 224, 256, 8>(g, stream);
   else if (pipe_ok && shape == 0)
     launch_pipe<OutTag, 256, 256, 8, 4>(g, stream);
   else if (pipe_ok && shape == 3)
