@@ -159,10 +159,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
     tok = w / (SPLIT / 2);
     part = (on_k ? 1 : 0) | (static_cast<int>(w % (SPLIT / 2)) << 1);
   }
-  if (tok >= a.tokens) {
-    __syncthreads();  // the workgroup's one barrier (step 4), taken on the way out
-    return;
-  }
+  if (tok >= a.tokens) return;
   const int64_t b = tok / a.seq_len;
   const int n = static_cast<int>(tok - b * a.seq_len);
   const int pl = lane % LPH;  // this lane holds elements 8*pl .. 8*pl+7 of its head
@@ -269,13 +266,11 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
   }
 
   // 4. Normalize, rotate, store; further batches only when H*D > G*512.
-  // The workgroup first meets once, each wave holding its first batch of
-  // rows, so that the workgroup's row stores leave together: measured C3
-  // ([1, 10530, 24, 128] + ring) 44.6 -> 43.9 us and table mode at
-  // [1, 3120, 32, 128] 19.3 -> 19.1 us, [1, 3510, 24, 128] unchanged
-  // (a barrier without the wait was no faster than none).
+  // Waves do not meet: a workgroup barrier here (so that a workgroup's row
+  // stores leave together) measured slower with the current loads
+  // ([1, 1560, 32, 128] tables 10.20 -> 10.32 us, [1, 3120, 32, 128] 17.57 ->
+  // 17.67 us, C3 41.30 -> 41.43 us).
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  __syncthreads();
   for (int g0 = gbeg; g0 < groups; g0 += G) {
     if (g0 != gbeg) load_batch(g0);
 #pragma unroll
