@@ -262,6 +262,9 @@ STREAMS = {
     "S_R_ln": _S("R_ln", 3120, 256, 2, 3, 1, 16, 0, False),
     "S_R_ln@64x8": _S("R_ln", 3120, 64, 8, 3, 1, 16, 0, False),
     "S_R_qk": _S("R_qk", 3120 * 8, 64, 2, 1, 1, 16, 0, True),
+    # q and k rows in place, and for the k rows the pre-RoPE stage as well:
+    # on average one row read, one and a half written.
+    "S_R_qks": _S("R_qks", 3120 * 8, 64, 2, 1, 1, 16, 0, True, out8=1),
     "S_T_rms": _S("T_rms", 4096, 64, 8, 1, 1, 16, 0, False, 1),
     "S_T_rms@no-weight": _S("T_rms", 4096, 64, 8, 1, 1, 16, 0, False),
     "S_T_ln": _S("T_ln", 4096, 256, 2, 3, 1, 16, 0, False),

@@ -166,6 +166,7 @@ extern "C" int jo_stream_rows(const void* const* in, void* const* out, float* sc
       // QK units: 1, 2 or 3 head groups of 512 elements per wave, in place or to a cache
       TRY(64, 1, 1, 1, 16) ||
       TRY(64, 2, 1, 1, 16) ||
+      TRY(64, 2, 1, 1, 16, 0, 1) ||   // QK pass that also writes the pre-RoPE K stage
       TRY(64, 3, 1, 1, 16) ||
       TRY(64, 4, 1, 1, 16) ||
       // bf16 rows -> fp8 rows (+ scales): hidden 3072 / 4096 / 16384
