@@ -515,11 +515,13 @@ void launch_pipe(const GemmArgs& g, hipStream_t stream) {
 // 128-byte-stage kernel (K % 128 == 0), the default for 8-wave tiles: the
 // tile and wave layout of the pipelined kernel, but K advances in 128-byte
 // stages through two LDS slots of (BM + BN) x 128 bytes. A wave's 1 KB direct
-// load then covers eight whole 128-byte rows (eight lanes per row) where a
-// 64-byte stage covers sixteen half lines: the vector L1 keeps one entry per
-// missed line, so whole lines bring twice the bytes per entry, and the loads
-// of the 64-byte stages were what held that kernel back (4096^3 without its
-// loads, a timing-only copy: 65 -> 48 us). Per stage s, one barrier:
+// load then covers eight whole 128-byte lines (eight lanes per row) where a
+// 64-byte stage covers sixteen half lines. The loads are what bounds the K
+// loop (a timing-only copy of the 64-byte kernel without them ran 4096^3 in
+// 48 instead of 65 us), and the vector L1 stalls on its pending misses to L2:
+// whole lines halve the L1 -> L2 requests for the same bytes (rocprofv3
+// TCP_TCC_READ_REQ) and took 4096^3 from 67.7 to 61.2 us. Per stage s, one
+// barrier:
 //   MFMAs of the first 64-byte half    | reads of the second half's fragments
 //   wait for those reads and for this wave's loads of stage s+1; barrier
 //   loads of stage s+2 into the slot of stage s (every wave holds its
