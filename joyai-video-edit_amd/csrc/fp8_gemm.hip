@@ -524,8 +524,8 @@ void launch_pipe(const GemmArgs& g, hipStream_t stream) {
 // barrier:
 //   MFMAs of the first 64-byte half    | reads of the second half's fragments
 //   wait for those reads and for this wave's loads of stage s+1; barrier
-//   loads of stage s+2 into the slot of stage s (every wave holds its
-//   fragments now); MFMAs of the second half | reads of stage s+1's first half.
+//   MFMAs of the second half | loads of stage s+2 into the slot of stage s
+//   (every wave holds its fragments now), reads of stage s+1's first half.
 // LDS rows are 128 bytes; chunk c of row r sits at chunk position
 // c ^ ((r >> 1) & 7): the sixteen consecutive rows a 16-lane group reads with
 // one ds_read_b128 then fall in sixteen distinct 16-byte bank groups.
@@ -561,13 +561,14 @@ __device__ __forceinline__ void fp8_gemm_pair_tile(const GemmArgs& g, uint8_t* s
   static_assert(128 * (BN * 2 + 16) <= 2 * kSlot, "epilogue staging fits the slots");
   const int lane = threadIdx.x % kWave;
   const int stages = g.K / kQBK;
+  // Load i of this wave's share of stage s, and all of them.
+  auto issue_one = [&](int s, int i) {
+    if (Loads::kEven || i + 1 < PER || ld.last)
+      __builtin_amdgcn_global_load_lds(ld.base[i] + (ld.off[i] + s * kQBK), (__attribute__((address_space(3))) void*)(smem + (s & 1) * kSlot + (wave + i * NW) * 1024), 16, 0, 0);
+  };
   auto issue = [&](int s) {
-    uint8_t* base = smem + (s & 1) * kSlot;
-    const int kb = s * kQBK;
 #pragma unroll
-    for (int i = 0; i < PER; ++i)
-      if (Loads::kEven || i + 1 < PER || ld.last)
-        __builtin_amdgcn_global_load_lds(ld.base[i] + (ld.off[i] + kb), (__attribute__((address_space(3))) void*)(base + (wave + i * NW) * 1024), 16, 0, 0);
+    for (int i = 0; i < PER; ++i) issue_one(s, i);
   };
 
   f32x16 acc[MI][J];
@@ -606,6 +607,19 @@ __device__ __forceinline__ void fp8_gemm_pair_tile(const GemmArgs& g, uint8_t* s
       const u32x4 hi = *reinterpret_cast<const u32x4*>(st + offa[k][1] + i * 32 * kQBK);
       af[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     }
+  };
+  // Fragment f of half k of stage s: B block f (f < J), else A block f - J.
+  auto read_one = [&](int s, int k, int f, i32x8 (&af)[MI], i32x8 (&bf)[J]) {
+    const uint8_t* st = smem + (s & 1) * kSlot;
+    const int off = f < J ? offb[k][0] + f * 32 * kQBK : offa[k][0] + (f - J) * 32 * kQBK;
+    const int off2 = f < J ? offb[k][1] + f * 32 * kQBK : offa[k][1] + (f - J) * 32 * kQBK;
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(st + off);
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(st + off2);
+    const i32x8 v{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    if (f < J)
+      bf[f] = v;
+    else
+      af[f - J] = v;
   };
   // Wait for this wave's LDS reads and for all but `later` stages of its
   // loads (PER instructions a stage; waves without a slot kPerWave - 1 issue
@@ -652,16 +666,33 @@ __device__ __forceinline__ void fp8_gemm_pair_tile(const GemmArgs& g, uint8_t* s
     for (int qi = 0; qi < KB; ++qi) mfma_q(qi, a1, b1);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (kNext) bare_barrier();
-    if constexpr (kMore) issue(s + 2);
-    if constexpr (kNext) read_frags(s + 1, 0, a0, b0);
+    // Second half, in a fixed order: each MFMA followed by up to two of stage
+    // s+2's loads (the first four MFMAs carry them) and one of stage s+1's
+    // first-half fragments. Issuing all of the stage's loads at once after the
+    // barrier measured 2-4% slower on 4096^3 and the 3120-row qkv / MLP-up
+    // shapes (level on the one-round MLP-down and attention-out shapes).
+    constexpr int NQ = MI * J - KB;  // MFMAs after the barrier
+    constexpr int NF = J + MI;       // fragments of the next first half
 #pragma unroll
-    for (int qi = KB; qi < MI * J; ++qi) mfma_q(qi, a1, b1);
+    for (int t = 0; t < NQ; ++t) {
+      mfma_q(KB + t, a1, b1);
+      if constexpr (kMore) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          if (2 * t + u < PER) issue_one(s + 2, 2 * t + u);
+      }
+      if constexpr (kNext) {
+        if (t < NF) read_one(s + 1, 0, t, a0, b0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
     if constexpr (kNext) {
 #pragma unroll
-      for (int qi = KB; qi < MI * J; ++qi) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-      }
+      for (int f = NQ; f < NF; ++f) read_one(s + 1, 0, f, a0, b0);
+    }
+    if constexpr (kMore) {
+#pragma unroll
+      for (int i = 2 * NQ; i < PER; ++i) issue_one(s + 2, i);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
