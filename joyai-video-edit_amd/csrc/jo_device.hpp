@@ -184,6 +184,22 @@ __device__ __forceinline__ void st8_nt(void* p, const u32x2& v) {
   __builtin_nontemporal_store(v, static_cast<u32x2*>(p));
 }
 
+// 16-byte store with the system-scope nontemporal policy (sc0 sc1 nt: the
+// line is written through rather than left dirty in L2), through a raw
+// buffer resource. `base` must be wave-uniform (a row base computed from the
+// wave index), so that the resource lives in scalar registers; `off` is the
+// lane's byte offset from it, below 2^31. Measured on MI355X for the QK
+// kernels' in-place row stores: [1, 1560, 32, 128] with tables 10.26-10.52 ->
+// 10.01 us, [1, 3120, 32, 128] 17.65 -> 17.43-17.55 us, [1, 3510, 24, 128]
+// grid 15.83 -> 15.60-15.78 us; the ring-cache mode, whose k rows go to
+// another buffer, measured 0.8% slower with it and keeps st16_nt, as do the
+// other row kernels (bare streams of their shapes showed no gain).
+__device__ __forceinline__ void st16_sys_nt(const void* base, int off, const u32x4& v) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(base), static_cast<short>(0), 0x7fffffff, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 19);  // 19 = sc0 | nt | sc1
+}
+
 __device__ __forceinline__ const void* byte_off(const void* p, int64_t bytes) {
   return static_cast<const char*>(p) + bytes;
 }

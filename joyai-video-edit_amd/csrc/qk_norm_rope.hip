@@ -292,7 +292,10 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
             float so[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) so[j] = (xv[j] * rs) * elem<BF16>(wv[t], j);
-            st16_nt(kstg + e * 2, pack<BF16>(so));
+            if constexpr (MODE == kKvCache)
+              st16_nt(kstg + e * 2, pack<BF16>(so));
+            else
+              st16_sys_nt(kstg, e * 2, pack<BF16>(so));
           }
         }
         float o[8];
@@ -305,7 +308,13 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
           o[2 * i] = e0 * c[i] - e1 * s[i];
           o[2 * i + 1] = e0 * s[i] + e1 * c[i];
         }
-        if ((g0 + g) < groups && e < a.row_elems) st16_nt(dst[t] + e * 2, pack<BF16>(o));
+        if ((g0 + g) < groups && e < a.row_elems) {
+          // dst[t] is the wave's row base (wave-uniform: from the wave index).
+          if constexpr (MODE == kKvCache)
+            st16_nt(dst[t] + e * 2, pack<BF16>(o));
+          else
+            st16_sys_nt(dst[t], e * 2, pack<BF16>(o));
+        }
       }
     }
   }
