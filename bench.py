@@ -217,21 +217,22 @@ def time_gpu(cfg, steps: int, warmup: int, dev, use_graph: bool = True) -> dict:
 # modulation rows a kernel reads, through the cache, for every row), for input
 # rows that come in groups (per-head rows of a strided view) the rows per
 # group, the bytes between groups and the offset of the first row, and an
-# extra output of 8 bytes per 16 read (an fp8 row next to a bf16 one). The
-# entry named S_<cfg> is the kernel's own access shape; entries named
+# extra output of 8 bytes per 16 read (an fp8 row next to a bf16 one), and
+# whether the 16-byte row stores are written through (wt, as the in-place QK
+# kernels store their rows). The entry named S_<cfg> is the kernel's own access shape; entries named
 # S_<cfg>@<what> are other shapes of the same bytes (@LPRxCH) or the shape
 # without the cached row reads (@no-weight, @no-mod) or without the stride
 # (@contiguous).
 # ---------------------------------------------------------------------------
 Stream = collections.namedtuple(
-    "Stream", "cfg rows lpr ch nin nout outb nscal inplace nconst group gstride goff out8",
-    defaults=(0, 0, 0, 0, 0))
+    "Stream", "cfg rows lpr ch nin nout outb nscal inplace nconst group gstride goff out8 wt",
+    defaults=(0, 0, 0, 0, 0, False))
 
 _S = Stream
 STREAMS = {
-    "S_C0": _S("C0", 3510 * 4, 64, 3, 1, 1, 16, 0, True),
-    "S_C0@64x1": _S("C0", 3510 * 12, 64, 1, 1, 1, 16, 0, True),
-    "S_C0@64x2": _S("C0", 3510 * 6, 64, 2, 1, 1, 16, 0, True),
+    "S_C0": _S("C0", 3510 * 4, 64, 3, 1, 1, 16, 0, True, wt=True),
+    "S_C0@64x1": _S("C0", 3510 * 12, 64, 1, 1, 1, 16, 0, True, wt=True),
+    "S_C0@64x2": _S("C0", 3510 * 6, 64, 2, 1, 1, 16, 0, True, wt=True),
     "S_C1": _S("C1", 10530, 64, 6, 1, 1, 8, 1, False),
     "S_C1@128x3": _S("C1", 10530, 128, 3, 1, 1, 8, 1, False),
     "S_C2": _S("C2", 10530, 128, 3, 2, 2, 16, 0, False, 2),
@@ -261,14 +262,14 @@ STREAMS = {
     "S_R_kn@contiguous": _S("R_kn", 99840, 16, 1, 1, 1, 16, 0, False, 1),
     "S_R_ln": _S("R_ln", 3120, 256, 2, 3, 1, 16, 0, False),
     "S_R_ln@64x8": _S("R_ln", 3120, 64, 8, 3, 1, 16, 0, False),
-    "S_R_qk": _S("R_qk", 3120 * 8, 64, 2, 1, 1, 16, 0, True),
+    "S_R_qk": _S("R_qk", 3120 * 8, 64, 2, 1, 1, 16, 0, True, wt=True),
     # q and k rows in place, and for the k rows the pre-RoPE stage as well:
     # on average one row read, one and a half written.
-    "S_R_qks": _S("R_qks", 3120 * 8, 64, 2, 1, 1, 16, 0, True, out8=1),
+    "S_R_qks": _S("R_qks", 3120 * 8, 64, 2, 1, 1, 16, 0, True, out8=1, wt=True),
     "S_T_rms": _S("T_rms", 4096, 64, 8, 1, 1, 16, 0, False, 1),
     "S_T_rms@no-weight": _S("T_rms", 4096, 64, 8, 1, 1, 16, 0, False),
     "S_T_ln": _S("T_ln", 4096, 256, 2, 3, 1, 16, 0, False),
-    "S_T_qk": _S("T_qk", 1560 * 8, 64, 2, 1, 1, 16, 0, True),
+    "S_T_qk": _S("T_qk", 1560 * 8, 64, 2, 1, 1, 16, 0, True, wt=True),
 }
 
 _STREAM_LIB = None
@@ -281,7 +282,7 @@ def stream_lib():
         path = ROOT / "joyai-video-edit_amd" / "joyomni_ops" / "libjoyomni_stream.so"
         lib = ctypes.CDLL(str(path))
         P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
-        lib.jo_stream_rows.argtypes = [P, P, P, I64, I, I, I, I, I, I, I, I, I64, I64, P]
+        lib.jo_stream_rows.argtypes = [P, P, P, I64, I, I, I, I, I, I, I, I, I64, I64, I, P]
         lib.jo_stream_rows.restype = I
         _STREAM_LIB = lib
     return _STREAM_LIB
@@ -332,7 +333,7 @@ def time_stream(spec, steps: int, warmup: int, dev) -> dict:
         pin, pout = ptrs[i % n_sets]
         rc = lib.jo_stream_rows(pin, pout, scal.data_ptr() if spec.nscal else None, spec.rows,
                                 spec.lpr, spec.ch, spec.nin, spec.nout, spec.outb, spec.nscal,
-                                spec.nconst, spec.out8, spec.group, spec.gstride, h)
+                                spec.nconst, spec.out8, spec.group, spec.gstride, int(spec.wt), h)
         if rc != 0:
             raise RuntimeError(f"jo_stream_rows failed ({rc}) for {spec}")
 

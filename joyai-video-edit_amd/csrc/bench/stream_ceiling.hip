@@ -20,6 +20,8 @@
 // every row uses, read through the cache by every row as the kernels do)
 // follow the row inputs in in[]; OUT8 adds an output stream of 8 bytes per 16
 // read (an fp8 row next to a bf16 one) after the NOUT outputs in out[].
+// With `wt` set, the 16-byte row stores use the system-scope nontemporal
+// policy (jo::st16_sys_nt) as the in-place QK kernels' row stores do.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -38,6 +40,7 @@ struct StreamArgs {
   uint32_t group_rows;    // input rows per contiguous group (0: all rows contiguous)
   int64_t group_stride;   // bytes between groups
   int nscal;
+  int wt;            // 16-byte row stores written through (sc0 sc1 nt)
   uint32_t mask;     // 0 at run time; keeps the dependency opaque to the compiler
 };
 
@@ -97,10 +100,17 @@ __global__ __launch_bounds__(256) void stream_rows_kernel(const StreamArgs a) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const u32x4 v = c[o % NIN][i];
-      if constexpr (OUTB == 16)
-        jo::st16_nt(a.out[o] + row * kOut + (i * LPR + lane) * 16,
-                    u32x4{v.x ^ dep, v.y ^ dep, v.z ^ dep, v.w ^ dep});
-      else
+      if constexpr (OUTB == 16) {
+        const u32x4 sv{v.x ^ dep, v.y ^ dep, v.z ^ dep, v.w ^ dep};
+        if (a.wt) {
+          // the wave's first row as the (wave-uniform) base of the resource
+          const int64_t row0 = __builtin_amdgcn_readfirstlane(static_cast<int>(row));
+          jo::st16_sys_nt(a.out[o] + row0 * kOut,
+                          static_cast<int>((row - row0) * kOut + (i * LPR + lane) * 16), sv);
+        } else {
+          jo::st16_nt(a.out[o] + row * kOut + (i * LPR + lane) * 16, sv);
+        }
+      } else
         jo::st8_nt(a.out[o] + row * kOut + (i * LPR + lane) * 8,
                    u32x2{v.x ^ v.y ^ dep, v.z ^ v.w ^ dep});
     }
@@ -133,11 +143,13 @@ bool try_launch(int lpr, int ch, int nin, int nout, int outb, int nconst, int ou
 // Shapes measured by bench.py: (lanes per row, chunks per lane, row input
 // streams, output streams, bytes stored per 16 bytes read, row-invariant
 // inputs, extra 8-byte output). in[] holds nin + nconst pointers, out[]
-// nout + out8. Returns 0 on success, 1 for a shape that is not instantiated or
-// bad sizes, 3 for a launch error.
+// nout + out8; wt != 0 writes the 16-byte row stores through. Returns 0 on
+// success, 1 for a shape that is not instantiated or bad sizes, 3 for a
+// launch error.
 extern "C" int jo_stream_rows(const void* const* in, void* const* out, float* scal, int64_t rows,
                               int lpr, int ch, int nin, int nout, int outb, int nscal, int nconst,
-                              int out8, int64_t group_rows, int64_t group_stride, void* stream) {
+                              int out8, int64_t group_rows, int64_t group_stride, int wt,
+                              void* stream) {
   if (rows <= 0 || rows > (int64_t{1} << 30)) return 1;
   if (group_rows < 0 || group_rows > (int64_t{1} << 30) || (group_rows && group_stride <= 0))
     return 1;
@@ -159,6 +171,7 @@ extern "C" int jo_stream_rows(const void* const* in, void* const* out, float* sc
   a.group_rows = static_cast<uint32_t>(group_rows);
   a.group_stride = group_stride;
   a.nscal = nscal;
+  a.wt = wt != 0;
   a.mask = 0u;
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define TRY(...) try_launch<__VA_ARGS__>(lpr, ch, nin, nout, outb, nconst, out8, a, st)

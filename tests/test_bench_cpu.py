@@ -90,15 +90,15 @@ def test_stream_library_rejects_bad_sizes_without_a_gpu(bench):
     pout = (ctypes.c_void_p * 3)()
     # rows <= 0, a group with no stride, too many streams, a shape that is not
     # instantiated
-    assert lib.jo_stream_rows(pin, pout, None, 0, 64, 6, 1, 1, 8, 1, 0, 0, 0, 0, None) == 1
-    assert lib.jo_stream_rows(pin, pout, None, 10, 16, 1, 1, 1, 16, 0, 1, 0, 32, 0, None) == 1
-    assert lib.jo_stream_rows(pin, pout, None, 10, 64, 6, 3, 1, 8, 1, 3, 0, 0, 0, None) == 1
-    assert lib.jo_stream_rows(pin, pout, None, 10, 64, 5, 1, 1, 8, 1, 0, 0, 0, 0, None) == 1
+    assert lib.jo_stream_rows(pin, pout, None, 0, 64, 6, 1, 1, 8, 1, 0, 0, 0, 0, 0, None) == 1
+    assert lib.jo_stream_rows(pin, pout, None, 10, 16, 1, 1, 1, 16, 0, 1, 0, 32, 0, 0, None) == 1
+    assert lib.jo_stream_rows(pin, pout, None, 10, 64, 6, 3, 1, 8, 1, 3, 0, 0, 0, 0, None) == 1
+    assert lib.jo_stream_rows(pin, pout, None, 10, 64, 5, 1, 1, 8, 1, 0, 0, 0, 0, 0, None) == 1
     # null stream pointers and a missing scale buffer
-    assert lib.jo_stream_rows(pin, pout, None, 10, 64, 6, 1, 1, 8, 0, 0, 0, 0, 0, None) == 1
+    assert lib.jo_stream_rows(pin, pout, None, 10, 64, 6, 1, 1, 8, 0, 0, 0, 0, 0, 0, None) == 1
     fake = (ctypes.c_void_p * 5)(*([16] * 5))
     fake_out = (ctypes.c_void_p * 3)(*([16] * 3))
-    assert lib.jo_stream_rows(fake, fake_out, None, 10, 64, 6, 1, 1, 8, 1, 0, 0, 0, 0, None) == 1
+    assert lib.jo_stream_rows(fake, fake_out, None, 10, 64, 6, 1, 1, 8, 1, 0, 0, 0, 0, 0, None) == 1
 
 
 def test_bench_refuses_more_than_one_gpu():
