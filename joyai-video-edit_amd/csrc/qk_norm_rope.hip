@@ -330,10 +330,13 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
 // quarters of two or more ([1, 3120, 32, 128] tables 18.6 -> 18.0 us,
 // [1, 1560, 32, 128] 11.3 -> 10.4 us); with 24 heads (six groups) a quarter
 // would be 1.5 groups and it costs ([1, 3510, 24, 128] 16.1 -> 18.5 us); six
-// (thirds) measured level with four there; twelve (one head group per wave)
-// no better than four ([1, 3510, 24, 128] 16.4 -> 16.3 us, C3 42.6 -> 43.0 us),
-// sixteen at 32 heads level with eight. The JO_KNOB_QK_SPLIT override (1, 2,
-// 4, 6, 8) forces the choice (launch shape only; results are identical).
+// (thirds of two groups each) is faster there once the in-place rows are
+// stored through ([1, 3510, 24, 128] grid 15.63 -> 15.35 us; with the plain
+// nontemporal stores it measured level with four) but not at 10530 tokens
+// (C3 41.65 -> 41.84 us); twelve (one head group per wave) measured no better
+// than four ([1, 3510, 24, 128] 16.4 -> 16.3 us, C3 42.6 -> 43.0 us), sixteen
+// at 32 heads level with eight. The JO_KNOB_QK_SPLIT override (1, 2, 4, 6, 8)
+// forces the choice (launch shape only; results are identical).
 int qk_split(int64_t tokens, int all_groups) {
   const int forced = launch_knob(JO_KNOB_QK_SPLIT);
   if (forced == 1 || forced == 2) return forced;
@@ -341,7 +344,9 @@ int qk_split(int64_t tokens, int all_groups) {
   if (forced == 6 && all_groups >= 3) return 6;
   if (forced == 4 || forced == 6 || forced == 8) return all_groups >= 2 ? 4 : 2;
   if (all_groups < 2) return 2;
-  return (tokens < 8192 && all_groups >= 8 && all_groups % 4 == 0) ? 8 : 4;
+  if (tokens < 8192 && all_groups >= 8 && all_groups % 4 == 0) return 8;
+  if (tokens < 8192 && all_groups >= 6 && all_groups % 3 == 0) return 6;
+  return 4;
 }
 
 template <int MODE, bool STAGE = false>
