@@ -219,21 +219,22 @@ def time_gpu(cfg, steps: int, warmup: int, dev, use_graph: bool = True) -> dict:
 # group, the bytes between groups and the offset of the first row, and an
 # extra output of 8 bytes per 16 read (an fp8 row next to a bf16 one), and
 # whether the 16-byte row stores are written through (wt, as the in-place QK
-# kernels store their rows). The entry named S_<cfg> is the kernel's own access shape; entries named
+# kernels store their rows) and whether workgroups take their rows in the
+# XCD-grouped order of the per-token quantizer (xcd). The entry named S_<cfg> is the kernel's own access shape; entries named
 # S_<cfg>@<what> are other shapes of the same bytes (@LPRxCH) or the shape
 # without the cached row reads (@no-weight, @no-mod) or without the stride
 # (@contiguous).
 # ---------------------------------------------------------------------------
 Stream = collections.namedtuple(
-    "Stream", "cfg rows lpr ch nin nout outb nscal inplace nconst group gstride goff out8 wt",
-    defaults=(0, 0, 0, 0, 0, False))
+    "Stream", "cfg rows lpr ch nin nout outb nscal inplace nconst group gstride goff out8 wt xcd",
+    defaults=(0, 0, 0, 0, 0, False, False))
 
 _S = Stream
 STREAMS = {
     "S_C0": _S("C0", 3510 * 4, 64, 3, 1, 1, 16, 0, True, wt=True),
     "S_C0@64x1": _S("C0", 3510 * 12, 64, 1, 1, 1, 16, 0, True, wt=True),
     "S_C0@64x2": _S("C0", 3510 * 6, 64, 2, 1, 1, 16, 0, True, wt=True),
-    "S_C1": _S("C1", 10530, 64, 6, 1, 1, 8, 1, False),
+    "S_C1": _S("C1", 10530, 64, 6, 1, 1, 8, 1, False, xcd=True),
     "S_C1@128x3": _S("C1", 10530, 128, 3, 1, 1, 8, 1, False),
     "S_C2": _S("C2", 10530, 128, 3, 2, 2, 16, 0, False, 2),
     "S_C2@no-mod": _S("C2", 10530, 128, 3, 2, 2, 16, 0, False),
@@ -333,7 +334,8 @@ def time_stream(spec, steps: int, warmup: int, dev) -> dict:
         pin, pout = ptrs[i % n_sets]
         rc = lib.jo_stream_rows(pin, pout, scal.data_ptr() if spec.nscal else None, spec.rows,
                                 spec.lpr, spec.ch, spec.nin, spec.nout, spec.outb, spec.nscal,
-                                spec.nconst, spec.out8, spec.group, spec.gstride, int(spec.wt), h)
+                                spec.nconst, spec.out8, spec.group, spec.gstride,
+                                int(spec.wt) | (int(spec.xcd) << 1), h)
         if rc != 0:
             raise RuntimeError(f"jo_stream_rows failed ({rc}) for {spec}")
 

@@ -20,8 +20,10 @@
 // every row uses, read through the cache by every row as the kernels do)
 // follow the row inputs in in[]; OUT8 adds an output stream of 8 bytes per 16
 // read (an fp8 row next to a bf16 one) after the NOUT outputs in out[].
-// With `wt` set, the 16-byte row stores use the system-scope nontemporal
-// policy (jo::st16_sys_nt) as the in-place QK kernels' row stores do.
+// flags bit 0 (wt): the 16-byte row stores use the system-scope nontemporal
+// policy (jo::st16_sys_nt), as the in-place QK kernels' row stores do; bit 1
+// (xcd): workgroups take their row blocks in jo::xcd_row_block order, as the
+// per-token quantizer does.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -41,6 +43,7 @@ struct StreamArgs {
   int64_t group_stride;   // bytes between groups
   int nscal;
   int wt;            // 16-byte row stores written through (sc0 sc1 nt)
+  int xcd;           // row blocks in xcd_row_block order
   uint32_t mask;     // 0 at run time; keeps the dependency opaque to the compiler
 };
 
@@ -51,7 +54,8 @@ __global__ __launch_bounds__(256) void stream_rows_kernel(const StreamArgs a) {
   constexpr int64_t kIn = int64_t(LPR) * CH * 16;
   constexpr int64_t kOut = int64_t(LPR) * CH * OUTB;
   const int lane = threadIdx.x % LPR;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
+  const int64_t blk = a.xcd ? jo::xcd_row_block<RPB>(blockIdx.x, gridDim.x) : blockIdx.x;
+  const int64_t row = blk * RPB + threadIdx.x / LPR;
   const bool ok = row < a.rows;
   u32x4 w[NCONST > 0 ? NCONST : 1][CH];
 #pragma unroll
@@ -143,12 +147,12 @@ bool try_launch(int lpr, int ch, int nin, int nout, int outb, int nconst, int ou
 // Shapes measured by bench.py: (lanes per row, chunks per lane, row input
 // streams, output streams, bytes stored per 16 bytes read, row-invariant
 // inputs, extra 8-byte output). in[] holds nin + nconst pointers, out[]
-// nout + out8; wt != 0 writes the 16-byte row stores through. Returns 0 on
+// nout + out8; flags as StreamArgs.wt (bit 0) and .xcd (bit 1). Returns 0 on
 // success, 1 for a shape that is not instantiated or bad sizes, 3 for a
 // launch error.
 extern "C" int jo_stream_rows(const void* const* in, void* const* out, float* scal, int64_t rows,
                               int lpr, int ch, int nin, int nout, int outb, int nscal, int nconst,
-                              int out8, int64_t group_rows, int64_t group_stride, int wt,
+                              int out8, int64_t group_rows, int64_t group_stride, int flags,
                               void* stream) {
   if (rows <= 0 || rows > (int64_t{1} << 30)) return 1;
   if (group_rows < 0 || group_rows > (int64_t{1} << 30) || (group_rows && group_stride <= 0))
@@ -171,7 +175,9 @@ extern "C" int jo_stream_rows(const void* const* in, void* const* out, float* sc
   a.group_rows = static_cast<uint32_t>(group_rows);
   a.group_stride = group_stride;
   a.nscal = nscal;
-  a.wt = wt != 0;
+  if (flags & ~3) return 1;
+  a.wt = flags & 1;
+  a.xcd = (flags >> 1) & 1;
   a.mask = 0u;
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define TRY(...) try_launch<__VA_ARGS__>(lpr, ch, nin, nout, outb, nconst, out8, a, st)

@@ -502,6 +502,33 @@ __device__ __forceinline__ int wave_uniform_row() {
     return threadIdx.x / LPR;
 }
 
+// Row block of workgroup b (of nb) for kernels that also write a few fp32
+// scales per row. Workgroups are dispatched round-robin over the 8 XCDs
+// (workgroup b runs on XCD b % 8), so in launch order the scales of 32
+// consecutive rows (one 128-byte line) would come from 8 XCDs, and each
+// XCD's L2 would write its part of the line back on its own. Within every
+// block of 8*G workgroups the index is transposed so that each XCD runs G
+// consecutive workgroups, i.e. 32 consecutive rows and whole lines of
+// scales; workgroups after the last whole block keep their order. The rows
+// and outputs stream as before (the 8 XCDs still work on one window of
+// 8*G*RPB consecutive rows). Measured on MI355X with bare streams of the
+// shape [10530, 3072] bf16 -> fp8 + 4-byte scales: 17.05 -> 16.89 us (the
+// scale stores' cost drops from ~0.2 us to ~0.05 us; without scales the
+// order changes nothing), and with the per-token quantizer on it
+// 17.27 -> 17.10 us. Used there only: the same order measured level for the
+// RMSNorm -> FP8 kernels and the FP8 epilogue of the residual + LayerNorm
+// kernel, slower for the RMSNorm -> FP8 per-block kernel at [4725, 3072]
+// (9.6-9.9 -> 10.1 us) and for two-wave rows ([3120, 4096]: 7.7 -> 9.4 us).
+template <int RPB>
+__device__ __forceinline__ int64_t xcd_row_block(int64_t b, int64_t nb) {
+  static_assert(RPB >= 1 && RPB <= 32 && (RPB & (RPB - 1)) == 0, "rows per workgroup");
+  constexpr int64_t G = 32 / RPB;
+  constexpr int64_t kSpan = 8 * G;
+  if (b >= (nb / kSpan) * kSpan) return b;
+  const int64_t l = b % kSpan;
+  return (b - l) + (l % 8) * G + l / 8;
+}
+
 // Block-wide reduction for the generic (one row per block) kernels.
 template <class Op>
 __device__ __forceinline__ float block_reduce(float v, float* slot) {

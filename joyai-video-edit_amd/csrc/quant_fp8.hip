@@ -30,7 +30,9 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restri
   __shared__ float red[kBlock / kWave];
   __shared__ float red2[kBlock / kWave];
   const int lane = threadIdx.x % LPR;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + wave_uniform_row<LPR>();
+  // One-wave rows: whole lines of scales per XCD (see xcd_row_block).
+  const int64_t blk = LPR == kWave ? xcd_row_block<RPB>(blockIdx.x, gridDim.x) : blockIdx.x;
+  const int64_t row = blk * RPB + wave_uniform_row<LPR>();
   const bool row_ok = row < M;
   const void* xr = byte_off(x, row * xs * Tag::kBytes);
 

@@ -99,6 +99,8 @@ def test_stream_library_rejects_bad_sizes_without_a_gpu(bench):
     fake = (ctypes.c_void_p * 5)(*([16] * 5))
     fake_out = (ctypes.c_void_p * 3)(*([16] * 3))
     assert lib.jo_stream_rows(fake, fake_out, None, 10, 64, 6, 1, 1, 8, 1, 0, 0, 0, 0, 0, None) == 1
+    # flags other than bit 0 (write-through stores) and bit 1 (XCD row order)
+    assert lib.jo_stream_rows(fake, fake_out, None, 10, 64, 6, 1, 1, 8, 0, 0, 0, 0, 0, 4, None) == 1
 
 
 def test_bench_refuses_more_than_one_gpu():
