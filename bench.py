@@ -231,9 +231,9 @@ Stream = collections.namedtuple(
 
 _S = Stream
 STREAMS = {
-    "S_C0": _S("C0", 3510 * 4, 64, 3, 1, 1, 16, 0, True, wt=True),
+    "S_C0": _S("C0", 3510 * 6, 64, 2, 1, 1, 16, 0, True, wt=True),
     "S_C0@64x1": _S("C0", 3510 * 12, 64, 1, 1, 1, 16, 0, True, wt=True),
-    "S_C0@64x2": _S("C0", 3510 * 6, 64, 2, 1, 1, 16, 0, True, wt=True),
+    "S_C0@64x3": _S("C0", 3510 * 4, 64, 3, 1, 1, 16, 0, True, wt=True),
     "S_C1": _S("C1", 10530, 64, 6, 1, 1, 8, 1, False, xcd=True),
     "S_C1@128x3": _S("C1", 10530, 128, 3, 1, 1, 8, 1, False),
     "S_C2": _S("C2", 10530, 128, 3, 2, 2, 16, 0, False, 2),
