@@ -24,7 +24,10 @@ packed qkv plus the pre-RoPE K stage; its line adds the time of the two calls
 the reference makes). T_* are the shapes of
 the reference's own benchmark script (test_bench.py): rmsnorm and LayerNorm +
 modulation at [4096, 4096], table-mode QK at [1, 1560, 32, 128], the FP8 GEMM
-at 4096^3.
+at 4096^3. B_img is the image stream of one DiT block at the deployment shape
+(FP8 mode, attention output a fixed input) composed from the drop-in ops with
+the reference's caller glue and through the fused callers: per-block time of
+both (`reference_composition_us_per_call`, `us_per_call`).
 
 Timing: max(W, 20) eager warmup calls, K eager calls (eager_us_per_call),
 then max(K, 100) calls captured into one HIP graph. Five times: the graph is
@@ -525,6 +528,61 @@ def unfused_kstage_us(cfg, dev, iters: int = 20):
     return round(us, 1)
 
 
+def time_block(steps: int, warmup: int, dev, calls: int = 20) -> dict:
+    """B_img: the image stream of one DiT block at the deployment shape (FP8
+    mode, attention output a fixed input), composed from the drop-in ops with
+    the reference's caller glue (workloads.block_reference) and through the
+    fused callers (workloads.block_fused). Each composition: max(warmup, 3)
+    eager calls, then `calls` blocks captured into one HIP graph, replayed once
+    untimed and then timed, five times, interleaved with the other
+    composition's replays; per-block time = median replay / calls."""
+    import torch
+    from joyomni_ops import workloads as W
+    b = W.make_block(dev)
+    img_f = b["img"].clone()
+    runs = {"reference": lambda: W.block_reference(b, b["img"]),
+            "fused": lambda: W.block_fused(b, img_f)}
+    stream = torch.cuda.Stream(dev)
+    graphs = {}
+    for name, fn in runs.items():
+        with torch.cuda.stream(stream):
+            for _ in range(max(warmup, 3)):
+                fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(calls):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        graphs[name] = g
+    cur = torch.cuda.current_stream(dev)
+    per = {name: [] for name in graphs}
+    for _ in range(TIMED_REPLAYS):
+        for name, g in graphs.items():
+            g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(cur)
+            g.replay()
+            e1.record(cur)
+            torch.cuda.synchronize()
+            per[name].append(e0.elapsed_time(e1) * 1000.0 / calls)
+    del graphs
+    torch.cuda.empty_cache()
+    ref_us = statistics.median(per["reference"])
+    fused_us = statistics.median(per["fused"])
+    flops = W.block_flops()
+    d = W.BLOCK
+    return {"us_per_call": round(fused_us, 3), "reference_composition_us_per_call": round(ref_us, 3),
+            "reference_over_fused": round(ref_us / fused_us, 3),
+            "min_us_per_call": round(min(per["fused"]), 3),
+            "max_us_per_call": round(max(per["fused"]), 3),
+            "gemm_flops": flops, "block_tflops": round(flops / (fused_us * 1e-6) / 1e12, 1),
+            "timed_calls": calls * TIMED_REPLAYS, "timing": "hip-graph",
+            "shape": f"img [{d['B']}, {d['L']}, {d['D']}], {d['H']} heads x {d['Dh']}, "
+                     f"MLP {d['F']}; attention output a fixed input"}
+
+
 def cpu_fn(cfg):
     """The oracle's restatement of the reference formula for a config (CPU tensors)."""
     from oracle import ops
@@ -658,6 +716,8 @@ def main() -> int:
         names.insert(0, HEADLINE)
     results = {}
     for n in names:
+        if n == "B_img":
+            continue
         if n in STREAMS:
             log(f"{n}: timing bare stream")
             results[n] = time_stream(STREAMS[n], args.steps, args.warmup, dev)
@@ -689,6 +749,11 @@ def main() -> int:
                 results[n]["hipblaslt_tflops"] = round(flops / (ab[1] * 1e-6) / 1e12, 1)
                 results[n]["hipblaslt_over_ours"] = round(ab[1] / ab[0], 3)
         log(f"{n}: {results[n]}")
+
+    if "B_img" in names or not args.only:
+        log("B_img: timing the block compositions")
+        results["B_img"] = time_block(args.steps, args.warmup, dev)
+        log(f"B_img: {results['B_img']}")
 
     # Each config's stream ceiling: its kernel's own shape, and the fastest shape.
     for sname, spec in STREAMS.items():

@@ -329,3 +329,132 @@ def launch(cfg: Config, t: dict, stream_handle: int, freqs: torch.Tensor | None 
                       gw, d["t0"], 0.0, stream_handle)
     else:
         raise ValueError(cfg.op)
+
+
+# ---------------------------------------------------------------------------
+# B_img: the image stream of one MMDoubleStreamBlock (dit.py:351-457) in FP8
+# mode at the deployment shape, attention excluded, composed twice from this
+# package's ops:
+#   block_reference  the calls the reference's forward makes, with its caller
+#                    glue (sgl_fused_ops.py:30-117, fp8_linear.py:155-169):
+#                    expanded modulation rows, .contiguous() q / k copies and
+#                    halved bf16 rotation tables, the drop-in kernels;
+#   block_fused      the same computation through the fused callers: LayerNorm
+#                    + AdaLN with the FP8 epilogue, QK norm + RoPE from grid
+#                    positions in place on the packed qkv, gated residual +
+#                    LayerNorm + AdaLN + FP8 in one pass.
+# The attention output is a fixed input (the stand-in for flash attention), so
+# the residual stream of the two compositions is bit-identical; q and k differ
+# only by the bf16 rounding of the reference's rotation tables.
+# ---------------------------------------------------------------------------
+BLOCK = dict(B=1, L=3120, D=4096, H=32, Dh=128, F=16384, grid=(30, 52), t0=0,
+             rope_dims=(44, 42, 42), theta=10000.0, eps=1e-6)
+
+
+def _fp8_weight(n: int, k: int, g: torch.Generator, device) -> tuple:
+    from .dit_ops import quantize_weight_per_channel
+    w = (torch.randn(n, k, generator=g, device=device) * (k ** -0.5)).to(torch.bfloat16)
+    w_q, w_s = quantize_weight_per_channel(w)
+    bias = (0.02 * torch.randn(n, generator=g, device=device)).to(torch.bfloat16)
+    return w_q, w_s, bias
+
+
+def grid_freqs_cis(L: int, head_dim: int, grid_hw, t0: int, rope_dims, theta: float,
+                   device) -> tuple:
+    """(cos, sin) fp32 [1, L, head_dim] as Transformer3DModel passes vis_freqs_cis
+    (dit.py:745-783, 918-933: per-axis angles pos * 1/theta^(2j/dim) for the t, h,
+    w pairs of token n = (f, h, w), each repeated for the two elements of its
+    pair), source id 0."""
+    from . import rope_freqs
+    gh, gw = grid_hw
+    freqs = rope_freqs(head_dim, rope_dims, theta)[0].to(device)
+    n = torch.arange(L, device=device)
+    per = gh * gw
+    pos = torch.stack([(t0 + n // per).float(), ((n % per) // gw).float(), (n % gw).float()], 1)
+    pt, ph = rope_dims[0] // 2, rope_dims[1] // 2
+    axis = torch.zeros(head_dim // 2, dtype=torch.long, device=device)
+    axis[pt:pt + ph] = 1
+    axis[pt + ph:] = 2
+    ang = pos[:, axis] * freqs.unsqueeze(0)
+    cos = ang.cos().repeat_interleave(2, 1).unsqueeze(0).contiguous()
+    sin = ang.sin().repeat_interleave(2, 1).unsqueeze(0).contiguous()
+    return cos, sin
+
+
+def make_block(device, seed: int = 22) -> dict:
+    """Seeded block inputs on `device`: residual stream, modulation vectors,
+    attention stand-in, q / k norm weights, FP8 weights of the four Linears
+    (Fp8Linear.from_linear's per-channel quantization) and the rotation tables."""
+    d = BLOCK
+    g = torch.Generator(device=device).manual_seed(seed)
+    B, L, D, F = d["B"], d["L"], d["D"], d["F"]
+    out = {"img": torch.randn(B, L, D, generator=g, device=device).to(torch.bfloat16),
+           "attn": torch.randn(B, L, D, generator=g, device=device).to(torch.bfloat16)}
+    for name in ("shift1", "scale1", "gate1", "shift2", "scale2", "gate2"):
+        out[name] = (0.2 * torch.randn(B, D, generator=g, device=device)).to(torch.bfloat16)
+    out["q_norm"] = (1 + 0.1 * torch.randn(d["Dh"], generator=g, device=device)).to(torch.bfloat16)
+    out["k_norm"] = (1 + 0.1 * torch.randn(d["Dh"], generator=g, device=device)).to(torch.bfloat16)
+    out["qkv"] = _fp8_weight(3 * D, D, g, device)
+    out["proj"] = _fp8_weight(D, D, g, device)
+    out["up"] = _fp8_weight(F, D, g, device)
+    out["down"] = _fp8_weight(D, F, g, device)
+    out["freqs_cis"] = grid_freqs_cis(L, d["Dh"], d["grid"], d["t0"], d["rope_dims"],
+                                      d["theta"], device)
+    return out
+
+
+def _ref_layernorm_modulate(x, shift, scale, eps):
+    """sgl_fused_ops.py:30-54: scale / shift expanded to [B*L, D] copies, then
+    fused_norm_scale_shift(..., "layer")."""
+    from . import fused_norm_scale_shift
+    B, L, D = x.shape
+    scale_2d = scale.unsqueeze(1).expand(B, L, D).reshape(-1, D).contiguous()
+    shift_2d = shift.unsqueeze(1).expand(B, L, D).reshape(-1, D).contiguous()
+    return fused_norm_scale_shift(x.reshape(-1, D), None, None, scale_2d, shift_2d, "layer",
+                                  eps).reshape(B, L, D)
+
+
+def block_reference(b: dict, img: torch.Tensor):
+    """The image stream of dit.py:351-457 (FP8 on, K cached after RoPE) with the
+    reference's caller glue; returns (img', q, k). img is not modified."""
+    from . import dit_ops
+    d = BLOCK
+    B, L, D, H, Dh, eps = d["B"], d["L"], d["D"], d["H"], d["Dh"], d["eps"]
+    m = _ref_layernorm_modulate(img, b["shift1"], b["scale1"], eps)
+    qkv = dit_ops.fp8_linear(m, *b["qkv"])
+    iv = qkv.view(B, L, 3, H, Dh)
+    q, k = dit_ops.fused_qk_norm_rope_3d(iv[:, :, 0], iv[:, :, 1], b["q_norm"], b["k_norm"],
+                                         b["freqs_cis"], eps=eps)
+    img = dit_ops.fused_add_gate(img, dit_ops.fp8_linear(b["attn"], *b["proj"]), b["gate1"])
+    m2 = _ref_layernorm_modulate(img, b["shift2"], b["scale2"], eps)
+    h = torch.nn.functional.gelu(dit_ops.fp8_linear(m2, *b["up"]), approximate="tanh")
+    img = dit_ops.fused_add_gate(img, dit_ops.fp8_linear(h, *b["down"]), b["gate2"])
+    return img, q, k
+
+
+def block_fused(b: dict, img: torch.Tensor):
+    """block_reference through the fused callers; img (contiguous) is updated in
+    place and returned as (img', q, k), q / k being views of the packed qkv."""
+    from . import dit_ops
+    d = BLOCK
+    B, L, D, H, Dh, eps = d["B"], d["L"], d["D"], d["H"], d["Dh"], d["eps"]
+    x_q, x_s = dit_ops.layernorm_modulate_fp8(img, b["shift1"], b["scale1"], eps=eps)
+    qkv = dit_ops.fp8_linear_quantized(x_q, x_s, *b["qkv"]).view(B, L, 3, H, Dh)
+    q, k = dit_ops.fused_qk_norm_rope_3d_grid_views(
+        qkv[:, :, 0], qkv[:, :, 1], b["q_norm"], b["k_norm"], grid_hw=d["grid"], t0=d["t0"],
+        rope_dims=d["rope_dims"], theta=d["theta"], eps=eps)
+    proj = dit_ops.fp8_linear(b["attn"], *b["proj"]).view(B, L, D)
+    img, x_q, x_s = dit_ops.fused_add_gate_layernorm_modulate_fp8(
+        img, proj, b["gate1"], b["shift2"], b["scale2"], eps=eps)
+    h = torch.nn.functional.gelu(dit_ops.fp8_linear_quantized(x_q, x_s, *b["up"]),
+                                 approximate="tanh")
+    img = dit_ops.fused_add_gate(img, dit_ops.fp8_linear(h, *b["down"]).view(B, L, D),
+                                 b["gate2"])
+    return img, q, k
+
+
+def block_flops() -> int:
+    """Matrix-core flops of the block's four FP8 GEMMs."""
+    d = BLOCK
+    M, D, F = d["B"] * d["L"], d["D"], d["F"]
+    return 2 * M * D * (3 * D + D + F + F)
