@@ -24,7 +24,10 @@ packed qkv plus the pre-RoPE K stage; its line adds the time of the two calls
 the reference makes). T_* are the shapes of
 the reference's own benchmark script (test_bench.py): rmsnorm and LayerNorm +
 modulation at [4096, 4096], table-mode QK at [1, 1560, 32, 128], the FP8 GEMM
-at 4096^3. B_img is the image stream of one DiT block at the deployment shape
+at 4096^3. R_gq is the MLP activation gelu(h, approximate="tanh") fused with the
+down-projection's per-token FP8 quantization at [3120, 16384]; its line adds
+the time of the two calls the reference makes (torch's GELU, then the quant).
+B_img is the image stream of one DiT block at the deployment shape
 (FP8 mode, attention output a fixed input) composed from the drop-in ops with
 the reference's caller glue and through the fused callers: per-block time of
 both (`reference_composition_us_per_call`, `us_per_call`).
@@ -258,6 +261,7 @@ STREAMS = {
     "S_R_q4k": _S("R_q4k", 3120, 128, 4, 1, 1, 8, 1, False),
     "S_R_q4k@64x8": _S("R_q4k", 3120, 64, 8, 1, 1, 8, 1, False),
     "S_R_q16k": _S("R_q16k", 3120, 256, 8, 1, 1, 8, 1, False),
+    "S_R_gq": _S("R_gq", 3120, 256, 8, 1, 1, 8, 1, False),
     "S_R_rms": _S("R_rms", 99840, 16, 1, 1, 1, 16, 0, False, 1),
     "S_R_rms@no-weight": _S("R_rms", 99840, 16, 1, 1, 1, 16, 0, False),
     # K slice of the packed qkv [1, 3120, 3, 32, 128]: 32 head rows of 256 B
@@ -528,6 +532,41 @@ def unfused_kstage_us(cfg, dev, iters: int = 20):
     return round(us, 1)
 
 
+def unfused_gelu_quant_us(cfg, dev, iters: int = 20):
+    """R_gq as two calls, the reference's order (dit.py:433 then fp8_linear.py:166):
+    torch.nn.functional.gelu(h, approximate="tanh") then sgl_per_token_quant_fp8
+    (this build's op) on its bf16 output, eager, per call."""
+    if cfg.op != "gelu_quant":
+        return None
+    import torch
+
+    import joyomni_ops as jo
+    from joyomni_ops import workloads as W
+    sets = []
+    for _ in range(4):
+        t = {k: v.to(dev) for k, v in W.make_inputs(cfg).items()}
+        t.update(W.alloc_outputs(cfg, t))
+        sets.append(t)
+
+    def call(t):
+        jo.sgl_per_token_quant_fp8(torch.nn.functional.gelu(t["x"], approximate="tanh"),
+                                   t["q"], t["s"])
+
+    for i in range(4):
+        call(sets[i])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(iters):
+        call(sets[i % 4])
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / iters
+    del sets
+    torch.cuda.empty_cache()
+    return round(us, 1)
+
+
 def time_block(steps: int, warmup: int, dev, calls: int = 20) -> dict:
     """B_img: the image stream of one DiT block at the deployment shape (FP8
     mode, attention output a fixed input), composed from the drop-in ops with
@@ -732,7 +771,8 @@ def main() -> int:
         caller_us = None if args.no_compare else copy_then_rmsnorm_us(cfg, dev)
         if caller_us is not None:
             results[n]["copy_then_rmsnorm_us_per_call"] = caller_us
-        two_call_us = None if args.no_compare else unfused_kstage_us(cfg, dev)
+        two_call_us = None if args.no_compare else (unfused_kstage_us(cfg, dev)
+                                                    or unfused_gelu_quant_us(cfg, dev))
         if two_call_us is not None:
             results[n]["unfused_two_calls_us_per_call"] = two_call_us
         flops = W.algorithmic_flops(cfg)

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define JO_ABI_VERSION 2
+#define JO_ABI_VERSION 3
 
 /* Status codes. */
 #define JO_OK 0
@@ -287,6 +287,24 @@ int jo_fused_add_layernorm_scale_shift(const void* x, int64_t x_stride, void* re
 int jo_rmsnorm_quant_fp8(const void* x, int64_t x_stride, const void* weight, void* out_q,
                          int64_t q_stride, float* out_s, int64_t M, int64_t N, int dtype,
                          float eps, int64_t group_size, void* stream);
+
+/* ------------------------------------------------------------------------
+ * GELU (tanh approximation) + per-token FP8 e4m3 quantization of its output.
+ * No reference counterpart: it fuses the MLP activation of the DiT block's
+ * FP8 mode, torch.nn.functional.gelu(h, approximate="tanh")
+ * (deploy/xvideo/models/dit/dit.py:91-92,433), with the activation
+ * quantization of the following Fp8Linear.forward
+ * (deploy/xvideo/models/dit/fp8_linear.py:140-166, per_token_quant_fp8.cu:56-82).
+ *   a[r,j] = round_dtype(0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))), x = input[r,j]
+ *     (fp32, tanh rounded to fp32 before the 1 is added, as the formula);
+ *   then jo_sgl_per_token_quant_fp8's rule on the row a[r,:].
+ * output_act (optional, may be NULL): the rounded activation a, row stride
+ * act_stride; the FP8 bytes and scales are those of jo_sgl_per_token_quant_fp8
+ * applied to it. Other arguments and limits as jo_sgl_per_token_quant_fp8.
+ * ------------------------------------------------------------------------ */
+int jo_gelu_tanh_quant_fp8(const void* input, int dtype, int64_t num_tokens, int64_t hidden_dim,
+                           int64_t in_stride, void* output_q, int64_t q_stride, float* output_s,
+                           void* output_act, int64_t act_stride, void* stream);
 
 /* ------------------------------------------------------------------------
  * (Gated residual add +) Layer|RMS norm + AdaLN, quantized per token to FP8

@@ -21,10 +21,40 @@ namespace {
 // rows wider than a wave) holding a non-finite row recomputes the
 // NaN-skipping maximum and clamps that row.
 // ---------------------------------------------------------------------------
-template <class Tag, int LPR, int CH>
+// GELU with the tanh approximation, the activation torch applies between the
+// MLP's two Fp8Linears (dit.py:91-92, 433):
+//   gelu(x) = 0.5 * x * (1 + tanh(u)),  u = sqrt(2/pi) * (x + 0.044715 * x^3),
+// in fp32 with the rounding structure of that formula where it matters: tanh(u)
+// is rounded to fp32 before 1 is added, so where 1 + tanh(u) cancels (x below
+// about -3) the result moves in steps of 2^-24 * 0.5|x| as the formula's own
+// evaluation does. u is formed as x (b + b k x^2) (one fma, 3 operations
+// instead of 5), tanh(|u|) = 1 - 2 / (exp(2|u|) + 1) from the hardware exp2 and
+// reciprocal (each within 1 ulp): exp overflows to inf for large |u|, giving
+// tanh = +-1. gelu(+inf) = inf, gelu(-inf) = NaN (0 * inf), NaN propagates;
+// the caller rounds the result to the row's dtype.
+__device__ __forceinline__ float gelu_tanh(float x) {
+#pragma clang fp contract(off)
+  constexpr float kBeta = 0.7978845608028654f;         // sqrt(2 / pi)
+  constexpr float kBetaKappa = 0.035677408136300125f;  // sqrt(2 / pi) * 0.044715
+  constexpr float kTwoLog2e = 2.8853900817779268f;     // 2 / ln 2
+  const float u = x * __builtin_fmaf(kBetaKappa, x * x, kBeta);
+  const float t = __builtin_amdgcn_exp2f(fabsf(u) * kTwoLog2e);  // exp(2|u|)
+  // 1 - tanh(|u|) = 2 / (t + 1) = 1 / (0.5 t + 0.5), the fma exact up to its one rounding
+  const float r = __builtin_amdgcn_rcpf(__builtin_fmaf(t, 0.5f, 0.5f));
+  const float th = copysignf(1.0f - r, u);                        // tanh(u)
+  return x * __builtin_fmaf(0.5f, th, 0.5f);  // 0.5 x (1 + tanh(u)), 0.5 (1 + th) exact
+}
+
+// ACT: the row is first replaced by gelu_tanh of it, rounded to the row's
+// dtype (the bf16 / fp16 tensor torch's activation would return), and that
+// row is quantized; when act is not null it is also stored there (row
+// stride as elements).
+template <class Tag, int LPR, int CH, bool ACT = false>
 __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restrict__ x, int64_t xs,
                                                             uint8_t* __restrict__ q, int64_t qs,
-                                                            float* __restrict__ s, int64_t M, int N) {
+                                                            float* __restrict__ s, int64_t M, int N,
+                                                            void* __restrict__ act = nullptr,
+                                                            int64_t as = 0) {
   static_assert(Tag::kVec == 8, "fp8 rows are built from 8-element chunks");
   constexpr int RPB = kBlock / LPR;
   __shared__ float red[kBlock / kWave];
@@ -42,6 +72,24 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restri
     const int e = (i * LPR + lane) * 8;
     c[i] = (row_ok && e < N) ? ld16_nt(byte_off(xr, static_cast<int64_t>(e) * Tag::kBytes))
                              : u32x4{0u, 0u, 0u, 0u};
+  }
+  if constexpr (ACT) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      float v[8];
+      unpack<Tag>(c[i], v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = gelu_tanh(v[j]);
+      c[i] = pack<Tag>(v);  // gelu(0) = 0 keeps the lanes past N at zero
+    }
+    if (act != nullptr && row_ok) {
+      char* ar = static_cast<char*>(act) + row * as * Tag::kBytes;
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int e = (i * LPR + lane) * 8;
+        if (e < N) st16_nt(ar + static_cast<int64_t>(e) * Tag::kBytes, c[i]);
+      }
+    }
   }
   float amax = 0.f;
 #pragma unroll
@@ -81,44 +129,61 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(const void* __restri
 
 // One row per workgroup, element-wise accesses: any hidden size and any
 // alignment (rows whose size is not a multiple of 8, or unaligned views).
-template <class Tag>
+template <class Tag, bool ACT>
+__device__ __forceinline__ float generic_value(const void* x, int64_t i) {
+  const float v = load_elem<Tag>(x, i);
+  if constexpr (ACT)
+    return round_to<Tag>(gelu_tanh(v));
+  else
+    return v;
+}
+
+template <class Tag, bool ACT = false>
 __global__ __launch_bounds__(kBlock) void quant_generic_kernel(const void* __restrict__ x,
                                                                int64_t xs, uint8_t* __restrict__ q,
                                                                int64_t qs, float* __restrict__ s,
-                                                               int N) {
+                                                               int N, void* __restrict__ act = nullptr,
+                                                               int64_t as = 0) {
   __shared__ float red[kBlock / kWave];
   const int64_t row = blockIdx.x;
   const int64_t xo = row * xs;
   float amax = 0.f;
-  for (int i = threadIdx.x; i < N; i += kBlock) amax = fmaxf(amax, fabsf(load_elem<Tag>(x, xo + i)));
+  for (int i = threadIdx.x; i < N; i += kBlock) {
+    const float v = generic_value<Tag, ACT>(x, xo + i);
+    amax = fmaxf(amax, fabsf(v));
+    if (ACT && act != nullptr) store_elem<Tag>(act, row * as + i, v);
+  }
   amax = block_reduce<OpAmax>(amax, red);
   const float scale = amax / kFp8Max;
   if (threadIdx.x == 0) s[row] = scale;
   const float inv = (scale == 0.f) ? 0.f : 1.0f / scale;
   uint8_t* qr = q + row * qs;
-  for (int i = threadIdx.x; i < N; i += kBlock) qr[i] = fp8_byte(load_elem<Tag>(x, xo + i) * inv);
+  for (int i = threadIdx.x; i < N; i += kBlock)
+    qr[i] = fp8_byte(generic_value<Tag, ACT>(x, xo + i) * inv);
 }
 
-template <class Tag>
+template <class Tag, bool ACT = false>
 int launch_quant(const void* x, int64_t M, int64_t N, int64_t xs, void* q, int64_t qs, float* s,
-                 hipStream_t stream) {
+                 hipStream_t stream, void* act = nullptr, int64_t as = 0,
+                 const char* op = "sgl_per_token_quant_fp8") {
   const bool vec_ok = (N % 8 == 0) && aligned(x, 16) && ((xs * Tag::kBytes) % 16 == 0) &&
-                      aligned(q, 8) && (qs % 8 == 0);
+                      aligned(q, 8) && (qs % 8 == 0) &&
+                      (act == nullptr || (aligned(act, 16) && (as * Tag::kBytes) % 16 == 0));
   bool launched = false;
   if (vec_ok) {
     launched = dispatch_row_shape<8, false, 128>(N, [&](auto lpr, auto ch) {
       constexpr int LPR = decltype(lpr)::value;
       constexpr int CH = decltype(ch)::value;
-      hipLaunchKernelGGL((quant_rows_kernel<Tag, LPR, CH>), dim3(row_blocks(M, LPR)), dim3(kBlock),
-                         0, stream, x, xs, static_cast<uint8_t*>(q), qs, s, M,
-                         static_cast<int>(N));
+      hipLaunchKernelGGL((quant_rows_kernel<Tag, LPR, CH, ACT>), dim3(row_blocks(M, LPR)),
+                         dim3(kBlock), 0, stream, x, xs, static_cast<uint8_t*>(q), qs, s, M,
+                         static_cast<int>(N), act, as);
     }, M);
   }
   if (!launched) {
-    hipLaunchKernelGGL((quant_generic_kernel<Tag>), dim3(M), dim3(kBlock), 0, stream, x, xs,
-                       static_cast<uint8_t*>(q), qs, s, static_cast<int>(N));
+    hipLaunchKernelGGL((quant_generic_kernel<Tag, ACT>), dim3(M), dim3(kBlock), 0, stream, x, xs,
+                       static_cast<uint8_t*>(q), qs, s, static_cast<int>(N), act, as);
   }
-  return launch_status("sgl_per_token_quant_fp8");
+  return launch_status(op);
 }
 
 // ---------------------------------------------------------------------------
@@ -522,6 +587,32 @@ extern "C" int jo_sgl_per_token_quant_fp8(const void* input, int dtype, int64_t 
                               output_s, st);
   return launch_quant<F16>(input, num_tokens, hidden_dim, in_stride, output_q, q_stride, output_s,
                            st);
+}
+
+extern "C" int jo_gelu_tanh_quant_fp8(const void* input, int dtype, int64_t num_tokens,
+                                     int64_t hidden_dim, int64_t in_stride, void* output_q,
+                                     int64_t q_stride, float* output_s, void* output_act,
+                                     int64_t act_stride, void* stream) {
+  JO_REQUIRE(dtype == JO_DTYPE_BF16 || dtype == JO_DTYPE_F16,
+             "gelu_tanh_quant_fp8: input must be bf16 or fp16");
+  JO_REQUIRE(num_tokens >= 0 && hidden_dim >= 0, "gelu_tanh_quant_fp8: negative size");
+  JO_REQUIRE(hidden_dim % 4 == 0, "hidden_dim must be divisible by 4, got %lld",
+             static_cast<long long>(hidden_dim));
+  JO_REQUIRE(hidden_dim <= INT32_MAX, "gelu_tanh_quant_fp8: hidden_dim too large");
+  JO_REQUIRE(num_tokens <= kMaxRows, "gelu_tanh_quant_fp8: shape too large (more than %lld rows)",
+             static_cast<long long>(kMaxRows));
+  JO_REQUIRE(in_stride >= hidden_dim && q_stride >= hidden_dim,
+             "gelu_tanh_quant_fp8: row stride smaller than hidden_dim");
+  JO_REQUIRE(output_act == nullptr || act_stride >= hidden_dim,
+             "gelu_tanh_quant_fp8: activation row stride smaller than hidden_dim");
+  if (num_tokens == 0) return JO_OK;
+  JO_REQUIRE(input && output_q && output_s, "gelu_tanh_quant_fp8: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == JO_DTYPE_BF16)
+    return launch_quant<BF16, true>(input, num_tokens, hidden_dim, in_stride, output_q, q_stride,
+                                    output_s, st, output_act, act_stride, "gelu_tanh_quant_fp8");
+  return launch_quant<F16, true>(input, num_tokens, hidden_dim, in_stride, output_q, q_stride,
+                                 output_s, st, output_act, act_stride, "gelu_tanh_quant_fp8");
 }
 
 extern "C" int jo_rmsnorm_quant_fp8(const void* x, int64_t x_stride, const void* weight,

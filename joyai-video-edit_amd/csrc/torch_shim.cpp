@@ -231,6 +231,44 @@ void sgl_per_token_quant_fp8(torch::Tensor input, torch::Tensor output_q,
 // ---------------------------------------------------------------------------
 // New ops.
 // ---------------------------------------------------------------------------
+// gelu(input, approximate="tanh") quantized per token as sgl_per_token_quant_fp8
+// would quantize it; output_act, when given, receives the activation itself.
+void gelu_tanh_quant_fp8(torch::Tensor input, torch::Tensor output_q, torch::Tensor output_s,
+                         const c10::optional<torch::Tensor>& output_act) {
+  JO_CHECK_CUDA(input);
+  JO_CHECK_CUDA(output_q);
+  JO_CHECK_CUDA(output_s);
+  TORCH_CHECK(input.dim() == 2 && input.stride(-1) == 1,
+              "input must be 2D [num_tokens, hidden_dim] with contiguous rows");
+  const int64_t num_tokens = input.size(0);
+  const int64_t hidden_dim = input.size(1);
+  TORCH_CHECK(hidden_dim % 4 == 0, "hidden_dim must be divisible by 4, got ", hidden_dim);
+  TORCH_CHECK(input.scalar_type() == torch::kBFloat16 || input.scalar_type() == torch::kFloat16,
+              "gelu_tanh_quant_fp8: input must be bf16 or fp16");
+  TORCH_CHECK(output_q.scalar_type() == at::kFloat8_e4m3fn, "output_q must be float8_e4m3fn");
+  TORCH_CHECK(output_q.is_contiguous() && output_q.numel() == input.numel(),
+              "output_q must be a contiguous tensor with input's number of elements");
+  TORCH_CHECK(output_s.scalar_type() == torch::kFloat32, "output_s must be float32");
+  TORCH_CHECK(output_s.is_contiguous() && output_s.numel() == num_tokens,
+              "output_s must be a contiguous tensor of num_tokens floats");
+  void* act = nullptr;
+  if (output_act.has_value()) {
+    const torch::Tensor& a = *output_act;
+    JO_CHECK_CUDA(a);
+    TORCH_CHECK(a.scalar_type() == input.scalar_type() && a.is_contiguous() &&
+                    a.numel() == input.numel(),
+                "output_act must be a contiguous tensor of input's dtype and size");
+    act = a.data_ptr();
+  }
+  if (num_tokens == 0) return;
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(input.device());
+  check_status(jo_gelu_tanh_quant_fp8(input.data_ptr(), dtype_code(input), num_tokens, hidden_dim,
+                                      row_stride(input), output_q.data_ptr(), hidden_dim,
+                                      output_s.data_ptr<float>(), act, hidden_dim,
+                                      current_stream(input)),
+               "gelu_tanh_quant_fp8");
+}
+// ---------------------------------------------------------------------------
 namespace {
 
 struct QKGeom {
@@ -744,6 +782,9 @@ TORCH_LIBRARY(joyomni_ops, m) {
   m.def(
       "kv_commit_rope(Tensor src_k, Tensor? src_v, Tensor(a!) dst_k, Tensor(b!)? dst_v, "
       "int dst_offset, Tensor cos, Tensor sin) -> ()");
+  m.def(
+      "gelu_tanh_quant_fp8(Tensor input, Tensor! output_q, Tensor! output_s, "
+      "Tensor(a!)? output_act=None) -> ()");
   m.def("apply_rotary_emb(Tensor x, Tensor cos, Tensor sin) -> Tensor");
   m.def("rmsnorm_heads(Tensor x, Tensor weight, float eps, int round_first) -> Tensor");
 }
@@ -763,6 +804,7 @@ TORCH_LIBRARY_IMPL(joyomni_ops, CUDA, m) {
   m.impl("rmsnorm_quant_fp8", &joyomni_ops::rmsnorm_quant_fp8);
   m.impl("norm_scale_shift_quant_fp8", &joyomni_ops::norm_scale_shift_quant_fp8);
   m.impl("kv_commit_rope", &joyomni_ops::kv_commit_rope);
+  m.impl("gelu_tanh_quant_fp8", &joyomni_ops::gelu_tanh_quant_fp8);
   m.impl("apply_rotary_emb", &joyomni_ops::apply_rotary_emb);
   m.impl("rmsnorm_heads", &joyomni_ops::rmsnorm_heads);
 }

@@ -52,6 +52,7 @@ __all__ = [
     "rmsnorm_heads",
     "fused_qk_norm_rope_3d_paired_kstage",
     "fused_qk_norm_rope_3d_grid_kstage",
+    "gelu_tanh_quant_fp8",
 ]
 
 _ops = torch.ops.joyomni_ops
@@ -87,6 +88,14 @@ def has_fp8() -> bool:
 
 def sgl_per_token_quant_fp8(input, output_q, output_s):
     _ops.sgl_per_token_quant_fp8(input, output_q, output_s)
+
+
+def gelu_tanh_quant_fp8(input, output_q, output_s, output_act=None):
+    """gelu(input, approximate="tanh") rounded to input's dtype, then quantized
+    per token as sgl_per_token_quant_fp8 does: input bf16/fp16 [M, K] with
+    contiguous rows, output_q fp8 [M, K], output_s fp32 [M] or [M, 1];
+    output_act (optional, input's dtype and size) receives the activation."""
+    _ops.gelu_tanh_quant_fp8(input, output_q, output_s, output_act)
 
 
 def fp8_scaled_mm(mat_a, mat_b, scales_a, scales_b, out_dtype, bias: Optional[torch.Tensor] = None):

@@ -38,6 +38,7 @@ _F = c_float
 SIGNATURES: dict[str, list] = {
     "jo_set_launch_override": [c_int, c_int],
     "jo_sgl_per_token_quant_fp8": [_P, c_int, _I64, _I64, _I64, _P, _I64, _P, _P],
+    "jo_gelu_tanh_quant_fp8": [_P, c_int, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P],
     "jo_fused_qk_norm_rope_3d_paired": [
         _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P, _P],
     "jo_fused_qk_norm_rope_3d_grid": [

@@ -33,6 +33,10 @@ Additional entry points for callers that can use the new fused ops:
   rms_norm_module           the torch RMSNorm module's forward (dit.py:244-249) that
                             the text stream applies to q and k (dit.py:384-385),
                             read from the packed qkv view.
+  gelu_quantize_activation_fp8  the MLP activation gelu(h, approximate="tanh")
+                            (dit.py:91-92, 433) and the quantization of the
+                            following Fp8Linear.forward in one pass (the bf16
+                            activation is never written).
   fp8_linear                Fp8Linear.forward (fp8_linear.py:155-169): per-token
                             quantization + fp8_scaled_mm; quantize_weight_per_channel
                             is its weight preparation (fp8_linear.py:100-110).
@@ -44,7 +48,7 @@ from typing import Optional, Sequence, Tuple
 import torch
 
 from . import (fp8_scaled_mm, fused_add_layernorm_scale_shift, fused_norm_scale_shift,
-               fused_qk_norm_rope_3d_grid, fused_qk_norm_rope_3d_grid_kstage,
+               fused_qk_norm_rope_3d_grid, fused_qk_norm_rope_3d_grid_kstage, gelu_tanh_quant_fp8,
                fused_qk_norm_rope_3d_paired, fused_qk_norm_rope_3d_paired_kstage,
                kv_commit_rope, norm_scale_shift_quant_fp8, rmsnorm, rmsnorm_heads,
                rope_freqs, sgl_per_token_quant_fp8)
@@ -293,6 +297,21 @@ def quantize_activation_fp8(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor
     x_q = torch.empty((M, K), device=x_2d.device, dtype=torch.float8_e4m3fn)
     x_scale = torch.empty((M, 1), device=x_2d.device, dtype=torch.float32)
     sgl_per_token_quant_fp8(x_2d, x_q, x_scale)
+    return x_q, x_scale
+
+
+def gelu_quantize_activation_fp8(h: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """quantize_activation_fp8(torch.nn.functional.gelu(h, approximate="tanh")) in
+    one pass (the MLP activation of dit.py:433 and the activation side of the
+    next Fp8Linear.forward, fp8_linear.py:140-166): h [..., K] bf16/fp16 ->
+    (x_q fp8 e4m3fn [M, K], x_scale fp32 [M, 1]). The activation is evaluated
+    in fp32 and rounded to h's dtype before it is quantized, as the two calls do."""
+    h_2d = h.reshape(-1, h.shape[-1])
+    if h_2d.stride(-1) != 1:
+        h_2d = h_2d.contiguous()
+    M, K = h_2d.shape
+    x_q, x_scale = _fp8_outputs(M, K, h_2d.device)
+    gelu_tanh_quant_fp8(h_2d, x_q, x_scale)
     return x_q, x_scale
 
 

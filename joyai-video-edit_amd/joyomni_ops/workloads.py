@@ -30,6 +30,8 @@ Deployment shapes through the reference-signature entry points (reported):
   R_kn    rmsnorm_qk_bf16's per-head norm read straight from the K slice of the
           packed qkv [1, 3120, 3, 32, 128] (jo_rmsnorm_heads; the reference
           first copies that slice with .contiguous())
+  R_gq    the MLP activation gelu(h, approximate="tanh") and the next Fp8Linear's
+          per-token FP8 quantization in one pass (gelu_tanh_quant_fp8), h [3120, 16384]
   R_qks   the K-cache-before-RoPE branch (dit.py:360-370) in one pass:
           fused_qk_norm_rope_3d_paired_kstage on the q / k slices of the packed
           qkv [1, 3120, 3, 32, 128], bf16 [3120, 64] tables, pre-RoPE K to a
@@ -90,6 +92,9 @@ CONFIGS: dict[str, Config] = {
     "R_rms": Config("R_rms", "rmsnorm", 14, dict(M=99840, N=128, eps=1e-6)),
     "R_kn": Config("R_kn", "rms_heads", 16, dict(B=1, L=3120, H=32, D=128, eps=1e-6)),
     "R_qks": Config("R_qks", "qk_kstage", 21, dict(B=1, L=3120, H=32, D=128, eps=1e-6)),
+    # MLP activation + the down-projection's FP8 quantization in one pass
+    # (gelu_tanh_quant_fp8) on the up-projection's output [3120, 16384]
+    "R_gq": Config("R_gq", "gelu_quant", 23, dict(M=3120, K=16384)),
     # The shapes of the reference's own benchmark script
     # (deploy/joyomni_ops/tests/test_bench.py:59-200); reported, not gated.
     "T_rms": Config("T_rms", "rmsnorm", 17, dict(M=4096, N=4096, eps=1e-6)),
@@ -129,6 +134,9 @@ def make_inputs(cfg: Config, device="cpu") -> dict:
                                          dtype=torch.bfloat16)
     elif cfg.op == "quant":
         out["x"] = with_outliers(torch.randn(d["M"], d["K"], generator=g), g).to(torch.bfloat16)
+    elif cfg.op == "gelu_quant":
+        # an up-projection output: N(0, 1) scaled by 2, with outliers
+        out["x"] = with_outliers(2 * torch.randn(d["M"], d["K"], generator=g), g).to(torch.bfloat16)
     elif cfg.op in ("add_ln", "add_ln_quant"):
         out["x"] = torch.randn(d["M"], d["N"], generator=g).to(torch.bfloat16)
         out["residual"] = torch.randn(d["M"], d["N"], generator=g).to(torch.bfloat16)
@@ -201,7 +209,7 @@ def algorithmic_bytes(cfg: Config) -> int:
         return 2 * d["M"] * d["N"] * 2 + d["N"] * 2        # x in, out, weight
     if cfg.op == "rms_heads":
         return 2 * d["B"] * d["L"] * d["H"] * d["D"] * 2 + d["D"] * 2   # K slice in, out, weight
-    if cfg.op == "quant":
+    if cfg.op in ("quant", "gelu_quant"):
         return d["M"] * d["K"] * 3 + d["M"] * 4            # bf16 in, fp8 out, scales
     if cfg.op == "add_ln":
         return 4 * d["M"] * d["N"] * 2 + 2 * d["N"] * 2    # x, res in; res, y out; mod rows
@@ -229,7 +237,7 @@ def algorithmic_flops(cfg: Config) -> int | None:
 def alloc_outputs(cfg: Config, inputs: dict) -> dict:
     d = cfg.dims
     dev = next(iter(inputs.values())).device
-    if cfg.op == "quant":
+    if cfg.op in ("quant", "gelu_quant"):
         return {"q": torch.empty(d["M"], d["K"], dtype=torch.float8_e4m3fn, device=dev),
                 "s": torch.empty(d["M"], dtype=torch.float32, device=dev)}
     if cfg.op == "rms_quant":
@@ -262,6 +270,9 @@ def launch(cfg: Config, t: dict, stream_handle: int, freqs: torch.Tensor | None 
     if cfg.op == "quant":
         _abi.call("jo_sgl_per_token_quant_fp8", p(t["x"]), _abi.JO_DTYPE_BF16, d["M"], d["K"],
                   d["K"], p(t["q"]), d["K"], p(t["s"]), stream_handle)
+    elif cfg.op == "gelu_quant":
+        _abi.call("jo_gelu_tanh_quant_fp8", p(t["x"]), _abi.JO_DTYPE_BF16, d["M"], d["K"], d["K"],
+                  p(t["q"]), d["K"], p(t["s"]), None, 0, stream_handle)
     elif cfg.op == "rms_quant":
         _abi.call("jo_rmsnorm_quant_fp8", p(t["x"]), d["N"], p(t["weight"]), p(t["q"]), d["N"],
                   p(t["s"]), d["M"], d["N"], _abi.JO_DTYPE_BF16, d["eps"], d["group"],
@@ -342,10 +353,13 @@ def launch(cfg: Config, t: dict, stream_handle: int, freqs: torch.Tensor | None 
 #   block_fused      the same computation through the fused callers: LayerNorm
 #                    + AdaLN with the FP8 epilogue, QK norm + RoPE from grid
 #                    positions in place on the packed qkv, gated residual +
-#                    LayerNorm + AdaLN + FP8 in one pass.
-# The attention output is a fixed input (the stand-in for flash attention), so
-# the residual stream of the two compositions is bit-identical; q and k differ
-# only by the bf16 rounding of the reference's rotation tables.
+#                    LayerNorm + AdaLN + FP8 in one pass, the MLP's GELU with
+#                    the next FP8 quantization in one pass.
+# The attention output is a fixed input (the stand-in for flash attention).
+# The residual stream of the two compositions agrees up to the GELU, which
+# torch and this package evaluate with different tanh implementations (each
+# within 1 bf16 ulp of the fp32 formula); q and k differ only by the bf16
+# rounding of the reference's rotation tables.
 # ---------------------------------------------------------------------------
 BLOCK = dict(B=1, L=3120, D=4096, H=32, Dh=128, F=16384, grid=(30, 52), t0=0,
              rope_dims=(44, 42, 42), theta=10000.0, eps=1e-6)
@@ -432,9 +446,11 @@ def block_reference(b: dict, img: torch.Tensor):
     return img, q, k
 
 
-def block_fused(b: dict, img: torch.Tensor):
+def block_fused(b: dict, img: torch.Tensor, fuse_gelu: bool = True):
     """block_reference through the fused callers; img (contiguous) is updated in
-    place and returned as (img', q, k), q / k being views of the packed qkv."""
+    place and returned as (img', q, k), q / k being views of the packed qkv.
+    fuse_gelu=False keeps torch's GELU and the separate quantization (then the
+    residual stream is bit-identical to block_reference's)."""
     from . import dit_ops
     d = BLOCK
     B, L, D, H, Dh, eps = d["B"], d["L"], d["D"], d["H"], d["Dh"], d["eps"]
@@ -446,10 +462,14 @@ def block_fused(b: dict, img: torch.Tensor):
     proj = dit_ops.fp8_linear(b["attn"], *b["proj"]).view(B, L, D)
     img, x_q, x_s = dit_ops.fused_add_gate_layernorm_modulate_fp8(
         img, proj, b["gate1"], b["shift2"], b["scale2"], eps=eps)
-    h = torch.nn.functional.gelu(dit_ops.fp8_linear_quantized(x_q, x_s, *b["up"]),
-                                 approximate="tanh")
-    img = dit_ops.fused_add_gate(img, dit_ops.fp8_linear(h, *b["down"]).view(B, L, D),
-                                 b["gate2"])
+    up = dit_ops.fp8_linear_quantized(x_q, x_s, *b["up"])
+    if fuse_gelu:
+        h_q, h_s = dit_ops.gelu_quantize_activation_fp8(up)
+    else:
+        h_q, h_s = dit_ops.quantize_activation_fp8(
+            torch.nn.functional.gelu(up, approximate="tanh"))
+    img = dit_ops.fused_add_gate(img, dit_ops.fp8_linear_quantized(h_q, h_s, *b["down"])
+                                 .view(B, L, D), b["gate2"])
     return img, q, k
 
 

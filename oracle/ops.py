@@ -49,6 +49,27 @@ def per_token_quant_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 
 
 # ---------------------------------------------------------------------------
+# MLP activation of the DiT block's FP8 mode, deploy/xvideo/models/dit/dit.py:91-92
+# and :433 (torch.nn.functional.gelu(h, approximate="tanh") on the up-projection's
+# bf16 output), followed by the next Fp8Linear's activation quantization
+# (fp8_linear.py:140-166 -> per_token_quant_fp8 above).
+# ---------------------------------------------------------------------------
+def gelu_tanh_f32(x: torch.Tensor) -> torch.Tensor:
+    """0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) in fp32 (torch's CPU kernel)."""
+    return torch.nn.functional.gelu(x.float(), approximate="tanh")
+
+
+def gelu_tanh_quant_fp8(x: torch.Tensor, act: torch.Tensor | None = None):
+    """x bf16/fp16 [M, K] -> (q uint8 [M, K], s fp32 [M], act [M, K] in x's dtype):
+    the activation rounded to x's dtype, then per_token_quant_fp8 of it. With
+    `act` given, the quantization is applied to that activation instead (the
+    check of a kernel's quantization given its own activation)."""
+    a = gelu_tanh_f32(x).to(x.dtype) if act is None else act
+    q, s = per_token_quant_fp8(a)
+    return q, s, a
+
+
+# ---------------------------------------------------------------------------
 # RMSNorm — deploy/joyomni_ops/csrc/rmsnorm.cu:41-60; formula of
 # deploy/joyomni_ops/tests/test_bench.py:65-67 and test_parity_light.py:31-32.
 # ---------------------------------------------------------------------------

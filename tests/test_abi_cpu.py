@@ -55,7 +55,7 @@ def test_ctypes_signatures_match_header(abi):
 
 
 def test_abi_version(abi):
-    assert abi.lib().jo_abi_version() == 2
+    assert abi.lib().jo_abi_version() == 3
 
 
 # Launch-size bounds of the entry points (work items of one launch < 2^32).
@@ -69,6 +69,11 @@ BAD_CALLS = [
     ("jo_sgl_per_token_quant_fp8", (8, 2, 4, 6, 6, 8, 6, 8, None), "divisible by 4"),
     ("jo_sgl_per_token_quant_fp8", (None, 2, 4, 8, 8, 8, 8, 8, None), "null pointer"),
     ("jo_sgl_per_token_quant_fp8", (8, 2, 4, 8, 4, 8, 8, 8, None), "row stride"),
+    ("jo_gelu_tanh_quant_fp8", (8, 0, 4, 8, 8, 8, 8, 8, None, 0, None), "bf16 or fp16"),
+    ("jo_gelu_tanh_quant_fp8", (8, 2, 4, 6, 6, 8, 6, 8, None, 0, None), "divisible by 4"),
+    ("jo_gelu_tanh_quant_fp8", (None, 2, 4, 8, 8, 8, 8, 8, None, 0, None), "null pointer"),
+    ("jo_gelu_tanh_quant_fp8", (8, 2, 4, 8, 4, 8, 8, 8, None, 0, None), "row stride"),
+    ("jo_gelu_tanh_quant_fp8", (8, 2, 4, 8, 8, 8, 8, 8, 8, 4, None), "activation row stride"),
     ("jo_fused_qk_norm_rope_3d_paired",
      (16, 16, 1, 4, 2, 96, 768, 192, 768, 192, 1e-6, 16, 16, 16, 16, None), "head_dim"),
     ("jo_fused_qk_norm_rope_3d_paired",
@@ -118,6 +123,8 @@ BAD_CALLS = [
     ("jo_rmsnorm", (16, 8, 16, 16, 8, MAX_ROWS + 1, 8, 2, 1e-6, None), "bad shape"),
     ("jo_rmsnorm", (None, 8, 16, 16, 8, MAX_ROWS, 8, 2, 1e-6, None), "null pointer"),
     ("jo_sgl_per_token_quant_fp8", (16, 2, MAX_ROWS + 1, 8, 8, 16, 8, 16, None), "shape too large"),
+    ("jo_gelu_tanh_quant_fp8", (16, 2, MAX_ROWS + 1, 8, 8, 16, 8, 16, None, 0, None),
+     "shape too large"),
     ("jo_rmsnorm_quant_fp8", (16, 256, 16, 16, 256, 16, MAX_ROWS + 1, 256, 2, 1e-6, 0, None),
      "bad shape"),
     ("jo_rmsnorm_heads", (16, 1152, 128, 16, 16, 128, MAX_ROWS // 3 + 1, 3, 128, 2, 1e-6, 0, None),
@@ -168,6 +175,7 @@ def test_empty_inputs_are_noops(abi):
     lib = abi.lib()
     # zero rows / zero tokens: valid, nothing to launch
     assert lib.jo_sgl_per_token_quant_fp8(None, 2, 0, 8, 8, None, 8, None, None) == abi.JO_OK
+    assert lib.jo_gelu_tanh_quant_fp8(None, 2, 0, 8, 8, None, 8, None, None, 0, None) == abi.JO_OK
     assert lib.jo_rmsnorm(None, 8, None, None, 8, 0, 8, 2, 1e-6, None) == abi.JO_OK
     assert lib.jo_rmsnorm_heads(None, 1152, 128, None, None, 128, 0, 3, 128, 2, 1e-6, 1,
                                 None) == abi.JO_OK

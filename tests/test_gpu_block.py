@@ -7,10 +7,15 @@ package's ops, with the attention output a fixed input.
 halved bf16 rotation tables; fp8_linear.py:155-169) through the drop-in ops;
 `block_fused` makes them through the fused callers (LayerNorm + AdaLN + FP8 in
 one pass, QK norm + RoPE from grid positions in place on the packed qkv, gated
-residual + LayerNorm + AdaLN + FP8 in one pass). The residual stream that
-leaves the block must be bit-identical; q and k are each checked against the
-CPU oracle with the tables their path uses (fp32 grid tables for the fused
-path, the reference's bf16 tables for the drop-in path) to 1 bf16 ulp.
+residual + LayerNorm + AdaLN + FP8 in one pass, GELU + FP8 in one pass). With
+torch's GELU kept (fuse_gelu=False) the residual stream that leaves the block
+must be bit-identical; with the fused GELU it may differ where the two GELU
+evaluations round a bf16 activation differently (each within 1 ulp of the
+formula, tests/test_gpu_gelu_quant.py), and the residual is held to 1 bf16 ulp
+of the reference composition's (floored at 2^-10 of the row maximum). q and k
+are each checked against the CPU oracle with the tables their path uses (fp32
+grid tables for the fused path, the reference's bf16 tables for the drop-in
+path) to 1 bf16 ulp.
 """
 from __future__ import annotations
 
@@ -40,6 +45,7 @@ def test_block_fused_matches_reference_composition(dev):
 
     r_in = img0.clone()
     r_img, r_q, r_k = W.block_reference(b, r_in)
+    u_img, _, _ = W.block_fused(b, img0.clone(), fuse_gelu=False)
     f_in = img0.clone()
     f_img, f_q, f_k = W.block_fused(b, f_in)
     torch.cuda.synchronize()
@@ -47,7 +53,12 @@ def test_block_fused_matches_reference_composition(dev):
           flush=True)
 
     assert torch.isfinite(r_img.float()).all()
-    assert torch.equal(f_img.cpu(), r_img.cpu()), "residual stream differs between compositions"
+    assert torch.equal(u_img.cpu(), r_img.cpu()), "residual stream differs between compositions"
+    ref = r_img.float().cpu()
+    assert_bf16_within_ulp(f_img.cpu(), ref, ref.abs().amax(-1, keepdim=True),
+                           what="residual with the fused GELU")
+    print(f"fused GELU: {int((f_img != r_img).sum())} of {r_img.numel()} residual values differ",
+          flush=True)
     assert torch.equal(r_in.cpu(), img0.cpu()), "block_reference modified its input"
 
     frames = L // (d["grid"][0] * d["grid"][1])

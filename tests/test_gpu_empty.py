@@ -35,6 +35,14 @@ def case_per_token_quant(jo, dev):
     return [(q, (0, 256), FP8), (s, (0, 1), torch.float32)]
 
 
+def case_gelu_quant(jo, dev):
+    q = torch.empty(0, 256, dtype=FP8, device=dev)
+    s = torch.empty(0, 1, dtype=torch.float32, device=dev)
+    a = torch.empty(0, 256, dtype=BF, device=dev)
+    jo.gelu_tanh_quant_fp8(_rows(dev), q, s, a)
+    return [(q, (0, 256), FP8), (s, (0, 1), torch.float32), (a, (0, 256), BF)]
+
+
 def case_fp8_scaled_mm(jo, dev):
     a = torch.empty(0, 64, dtype=FP8, device=dev)
     b = torch.zeros(32, 64, dtype=FP8, device=dev).t()
@@ -116,7 +124,8 @@ def case_kv_commit(jo, dev):
     return [(dst, (2, 1, 8, 4, 128), BF)]
 
 
-CASES = [case_norm_scale_shift, case_rmsnorm, case_per_token_quant, case_fp8_scaled_mm,
+CASES = [case_norm_scale_shift, case_rmsnorm, case_per_token_quant, case_gelu_quant,
+         case_fp8_scaled_mm,
          case_add_layernorm, case_rmsnorm_quant, case_norm_quant, case_rmsnorm_heads,
          case_apply_rotary_emb, case_qk_paired, case_qk_grid, case_qk_kvcache, case_kv_commit]
 

@@ -335,6 +335,44 @@ def test_ring_slots():
     assert ops.ring_slots(3, 7, 6) == [6, 0, 1]
 
 
+def test_gelu_tanh_oracle_matches_float64_closed_form():
+    """gelu_tanh_f32 (torch's fp32 kernel) against the formula in float64 with
+    math.tanh: within a few fp32 ulps where 1 + tanh(u) does not cancel, and
+    within one fp32 step of tanh near -1 (2^-24 * 0.5|x|) where it does; known
+    values; the erf form (approximate="none"), a plausible slip, differs."""
+    xs = torch.cat([torch.linspace(-12, 12, 20001), torch.tensor([0.0, -0.0, 1e-30, -1e-30, 1e10])])
+    got = ops.gelu_tanh_f32(xs)
+    c = math.sqrt(2.0 / math.pi)
+    for x, g in zip(xs.tolist(), got.tolist()):
+        want = 0.5 * x * (1.0 + math.tanh(c * (x + 0.044715 * x ** 3)))
+        tol = 4 * abs(want) * 2.0 ** -23 + 0.5 * abs(x) * 2.0 ** -23
+        assert abs(g - want) <= tol, (x, g, want)
+    # 0.5 (1 + tanh(sqrt(2/pi) * 1.044715)) = 0.841191990...
+    assert abs(ops.gelu_tanh_f32(torch.tensor([1.0])).item() - 0.8411919906) < 1e-7
+    assert ops.gelu_tanh_f32(torch.tensor([0.0])).item() == 0.0
+    special = ops.gelu_tanh_f32(torch.tensor([float("inf"), float("-inf"), float("nan"), -20.0]))
+    assert special[0].item() == float("inf") and math.isnan(special[1].item())
+    assert math.isnan(special[2].item()) and special[3].item() == 0.0
+    erf_form = F.gelu(xs, approximate="none")
+    assert (erf_form - got).abs().max().item() > 1e-4
+
+
+def test_gelu_quant_oracle_quantizes_the_rounded_activation():
+    """The fused op's oracle quantizes the bf16 activation torch would return:
+    bytes and scales equal the C encoder's on that activation, and a planted
+    slip (quantizing the fp32 activation) changes scales."""
+    g = torch.Generator().manual_seed(5)
+    # rows whose largest activation is not simply x (gelu(x) = x only for large x)
+    x = (0.5 * torch.randn(32, 512, generator=g)).to(torch.bfloat16)
+    q, s, a = ops.gelu_tanh_quant_fp8(x)
+    assert a.dtype == torch.bfloat16
+    assert torch.equal(a, ops.gelu_tanh_f32(x).to(torch.bfloat16))
+    qc, sc = fp8ref.per_token_quant(a.float().numpy())
+    assert np.array_equal(q.numpy(), qc) and np.array_equal(s.numpy(), sc)
+    _, s_slip = ops.per_token_quant_fp8(ops.gelu_tanh_f32(x))
+    assert not torch.equal(s_slip, s)
+
+
 def test_norm_quant_oracle_quantizes_the_rounded_y():
     """The FP8 epilogue quantizes the 16-bit y the unfused op returns: its
     scale is amax|bf16 y| / 448 (checked against torch's max and the C
