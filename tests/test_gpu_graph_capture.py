@@ -2,7 +2,8 @@
 them (deploy/xvideo/serving/graph_runner.py:169-171).
 
 One image-stream block of the DiT at a small shape (dit.py:351-476 with the
-FP8 linears of fp8_linear.py:138-169) is captured once into a graph; then,
+FP8 linears of fp8_linear.py:138-169, up to the MLP activation quantized for
+the down projection) is captured once into a graph; then,
 three times, new inputs are copied into the graph's static buffers, the graph
 is replayed, and every output is compared bit for bit with the same block run
 eagerly on the same inputs (eager work and synchronizations in between, and a
@@ -73,9 +74,10 @@ def block(s: dict, qk: str = "views") -> dict:
     res, x_q2, x_s2 = dit_ops.fused_add_gate_layernorm_modulate_fp8(
         s["res"], attn, s["gate"], s["shift2"], s["scale2"])
     up = dit_ops.fp8_linear_quantized(x_q2, x_s2, s["wq_up"], s["ws_up"], s["b_up"])
+    h_q, h_s = dit_ops.gelu_quantize_activation_fp8(up)  # the MLP activation, quantized
     txt_q = dit_ops.rms_norm_module(s["txt_qkv"][:, :, 0], s["tqw"])
     return {"x_q": x_q, "x_s": x_s, "qkv": qkv, "k_pre": k_pre, "res": res, "x_q2": x_q2,
-            "x_s2": x_s2, "up": up, "txt_q": txt_q}
+            "x_s2": x_s2, "up": up, "h_q": h_q, "h_s": h_s, "txt_q": txt_q}
 
 
 def as_bits(t: torch.Tensor) -> torch.Tensor:
