@@ -83,7 +83,7 @@ METRIC = "µs/call + achieved HBM GB/s (% of ~8 TB/s) per op at 720p 3-frame chu
 PEAK_GBPS = 8000.0
 PEAK_FP8_TFLOPS = 5000.0
 HEADLINE = "C1"
-HEADLINE_KERNEL = "quant_rows_kernel<BF16, 64, 6>"
+HEADLINE_KERNEL = "quant_rows_kernel<BF16, 64, 6, false>"
 ROT_BYTES = 640e6
 
 
