@@ -184,6 +184,31 @@ __device__ __forceinline__ void st8_nt(void* p, const u32x2& v) {
   __builtin_nontemporal_store(v, static_cast<u32x2*>(p));
 }
 
+// Division of a 32-bit unsigned n by a divisor fixed for a launch, as a
+// multiply-high, a subtraction, an add and two shifts instead of the ~15
+// instructions of an integer division by a run-time value (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", PLDI
+// 1994, the round-up method of their section 4 with the N+1-bit multiplier
+// 2^32 + m): with l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1,
+// t = mulhi(m, n), n / d = (t + ((n - t) >> min(l, 1))) >> max(l - 1, 0).
+// Exact for every n < 2^32 and 1 <= d < 2^32. make_fastdiv runs on the host.
+struct FastDiv {
+  uint32_t d, m;
+  int s1, s2;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  int l = 0;
+  while ((uint64_t{1} << l) < d) ++l;
+  const uint64_t m = ((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1;
+  return FastDiv{d, static_cast<uint32_t>(m), l < 1 ? l : 1, l > 1 ? l - 1 : 0};
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  const uint32_t t = __umulhi(n, f.m);
+  return (t + ((n - t) >> f.s1)) >> f.s2;
+}
+
 // 16-byte store with the system-scope nontemporal policy (sc0 sc1 nt: the
 // line is written through rather than left dirty in L2), through a raw
 // buffer resource. `base` must be wave-uniform (a row base computed from the

@@ -46,6 +46,8 @@ struct QKArgs {
   int t0;
   float source_id;
   int cache_slots, slot_start;  // KVC
+  // The run-time divisors of the kernel's index arithmetic (set by launch_qk).
+  FastDiv fd_seq, fd_row, fd_gw, fd_frame, fd_slots;
   // GRID / KVC: [2, D/2] axis and source-id frequencies, carried by value in
   // the kernel arguments (lanes index them with their own pair numbers, which
   // compiles to loads from the kernel-argument segment). No device copy, so a
@@ -147,6 +149,9 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
   // waves per token: [1, 3510, 24, 128] 16.38 -> 16.15 us, C3 43.9 -> 43.4 us,
   // table mode at [1, 3120, 32, 128] 19.0 -> 18.7 us). part: bit 0 = k, bit 1
   // and up = the part of the head groups (SPLIT >= 4).
+  // Token and wave indices fit 32 bits (the launch check bounds the tokens),
+  // so the index arithmetic is 32-bit, with the run-time divisions by
+  // multiply-high (FastDiv): [1, 3510, 24, 128] grid 15.3-15.5 -> 15.1 us.
   int64_t tok;
   int part;
   if constexpr (SPLIT == 1) {
@@ -155,13 +160,14 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
   } else {
     const int64_t per_tensor = a.tokens * (SPLIT / 2);
     const bool on_k = wid >= per_tensor;
-    const int64_t w = on_k ? wid - per_tensor : wid;
+    const uint32_t w = static_cast<uint32_t>(on_k ? wid - per_tensor : wid);
     tok = w / (SPLIT / 2);
     part = (on_k ? 1 : 0) | (static_cast<int>(w % (SPLIT / 2)) << 1);
   }
   if (tok >= a.tokens) return;
-  const int64_t b = tok / a.seq_len;
-  const int n = static_cast<int>(tok - b * a.seq_len);
+  const uint32_t b32 = fdiv(static_cast<uint32_t>(tok), a.fd_seq);
+  const int64_t b = b32;
+  const int n = static_cast<int>(static_cast<uint32_t>(tok) - b32 * static_cast<uint32_t>(a.seq_len));
   const int pl = lane % LPH;  // this lane holds elements 8*pl .. 8*pl+7 of its head
 
   // Destination token of the rotated k (grid modes: frame ring slot).
@@ -169,10 +175,13 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
   int f = 0, rr = 0;
   if constexpr (MODE != kTable) {
     const int frame_tokens = a.grid_h * a.grid_w;
-    f = n / frame_tokens;
+    f = static_cast<int>(fdiv(static_cast<uint32_t>(n), a.fd_frame));
     rr = n - f * frame_tokens;
-    if constexpr (MODE == kKvCache)
-      kdst_tok = static_cast<int64_t>((a.slot_start + f) % a.cache_slots) * frame_tokens + rr;
+    if constexpr (MODE == kKvCache) {
+      const uint32_t slot = static_cast<uint32_t>(a.slot_start + f);
+      const uint32_t ring = slot - fdiv(slot, a.fd_slots) * static_cast<uint32_t>(a.cache_slots);
+      kdst_tok = static_cast<int64_t>(ring) * frame_tokens + rr;
+    }
   }
   char* qrow = static_cast<char*>(a.q) + (b * a.q_bs + n * a.q_ts) * 2;
   const char* krow = static_cast<const char*>(a.k) + (b * a.k_bs + n * a.k_ts) * 2;
@@ -222,7 +231,8 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
   // outside this wave's range reads a valid chunk of the same row instead.
   // Its lanes form whole heads (a chunk holds 512/HD complete heads), so
   // their values stay within heads that are never stored.
-  const int e_safe = (lane * 8) % a.row_elems;
+  const uint32_t l8 = static_cast<uint32_t>(lane * 8);
+  const int e_safe = static_cast<int>(l8 - fdiv(l8, a.fd_row) * static_cast<uint32_t>(a.row_elems));
   u32x4 x[NS][G];
   auto load_batch = [&](int g0) {
 #pragma unroll
@@ -245,7 +255,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
     c[0] = bf16_lo(cw.x); c[1] = bf16_hi(cw.x); c[2] = bf16_lo(cw.y); c[3] = bf16_hi(cw.y);
     s[0] = bf16_lo(sw.x); s[1] = bf16_hi(sw.x); s[2] = bf16_lo(sw.y); s[3] = bf16_hi(sw.y);
   } else {
-    const int hh = rr / a.grid_w;
+    const int hh = static_cast<int>(fdiv(static_cast<uint32_t>(rr), a.fd_gw));
     const int ww = rr - hh * a.grid_w;
     const float tpos = static_cast<float>(a.t0 + f);
     float mc[K], ms[K];
@@ -350,7 +360,15 @@ int qk_split(int64_t tokens, int all_groups) {
 }
 
 template <int MODE, bool STAGE = false>
-int launch_qk(const QKArgs& a, int head_dim, hipStream_t stream, const char* op) {
+int launch_qk(const QKArgs& args, int head_dim, hipStream_t stream, const char* op) {
+  QKArgs a = args;
+  a.fd_seq = make_fastdiv(static_cast<uint32_t>(a.seq_len));
+  a.fd_row = make_fastdiv(static_cast<uint32_t>(a.row_elems));
+  if (MODE != kTable) {
+    a.fd_gw = make_fastdiv(static_cast<uint32_t>(a.grid_w));
+    a.fd_frame = make_fastdiv(static_cast<uint32_t>(a.grid_h) * static_cast<uint32_t>(a.grid_w));
+  }
+  if (MODE == kKvCache) a.fd_slots = make_fastdiv(static_cast<uint32_t>(a.cache_slots));
   const int all_groups = (a.row_elems + 511) / 512;
   const int split = qk_split(a.tokens, all_groups);
   const int parts = split >= 4 ? split / 2 : 1;
