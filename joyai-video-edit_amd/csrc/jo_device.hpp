@@ -198,6 +198,7 @@ struct FastDiv {
 };
 
 inline FastDiv make_fastdiv(uint32_t d) {
+  if (d == 0) return FastDiv{0, 0, 0, 0};  // callers pass d >= 1; no division by zero here
   int l = 0;
   while ((uint64_t{1} << l) < d) ++l;
   const uint64_t m = ((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1;

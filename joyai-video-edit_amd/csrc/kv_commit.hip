@@ -41,6 +41,7 @@ struct CommitArgs {
   const float* cos;          // [B?, T, D] fp32: token stride tab_ts, batch stride tab_bs
   const float* sin;          // (tab_bs 0: one table for every batch row)
   int64_t tab_ts, tab_bs;
+  FastDiv fd_tokens, fd_batch;  // the row index's divisors (set by launch_commit)
 };
 
 // The pair rotation with torch's rounding sequence.
@@ -61,15 +62,21 @@ template <class Tag, int CH, bool KV2>
 __global__ __launch_bounds__(kBlock) void rope_commit_kernel(const CommitArgs a) {
   static_assert(Tag::kVec == 8, "16-bit rows");
   const int lane = threadIdx.x % kWave;
-  const int64_t wid = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + threadIdx.x / kWave;
+  // The wave index through readfirstlane, and 32-bit row arithmetic with
+  // multiply-high division (rows < 2^32 by the launch check): the index math
+  // is scalar instead of 64-bit divisions in every lane.
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) +
+                      __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int64_t rows = a.layers * a.batch * a.tokens;
   const bool v_wave = KV2 && wid >= rows;  // wave-uniform
   const int64_t row = v_wave ? wid - rows : wid;
   if (row >= rows) return;
-  const int64_t n = row % a.tokens;
-  const int64_t lb = row / a.tokens;
-  const int64_t b = lb % a.batch;
-  const int64_t l = lb / a.batch;
+  const uint32_t r32 = static_cast<uint32_t>(row);
+  const uint32_t lb32 = fdiv(r32, a.fd_tokens);
+  const uint32_t l32 = fdiv(lb32, a.fd_batch);
+  const int64_t n = r32 - lb32 * static_cast<uint32_t>(a.tokens);
+  const int64_t b = lb32 - l32 * static_cast<uint32_t>(a.batch);
+  const int64_t l = l32;
   const int64_t so = l * a.s_ls + b * a.s_bs + n * a.s_ts;
   const int64_t dof = l * a.d_ls + b * a.d_bs + (a.d_off + n) * a.d_ts;
   const bool do_k = !v_wave;
@@ -161,7 +168,10 @@ __global__ __launch_bounds__(kBlock) void rope_commit_generic_kernel(const Commi
 }
 
 template <class Tag>
-int launch_commit(const CommitArgs& a, hipStream_t stream) {
+int launch_commit(const CommitArgs& args, hipStream_t stream) {
+  CommitArgs a = args;
+  a.fd_tokens = make_fastdiv(static_cast<uint32_t>(a.tokens));
+  a.fd_batch = make_fastdiv(static_cast<uint32_t>(a.batch));
   const int b = Tag::kBytes;
   const int64_t rows = a.layers * a.batch * a.tokens;
   auto al = [&](const void* p, int64_t stride_elems) {
