@@ -401,13 +401,15 @@ struct RmsArgs {
   int64_t M;
   int N;
   float eps;
+  FastDiv fd_heads;  // HEADS: the row index's divisor (set by launch_rmsnorm)
 };
 
 template <bool HEADS>
 __device__ __forceinline__ int64_t rms_row_offset(const RmsArgs& a, int64_t row) {
   if constexpr (HEADS) {
-    // M < 2^32 (checked on the host), so the division can be 32-bit.
-    const uint32_t t = static_cast<uint32_t>(row) / static_cast<uint32_t>(a.heads);
+    // M < 2^32 (checked on the host), so the division can be 32-bit, by
+    // multiply-high ([1, 3120, 32, 128] K slice: R_kn).
+    const uint32_t t = fdiv(static_cast<uint32_t>(row), a.fd_heads);
     return static_cast<int64_t>(t) * a.xs + (row - static_cast<int64_t>(t) * a.heads) * a.xhs;
   } else {
     return row * a.xs;
@@ -515,7 +517,9 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_generic_kernel(const RmsArgs a
 }
 
 template <class Tag, bool HEADS, int MODE>
-int launch_rmsnorm(const RmsArgs& a, hipStream_t stream, const char* op) {
+int launch_rmsnorm(const RmsArgs& args, hipStream_t stream, const char* op) {
+  RmsArgs a = args;
+  if (HEADS) a.fd_heads = make_fastdiv(static_cast<uint32_t>(a.heads));
   const int b = Tag::kBytes;
   const bool vec_ok = (a.N % Tag::kVec == 0) && aligned(a.x, 16) && (a.xs * b) % 16 == 0 &&
                       (!HEADS || (a.xhs * b) % 16 == 0) && aligned(a.w, 16) &&
