@@ -11,16 +11,6 @@
 namespace jo {
 namespace {
 
-// ---------------------------------------------------------------------------
-// Per-token quantization: follows per_token_quant_fp8.cu:56-82.
-//   amax = max |x| (NaN ignored: fmaxf), scale = amax / 448 (IEEE division),
-//   inv = (scale == 0) ? 0 : 1 / scale, q = e4m3fn(clamp(x * inv, +-448)).
-// The row maximum is first taken NaN-propagating; when it is finite (no NaN,
-// no inf in the row) it is the reference's amax and, with a finite inv, the
-// clamp cannot change a code, so it is skipped. Any wave (workgroup, for
-// rows wider than a wave) holding a non-finite row recomputes the
-// NaN-skipping maximum and clamps that row.
-// ---------------------------------------------------------------------------
 // GELU with the tanh approximation, the activation torch applies between the
 // MLP's two Fp8Linears (dit.py:91-92, 433):
 //   gelu(x) = 0.5 * x * (1 + tanh(u)),  u = sqrt(2/pi) * (x + 0.044715 * x^3),
@@ -45,6 +35,16 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return x * __builtin_fmaf(0.5f, th, 0.5f);  // 0.5 x (1 + tanh(u)), 0.5 (1 + th) exact
 }
 
+// ---------------------------------------------------------------------------
+// Per-token quantization: follows per_token_quant_fp8.cu:56-82.
+//   amax = max |x| (NaN ignored: fmaxf), scale = amax / 448 (IEEE division),
+//   inv = (scale == 0) ? 0 : 1 / scale, q = e4m3fn(clamp(x * inv, +-448)).
+// The row maximum is first taken NaN-propagating; when it is finite (no NaN,
+// no inf in the row) it is the reference's amax and, with a finite inv, the
+// clamp cannot change a code, so it is skipped. Any wave (workgroup, for
+// rows wider than a wave) holding a non-finite row recomputes the
+// NaN-skipping maximum and clamps that row.
+// ---------------------------------------------------------------------------
 // ACT: the row is first replaced by gelu_tanh of it, rounded to the row's
 // dtype (the bf16 / fp16 tensor torch's activation would return), and that
 // row is quantized; when act is not null it is also stored there (row
