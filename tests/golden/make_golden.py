@@ -161,6 +161,18 @@ def build() -> dict[str, np.ndarray]:
     x = (torch.randn(5, 3, 128, generator=g) * 2).to(torch.bfloat16)
     w = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16)
     fx.update(rmsmod_x=bits(x), rmsmod_w=bits(w), rmsmod_y=bits(ops.rms_norm_module(x, w, 1e-6)))
+
+    # GELU(tanh) + per-token FP8 (dit.py:91-92,433, then fp8_linear.py:140-166):
+    # the fp32 activation of the formula, and the oracle's bytes and scales on
+    # its bf16 rounding; rows with NaN / +-inf and a deep negative tail.
+    g = torch.Generator().manual_seed(110)
+    x = with_outliers(3 * torch.randn(6, 4096, generator=g), g)
+    x[0, :3] = torch.tensor([float("nan"), float("inf"), float("-inf")])
+    x[1, :64] = -20.0
+    x = x.to(torch.bfloat16)
+    q, s, _ = ops.gelu_tanh_quant_fp8(x)
+    fx.update(gelu_x=bits(x), gelu_act=f32(ops.gelu_tanh_f32(x)), gelu_q=q.numpy(),
+              gelu_s=f32(s))
     return fx
 
 

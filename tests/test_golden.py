@@ -6,7 +6,10 @@ tests/golden/make_golden.py from seeded inputs through the CPU oracle):
   GPU  the HIP kernels, through the torch ops the reference's callers use,
        match the stored outputs: FP8 bytes, scales, residuals and the KV-pool
        commit exactly, bf16 results within 1 bf16 ulp of the stored fp32
-       values, the GEMM within the fp32-accumulation bar.
+       values, the GEMM within the fp32-accumulation bar; for the GELU + FP8
+       op the activation within 1 bf16 ulp of the stored fp32 one (plus the
+       formula's own step where 1 + tanh cancels) and the bytes and scales
+       exact against the oracle's quantization of that activation.
 """
 from __future__ import annotations
 
@@ -175,3 +178,25 @@ def test_golden_rms_norm_module(fx, dev):
     y = dit_ops.rms_norm_module(x, bf16(fx["rmsmod_w"]).to(dev), 1e-6)
     torch.cuda.synchronize()
     assert torch.equal(y.cpu(), bf16(fx["rmsmod_y"])), "module rmsnorm differs"
+
+
+@pytest.mark.gpu
+def test_golden_gelu_quant(fx, dev):
+    import joyomni_ops as jo
+    from oracle import ops
+    x = bf16(fx["gelu_x"])
+    q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty(x.shape[0], dtype=torch.float32, device=dev)
+    a = torch.empty(x.shape, dtype=torch.bfloat16, device=dev)
+    jo.gelu_tanh_quant_fp8(x.to(dev), q, s, a)
+    torch.cuda.synchronize()
+    ref = torch.from_numpy(fx["gelu_act"])
+    act = a.float().cpu()
+    assert torch.equal(torch.isnan(act), torch.isnan(ref))
+    fin = torch.isfinite(ref)
+    assert torch.equal(act[~fin & ~torch.isnan(ref)], ref[~fin & ~torch.isnan(ref)])
+    ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -126))) - 7)
+    tol = ulp + 0.5 * x.float().abs() * 2.0 ** -23
+    assert bool(((act - ref).abs() <= tol)[fin].all()), "activation beyond 1 bf16 ulp"
+    qo, so = ops.per_token_quant_fp8(a.cpu())
+    assert torch.equal(q.view(torch.uint8).cpu(), qo) and torch.equal(s.cpu(), so)
