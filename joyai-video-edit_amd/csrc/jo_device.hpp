@@ -191,7 +191,9 @@ __device__ __forceinline__ void st8_nt(void* p, const u32x2& v) {
 // 1994, the round-up method of their section 4 with the N+1-bit multiplier
 // 2^32 + m): with l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1,
 // t = mulhi(m, n), n / d = (t + ((n - t) >> min(l, 1))) >> max(l - 1, 0).
-// Exact for every n < 2^32 and 1 <= d < 2^32. make_fastdiv runs on the host.
+// Exact for every n < 2^32 and 1 <= d < 2^32. make_fastdiv runs on the host;
+// fdiv on either side (the 64-bit product's high half is v_mul_hi_u32 on the
+// device).
 struct FastDiv {
   uint32_t d, m;
   int s1, s2;
@@ -205,8 +207,8 @@ inline FastDiv make_fastdiv(uint32_t d) {
   return FastDiv{d, static_cast<uint32_t>(m), l < 1 ? l : 1, l > 1 ? l - 1 : 0};
 }
 
-__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
-  const uint32_t t = __umulhi(n, f.m);
+__host__ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  const uint32_t t = static_cast<uint32_t>((uint64_t{n} * f.m) >> 32);
   return (t + ((n - t) >> f.s1)) >> f.s2;
 }
 
