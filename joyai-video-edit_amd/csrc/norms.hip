@@ -86,7 +86,8 @@ __device__ __forceinline__ u32x4 ld_mod(const void* base, int64_t stride, int64_
 // 56-82 (the input Fp8Linear.forward quantizes, fp8_linear.py:138-169)
 // instead of being written.
 // ---------------------------------------------------------------------------
-template <class Tag, int LPR, int CH, int NT, bool ADD, bool QNT, bool BCAST = false>
+template <class Tag, int LPR, int CH, int NT, bool ADD, bool QNT, bool BCAST = false,
+          bool EARLY = false>
 __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
   constexpr int V = Tag::kVec;
   constexpr int RPB = kBlock / LPR;
@@ -161,8 +162,21 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
   sum = row_reduce<LPR, OpSum>(sum, red_a);
   float mean = 0.f;
   float r;
+  // EARLY: per-row scale and shift issued once the mean is known, so that
+  // their latency overlaps the variance reduction; the launcher takes it only
+  // when the grid holds two or more full rounds of waves (below).
+  u32x4 esc[EARLY ? CH : 1], esh[EARLY ? CH : 1];
   if constexpr (NT == kLayer) {
     mean = div_by_len(sum, N);
+    if constexpr (EARLY) {
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int e = (i * LPR + lane) * V;
+        const bool ok = row_ok && e < N;
+        esc[i] = ok ? ld_mod<Tag>(a.scale, a.scs, mrow, e) : u32x4{0u, 0u, 0u, 0u};
+        esh[i] = ok ? ld_mod<Tag>(a.shift, a.shs, mrow, e) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
@@ -200,6 +214,9 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
     if constexpr (BCAST) {
       sc = bsc[i];
       sh = bsh[i];
+    } else if constexpr (EARLY) {
+      sc = esc[i];
+      sh = esh[i];
     } else {
       sc = ld_mod<Tag>(a.scale, a.scs, mrow, e);
       sh = ld_mod<Tag>(a.shift, a.shs, mrow, e);
@@ -335,8 +352,16 @@ int launch_norm_mod(const NormArgs& a, hipStream_t stream, const char* op) {
     launched = dispatch_row_shape<Tag::kVec, true, 256>(a.N, [&](auto lpr, auto ch) {
       constexpr int LPR = decltype(lpr)::value;
       constexpr int CH = decltype(ch)::value;
+      // Per-row scale and shift issued early (EARLY) pay when waves wait on
+      // others' completion: with four waves per row at [4096, 4096] (two full
+      // rounds of 8192 wave slots) 23.9 -> 23.4 us, while at [3120, 4096]
+      // (1.5 rounds) the same kernel lost, 18.2 -> 18.7 us.
+      constexpr bool kEarlyShape = LPR == 256 && CH == 2 && NT == kLayer && !ADD && !QNT;
       if (a.scs == 0 && a.shs == 0 && !a.gamma)
         hipLaunchKernelGGL((norm_mod_kernel<Tag, LPR, CH, NT, ADD, QNT, true>),
+                           dim3(row_blocks(a.M, LPR)), dim3(kBlock), 0, stream, a);
+      else if (kEarlyShape && a.M * (LPR / kWave) >= 2 * kFewRows)
+        hipLaunchKernelGGL((norm_mod_kernel<Tag, LPR, CH, NT, ADD, QNT, false, kEarlyShape>),
                            dim3(row_blocks(a.M, LPR)), dim3(kBlock), 0, stream, a);
       else
         hipLaunchKernelGGL((norm_mod_kernel<Tag, LPR, CH, NT, ADD, QNT>),

@@ -52,12 +52,16 @@ def test_fused_norm_scale_shift(dev, dtype, M, N, norm, affine):
     assert_within_ulp(y.cpu(), ref, dtype, row_floor(ref), what=f"{norm} {affine} {dtype} [{M},{N}]")
 
 
-@pytest.mark.parametrize("M", [4096, 8191, 8192])
-def test_fused_norm_scale_shift_row_shape_switch(dev, M):
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("affine", ["none", "gamma_beta"])
+@pytest.mark.parametrize("M", [3120, 4095, 4096, 8191, 8192])
+def test_fused_norm_scale_shift_row_shape_switch(dev, M, affine, dtype):
     """4096-wide rows take four waves per row below 8192 rows and one from
-    there: both sides of the switch against the oracle (4096 x 4096 is the
-    reference's own benchmark shape, test_bench.py)."""
-    test_fused_norm_scale_shift(dev, torch.bfloat16, M, 4096, "layer", "gamma_beta")
+    there, and with four waves per row the per-row LayerNorm loads its scale
+    and shift early from 4096 rows (two full rounds of waves) on: every side of
+    both switches against the oracle (4096 x 4096 is the reference's own
+    benchmark shape, test_bench.py)."""
+    test_fused_norm_scale_shift(dev, dtype, M, 4096, "layer", affine)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
