@@ -60,7 +60,10 @@ BASELINE config (C0-C4), timed on the host's cores with the same inputs:
 3 warmups, then at least 10 timed calls (more while under ~2 s), median
 (`cpu_us_per_call` in each config's line; the headline one in cpu_baseline).
 
-Prints ONE JSON line on stdout; progress goes to stderr.
+Prints ONE compact JSON line on stdout (under 4 KB: the headline with its
+roofline and CPU baseline, and per line only us/call, roofline fraction,
+stream ceiling and CPU time); progress and each line's full record go to
+stderr, and the full record of the run to --detail (gpurun_out/bench_detail.json).
 """
 from __future__ import annotations
 
@@ -728,6 +731,9 @@ def main() -> int:
                     help="time eager launches only (for profiler counter runs)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run a plain copy of this many MiB (counter calibration)")
+    ap.add_argument("--detail", default=str(ROOT / "gpurun_out" / "bench_detail.json"),
+                    help="file for the full per-line record ('' for none); stdout carries the "
+                         "compact summary line only")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -831,15 +837,83 @@ def main() -> int:
             if n == HEADLINE:
                 cpu = c
 
+    detail_path = Path(args.detail) if args.detail else None
+    line = summary_line(results, cpu, args.steps, args.warmup, cpu_model(),
+                        detail_path.name if detail_path else None)
+    if detail_path is not None:
+        # The whole per-line record (every field of every config and stream
+        # ceiling) goes to a file; stdout carries the compact line only.
+        full = dict(line, ops=results)
+        if copy is not None:
+            full["copy_probe"] = copy
+        try:
+            detail_path.parent.mkdir(parents=True, exist_ok=True)
+            detail_path.write_text(json.dumps(full, indent=1))
+            log(f"full record written to {detail_path}")
+        except OSError as ex:
+            log(f"could not write {detail_path}: {ex}")
+    for n, r in results.items():
+        log(f"line {n}: {json.dumps(r)}")
+    print(json.dumps(line, separators=(",", ":")), flush=True)
+    return 0
+
+
+SUMMARY_MAX_BYTES = 4096
+
+
+def _r(v, nd):
+    return None if v is None else round(v, nd)
+
+
+def compact_entry(name: str, r: dict) -> dict:
+    """The few figures of one line that the summary carries: per-call time,
+    fraction of the roofline (HBM, or the fp8 matrix-core peak for GEMMs), the
+    stream ceiling of the line's own access shape and the CPU baseline."""
+    if r.get("kind") == "stream-ceiling":
+        return {"us": _r(r["us_per_call"], 2), "frac": _r(r.get("frac_of_peak"), 3)}
+    if name == "B_img":
+        return {"us": _r(r["us_per_call"], 1), "ref_us": _r(r.get("reference_composition_us_per_call"), 1)}
+    e = {"us": _r(r["us_per_call"], 2)}
+    if r.get("bound") == "mfma":
+        e["tflops"] = _r(r.get("tflops"), 0)
+        e["frac"] = _r(r.get("frac_of_fp8_peak"), 3)
+        if "hipblaslt_over_ours" in r:
+            e["blt_x"] = _r(r["hipblaslt_over_ours"], 3)
+        return e
+    e["frac"] = _r(r.get("frac_of_peak"), 3)
+    if "stream_ceiling_us" in r:
+        e["S_us"] = _r(r["stream_ceiling_us"], 2)
+        e["fS"] = _r(r.get("frac_of_stream_ceiling"), 3)
+    if "cpu_us_per_call" in r:
+        e["cpu_us"] = _r(r["cpu_us_per_call"], 0)
+    for k, short in (("torch_reference_us_per_call", "ref_us"),
+                     ("unfused_two_calls_us_per_call", "ref_us"),
+                     ("copy_then_rmsnorm_us_per_call", "ref_us")):
+        if k in r:
+            e[short] = _r(r[k], 1)
+    return e
+
+
+def summary_line(results: dict, cpu, steps: int, warmup: int, host_cpu: str = "",
+                 detail: str | None = None) -> dict:
+    """The one JSON line bench.py prints: the headline (C1) with its roofline
+    and CPU baseline, and a compact entry for every other line that ran (the
+    BASELINE configs under "configs", the rest under "ops"). It is kept under
+    SUMMARY_MAX_BYTES so that a reader that keeps only the tail of stdout
+    still gets it whole; the full record goes to the detail file."""
+    from joyomni_ops import workloads as W
     h = results[HEADLINE]
     cfg = W.CONFIGS[HEADLINE]
+    configs = {n: compact_entry(n, results[n]) for n in BASELINE_CONFIGS if n in results}
+    ops = {n: compact_entry(n, r) for n, r in results.items()
+           if n not in configs and not n.startswith("S_")}
     line = {
         "metric": METRIC,
         "value": h["gbps"],
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "timed_calls": h["timed_calls"],
         "warmup_calls": h["warmup_calls"],
         "ms_per_step": round(h["us_per_call"] / 1000.0, 6),
@@ -853,22 +927,22 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": HEADLINE_KERNEL, "achieved": h["gbps"],
                      "peak": PEAK_GBPS, "unit": "GB/s", "frac": h["frac_of_peak"],
                      "traffic": load_traffic(HEADLINE_KERNEL),
-                     "algorithmic_bytes": h["algorithmic_bytes"],
-                     "stream_ceiling_us": h.get("stream_ceiling_us")},
+                     "algorithmic_bytes": h["algorithmic_bytes"]},
         "cpu_baseline": None if cpu is None else {
             "value": cpu["gbps"], "unit": "GB/s", "us_per_call": cpu["us_per_call"],
             "cores": cpu["threads"], "kind": "port",
-            "sample": f"oracle.ops.per_token_quant_fp8 (torch CPU) on the full C1 input, "
-                      f"median of {cpu['iters']} calls ({cpu['seconds']:.1f} s of CPU work) after "
-                      f"3 warmups, torch.set_num_threads({cpu['threads']}); host {cpu_model()}, "
-                      f"{os.cpu_count()} logical CPUs; every BASELINE config's CPU time is in "
-                      f"ops[cfg].cpu_us_per_call"},
-        "ops": results,
+            "sample": f"oracle per_token_quant_fp8 (torch CPU), full C1 input, median of "
+                      f"{cpu['iters']} calls ({cpu['seconds']:.1f} s) after 3 warmups; "
+                      f"{host_cpu[:48]}"},
+        "configs": configs,
+        "ops": ops,
+        "keys": "us=us/call, frac=of 8 TB/s (GEMM: of 5 PF fp8), S_us=stream ceiling of the "
+                "line's shape, fS=S_us/us, cpu_us=CPU oracle, ref_us=reference path, "
+                "blt_x=hipBLASLt time/ours",
     }
-    if copy is not None:
-        line["copy_probe"] = copy
-    print(json.dumps(line), flush=True)
-    return 0
+    if detail:
+        line["detail"] = detail
+    return line
 
 
 if __name__ == "__main__":

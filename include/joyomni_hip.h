@@ -74,7 +74,9 @@ int jo_abi_version(void);
 #define JO_KNOB_GEMM_SHAPE 2
 
 /* Sets knob `knob` to `value` (-1 restores the automatic choice) for every
- * later launch in the process. Returns JO_ERR_INVALID for an unknown knob. */
+ * later launch in the process. Returns JO_ERR_INVALID for an unknown knob or
+ * a value the knob does not list above (an environment value the knob does
+ * not accept is ignored at load, with a message on stderr). */
 int jo_set_launch_override(int knob, int value);
 
 /* ------------------------------------------------------------------------
@@ -300,7 +302,9 @@ int jo_rmsnorm_quant_fp8(const void* x, int64_t x_stride, const void* weight, vo
  *   then jo_sgl_per_token_quant_fp8's rule on the row a[r,:].
  * output_act (optional, may be NULL): the rounded activation a, row stride
  * act_stride; the FP8 bytes and scales are those of jo_sgl_per_token_quant_fp8
- * applied to it. Other arguments and limits as jo_sgl_per_token_quant_fp8.
+ * applied to it. output_act must not overlap input (JO_ERR_INVALID if the
+ * byte ranges of the two views meet). Other arguments and limits as
+ * jo_sgl_per_token_quant_fp8.
  * ------------------------------------------------------------------------ */
 int jo_gelu_tanh_quant_fp8(const void* input, int dtype, int64_t num_tokens, int64_t hidden_dim,
                            int64_t in_stride, void* output_q, int64_t q_stride, float* output_s,

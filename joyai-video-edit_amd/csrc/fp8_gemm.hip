@@ -815,7 +815,9 @@ int pick_tile_rows(int M, int N) {
 template <class OutTag>
 int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   const dim3 grid((g.N + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
-  const bool pipe_ok = g.K % kPBK == 0 && aligned(g.sb, 16) && (g.bias == nullptr || aligned(g.bias, 8)) &&
+  // K == 0 takes the register-staged kernel, which loads no operand bytes
+  // when K is 0 and stores the epilogue of a zero accumulator (the bias).
+  const bool pipe_ok = g.K > 0 && g.K % kPBK == 0 && aligned(g.sb, 16) && (g.bias == nullptr || aligned(g.bias, 8)) &&
                        256 * (g.lda > g.ldb ? g.lda : g.ldb) + g.K <= int64_t{UINT32_MAX};
   // 8-wave 256-column tiles measured faster than two 4-wave 128-column
   // workgroups per CU at every deployment shape (3120x12288x4096: 199 -> 185

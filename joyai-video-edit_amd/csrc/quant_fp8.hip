@@ -607,6 +607,17 @@ extern "C" int jo_gelu_tanh_quant_fp8(const void* input, int dtype, int64_t num_
              "gelu_tanh_quant_fp8: activation row stride smaller than hidden_dim");
   if (num_tokens == 0) return JO_OK;
   JO_REQUIRE(input && output_q && output_s, "gelu_tanh_quant_fp8: null pointer");
+  if (output_act != nullptr && hidden_dim > 0) {
+    // The element-wise path stores the activation of a row before it reads
+    // the row again to quantize it, so the activation must not overlap the
+    // input (the byte ranges the two row-strided views span).
+    const auto lo_in = reinterpret_cast<uintptr_t>(input);
+    const auto lo_act = reinterpret_cast<uintptr_t>(output_act);
+    const uintptr_t hi_in = lo_in + static_cast<uintptr_t>((num_tokens - 1) * in_stride + hidden_dim) * 2;
+    const uintptr_t hi_act = lo_act + static_cast<uintptr_t>((num_tokens - 1) * act_stride + hidden_dim) * 2;
+    JO_REQUIRE(hi_in <= lo_act || hi_act <= lo_in,
+               "gelu_tanh_quant_fp8: output_act must not overlap input");
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == JO_DTYPE_BF16)
     return launch_quant<BF16, true>(input, num_tokens, hidden_dim, in_stride, output_q, q_stride,

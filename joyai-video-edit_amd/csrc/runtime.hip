@@ -13,14 +13,35 @@ thread_local char g_last_error[512] = {0};
 
 constexpr int kKnobs = 3;
 
-// Each knob's environment variable is read once, when the library is loaded.
-int knob_from_env(const char* name) {
-  const char* v = getenv(name);
-  return (v && *v) ? atoi(v) : -1;
+// The values each knob accepts besides -1 (the library's own choice):
+// QK waves per token 1, 2, 4, 6, 8; KV rows on 1 or 2 waves; GEMM shapes 0-4.
+bool knob_value_ok(int knob, int v) {
+  if (v == -1) return true;
+  switch (knob) {
+    case JO_KNOB_QK_SPLIT: return v == 1 || v == 2 || v == 4 || v == 6 || v == 8;
+    case JO_KNOB_KV_SPLIT: return v == 1 || v == 2;
+    case JO_KNOB_GEMM_SHAPE: return v >= 0 && v <= 4;
+    default: return false;
+  }
 }
-std::atomic<int> g_knobs[kKnobs] = {{knob_from_env("JO_QK_SPLIT")},
-                                    {knob_from_env("JO_KV_SPLIT")},
-                                    {knob_from_env("JO_GEMM_SHAPE")}};
+
+// Each knob's environment variable is read once, when the library is loaded.
+// A value the knob does not accept is ignored (with a message on stderr), so a
+// mistyped override never silently selects another kernel.
+int knob_from_env(int knob, const char* name) {
+  const char* v = getenv(name);
+  if (!v || !*v) return -1;
+  char* end = nullptr;
+  const long x = strtol(v, &end, 10);
+  if (*end != 0 || x < -1 || x > 64 || !knob_value_ok(knob, static_cast<int>(x))) {
+    fprintf(stderr, "joyomni_hip: ignoring %s=%s (not a value this knob accepts)\n", name, v);
+    return -1;
+  }
+  return static_cast<int>(x);
+}
+std::atomic<int> g_knobs[kKnobs] = {{knob_from_env(JO_KNOB_QK_SPLIT, "JO_QK_SPLIT")},
+                                    {knob_from_env(JO_KNOB_KV_SPLIT, "JO_KV_SPLIT")},
+                                    {knob_from_env(JO_KNOB_GEMM_SHAPE, "JO_GEMM_SHAPE")}};
 }  // namespace
 
 void set_error(const char* fmt, ...) {
@@ -53,7 +74,8 @@ extern "C" int jo_abi_version(void) { return JO_ABI_VERSION; }
 
 extern "C" int jo_set_launch_override(int knob, int value) {
   JO_REQUIRE(knob >= 0 && knob < jo::kKnobs, "jo_set_launch_override: unknown knob %d", knob);
-  JO_REQUIRE(value >= -1 && value <= 64, "jo_set_launch_override: value %d out of range", value);
+  JO_REQUIRE(jo::knob_value_ok(knob, value),
+             "jo_set_launch_override: value %d is not one knob %d accepts", value, knob);
   jo::g_knobs[knob].store(value, std::memory_order_relaxed);
   return JO_OK;
 }

@@ -36,7 +36,17 @@ void check_status(int status, const char* op) {
   TORCH_CHECK(status == JO_OK, op, ": ", jo_last_error());
 }
 
+// The shim is compiled against include/joyomni_hip.h; a kernel library of
+// another ABI version (argument lists differ between versions) is refused at
+// the first launch instead of being called with misread arguments.
+void check_abi() {
+  static const int lib_abi = jo_abi_version();
+  TORCH_CHECK(lib_abi == JO_ABI_VERSION, "joyomni_ops: libjoyomni_hip.so has ABI version ",
+              lib_abi, ", this _C.so was built for ", JO_ABI_VERSION, "; rebuild both");
+}
+
 void* current_stream(const torch::Tensor& t) {
+  check_abi();
   return static_cast<void*>(
       c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.get_device()).stream());
 }

@@ -14,6 +14,10 @@ from ctypes import c_char_p, c_float, c_int, c_int32, c_int64, c_void_p
 
 LIB_NAME = "libjoyomni_hip.so"
 
+# The header's JO_ABI_VERSION this binding's SIGNATURES follow; a library
+# reporting another version is refused at load.
+JO_ABI_VERSION = 3
+
 JO_OK = 0
 JO_ERR_INVALID = 1
 JO_ERR_UNSUPPORTED = 2
@@ -95,6 +99,11 @@ def lib() -> ctypes.CDLL:
     handle.jo_last_error.argtypes = []
     handle.jo_abi_version.restype = c_int
     handle.jo_abi_version.argtypes = []
+    found = handle.jo_abi_version()
+    if found != JO_ABI_VERSION:
+        raise ImportError(
+            f"{path} has ABI version {found}, this binding expects {JO_ABI_VERSION}; "
+            "rebuild it (python joyai-video-edit_amd/build.py)")
     for name, argtypes in SIGNATURES.items():
         fn = getattr(handle, name, None)
         if fn is None:  # reported by the export test; call() raises on use

@@ -5,6 +5,7 @@ torch op library registers the reference's schemas byte-for-byte."""
 from __future__ import annotations
 
 import ctypes
+import os
 import re
 import subprocess
 from pathlib import Path
@@ -14,6 +15,7 @@ import torch
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "joyomni_hip.h"
+PKG = ROOT / "joyai-video-edit_amd"
 
 
 def header_functions() -> dict[str, int]:
@@ -74,6 +76,14 @@ BAD_CALLS = [
     ("jo_gelu_tanh_quant_fp8", (None, 2, 4, 8, 8, 8, 8, 8, None, 0, None), "null pointer"),
     ("jo_gelu_tanh_quant_fp8", (8, 2, 4, 8, 4, 8, 8, 8, None, 0, None), "row stride"),
     ("jo_gelu_tanh_quant_fp8", (8, 2, 4, 8, 8, 8, 8, 8, 8, 4, None), "activation row stride"),
+    # input rows span bytes [4096, 4160): an activation at the same address or
+    # starting inside that span is refused
+    ("jo_gelu_tanh_quant_fp8", (4096, 2, 4, 8, 8, 8192, 8, 16384, 4096, 8, None),
+     "must not overlap"),
+    ("jo_gelu_tanh_quant_fp8", (4096, 2, 4, 8, 8, 8192, 8, 16384, 4158, 8, None),
+     "must not overlap"),
+    ("jo_gelu_tanh_quant_fp8", (4096, 2, 4, 8, 8, 8192, 8, 16384, 4040, 8, None),
+     "must not overlap"),
     ("jo_fused_qk_norm_rope_3d_paired",
      (16, 16, 1, 4, 2, 96, 768, 192, 768, 192, 1e-6, 16, 16, 16, 16, None), "head_dim"),
     ("jo_fused_qk_norm_rope_3d_paired",
@@ -163,12 +173,35 @@ def test_validation_errors_without_gpu(abi, name, args, msg):
 
 def test_launch_override(abi):
     lib = abi.lib()
-    for knob in (abi.JO_KNOB_QK_SPLIT, abi.JO_KNOB_KV_SPLIT, abi.JO_KNOB_GEMM_SHAPE):
-        assert lib.jo_set_launch_override(knob, 4) == abi.JO_OK
+    accepted = {abi.JO_KNOB_QK_SPLIT: {1, 2, 4, 6, 8}, abi.JO_KNOB_KV_SPLIT: {1, 2},
+                abi.JO_KNOB_GEMM_SHAPE: {0, 1, 2, 3, 4}}
+    for knob, ok in accepted.items():
+        for v in range(-3, 66):
+            want = abi.JO_OK if (v == -1 or v in ok) else abi.JO_ERR_INVALID
+            assert lib.jo_set_launch_override(knob, v) == want, (knob, v)
+            if want != abi.JO_OK:
+                assert "not one knob" in abi.last_error()
         assert lib.jo_set_launch_override(knob, -1) == abi.JO_OK
     assert lib.jo_set_launch_override(3, 1) == abi.JO_ERR_INVALID
     assert "unknown knob" in abi.last_error()
-    assert lib.jo_set_launch_override(abi.JO_KNOB_QK_SPLIT, -2) == abi.JO_ERR_INVALID
+
+
+def test_launch_override_env_values_are_checked(tmp_path):
+    """An environment override the knob does not accept is ignored with a
+    message (a fresh process, since the variables are read at load)."""
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "from joyomni_ops import _abi\n"
+            "lib = _abi.lib()\n"
+            "assert lib.jo_set_launch_override(_abi.JO_KNOB_QK_SPLIT, -1) == 0\n"
+            "print('loaded')\n" % str(PKG))
+    env = dict(os.environ, JO_QK_SPLIT="3", JO_KV_SPLIT="2", JO_GEMM_SHAPE="7x")
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env,
+                       timeout=300)
+    assert r.returncode == 0 and "loaded" in r.stdout, r.stderr
+    assert "ignoring JO_QK_SPLIT=3" in r.stderr and "ignoring JO_GEMM_SHAPE=7x" in r.stderr
+    assert "JO_KV_SPLIT" not in r.stderr
 
 
 def test_empty_inputs_are_noops(abi):

@@ -112,3 +112,73 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=300)
     out = r.stdout + r.stderr
     assert "one GPU" in out and "--gpus 2" in out, out
+
+
+def _synthetic_results(bench):
+    """A results dict with every line a default run produces, each carrying
+    every field the timing code writes (long figures, as on the GPU)."""
+    from joyomni_ops import workloads as W
+    fake = {"us_per_call": 17.123456, "eager_us_per_call": 18.98765, "min_us_per_call": 17.0123,
+            "max_us_per_call": 17.9876, "timed_calls": 500, "warmup_calls": 20,
+            "timing": "hip-graph"}
+    results = {}
+    for n, cfg in W.CONFIGS.items():
+        if n == "B_img":
+            continue
+        r = bench._finish(dict(fake), W.algorithmic_bytes(cfg), 13, 51_234_567)
+        r.update(torch_reference_us_per_call=3988.123, unfused_two_calls_us_per_call=73.456,
+                 copy_then_rmsnorm_us_per_call=20.234, cpu_us_per_call=153211.7,
+                 cpu_gbps=0.63, cpu_iters=13, cpu_threads=16, gpu_over_cpu=8012.3,
+                 stream_ceiling="S_" + n, stream_ceiling_us=17.3456,
+                 frac_of_stream_ceiling=1.0081, best_stream="S_" + n + "@no-weight",
+                 best_stream_us=17.1, frac_of_best_stream=0.998)
+        if W.algorithmic_flops(cfg) is not None:
+            r.pop("frac_of_peak", None)
+            r.update(bound="mfma", algorithmic_flops=W.algorithmic_flops(cfg), tflops=2329.123,
+                     frac_of_fp8_peak=0.4658, ab_eager_us_per_call=138.21,
+                     hipblaslt_us_per_call=167.33, hipblaslt_tflops=1923.4,
+                     hipblaslt_over_ours=1.2104)
+        results[n] = r
+    for n, s in bench.STREAMS.items():
+        r = bench._finish(dict(fake), bench.stream_bytes(s), 13, 51_234_567)
+        r.update(shape="x" * 90, kind="stream-ceiling")
+        results[n] = r
+    results["B_img"] = {"us_per_call": 633.123, "reference_composition_us_per_call": 779.456,
+                        "reference_over_fused": 1.231, "min_us_per_call": 630.1,
+                        "max_us_per_call": 640.2, "gemm_flops": 1_260_000_000_000,
+                        "block_tflops": 1980.1, "timed_calls": 500, "timing": "hip-graph",
+                        "shape": "y" * 100}
+    return results
+
+
+def test_summary_line_fits_the_driver_tail(bench):
+    """The stdout line stays whole for a reader that keeps only the last 16 KB
+    of stdout: a full-size results dict (every config, stream ceiling and
+    comparison field) gives a line under 4 KB that still carries the headline,
+    its roofline (with traffic), the CPU baseline and every BASELINE config."""
+    import json
+    results = _synthetic_results(bench)
+    cpu = {"gbps": 1.83, "us_per_call": 53100.2, "threads": 16, "iters": 38, "seconds": 2.1}
+    line = bench.summary_line(results, cpu, 20, 5, "AMD EPYC 9575F 64-Core Processor" * 3,
+                              "bench_detail.json")
+    text = json.dumps(line, separators=(",", ":"))
+    assert len(text.encode()) <= bench.SUMMARY_MAX_BYTES, len(text)
+    back = json.loads(text)
+    for k in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+              "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config",
+              "roofline", "cpu_baseline"):
+        assert k in back, k
+    assert back["value"] == results["C1"]["gbps"]
+    rf = back["roofline"]
+    assert rf["bound"] == "hbm" and rf["unit"] == "GB/s" and rf["peak"] == 8000.0
+    assert abs(rf["frac"] - rf["achieved"] / rf["peak"]) < 1e-3
+    assert "traffic" in rf
+    cb = back["cpu_baseline"]
+    assert cb["kind"] == "port" and cb["cores"] == 16 and cb["unit"] == "GB/s"
+    for n in bench.BASELINE_CONFIGS:
+        e = back["configs"][n]
+        assert {"us", "frac", "S_us", "fS", "cpu_us"} <= set(e), (n, e)
+    for n in ("N3", "N4", "G1", "G3", "G4", "R_qks", "T_ln", "B_img"):
+        assert n in back["ops"], n
+    assert not any(n.startswith("S_") for n in back["ops"])
+    assert back["ops"]["G3"]["frac"] == 0.466 and back["ops"]["G3"]["blt_x"] == 1.21

@@ -200,3 +200,16 @@ def test_golden_gelu_quant(fx, dev):
     assert bool(((act - ref).abs() <= tol)[fin].all()), "activation beyond 1 bf16 ulp"
     qo, so = ops.per_token_quant_fp8(a.cpu())
     assert torch.equal(q.view(torch.uint8).cpu(), qo) and torch.equal(s.cpu(), so)
+    # The stored bytes and scales (the oracle's quantization of its own rounded
+    # activation): on a row whose scale the kernel reproduced, every element
+    # whose activation the kernel rounded as the oracle did carries the
+    # fixture's byte.
+    qf = torch.from_numpy(fx["gelu_q"])
+    sf = torch.from_numpy(fx["gelu_s"])
+    sk = s.cpu()
+    srow = (sk == sf) | (torch.isnan(sk) & torch.isnan(sf))
+    assert int(srow.sum()) >= (srow.numel() + 1) // 2, f"scales {sk} vs fixture {sf}"
+    same = (a.cpu() == ref.to(torch.bfloat16)) | (torch.isnan(act) & torch.isnan(ref))
+    mask = same & srow[:, None]
+    assert int(mask.sum()) >= mask.numel() // 2
+    assert torch.equal(q.view(torch.uint8).cpu()[mask], qf[mask]), "fp8 bytes differ from fixture"

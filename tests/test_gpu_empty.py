@@ -137,3 +137,39 @@ def test_empty_input(dev, case):
     torch.cuda.synchronize()
     for t, shape, dtype in outs:
         assert tuple(t.shape) == shape and t.dtype == dtype, (tuple(t.shape), t.dtype)
+
+
+@pytest.mark.parametrize("shape", [-1, 0, 1, 2, 3, 4])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_fp8_scaled_mm_zero_k(dev, shape, with_bias):
+    """K == 0 on zero-width views of real operands (non-null pointers into
+    larger buffers): the output is the epilogue of a zero accumulator, the
+    bias (or zeros), under every GEMM launch shape, and no operand byte is
+    read (the views' buffers hold random bytes that would show up)."""
+    import joyomni_ops as jo
+    from joyomni_ops import _abi
+    M, N = 300, 512
+    g = torch.Generator().manual_seed(5)
+    big_a = torch.randint(0, 120, (M, 128), generator=g, dtype=torch.uint8).to(dev).view(FP8)
+    big_w = torch.randint(0, 120, (N, 128), generator=g, dtype=torch.uint8).to(dev).view(FP8)
+    a = big_a[:, :0]
+    b = big_w[:, :0].t()
+    assert a.data_ptr() != 0 and b.data_ptr() != 0 and a.stride(0) == 128 and b.stride(1) == 128
+    sa = torch.rand(M, generator=g).to(dev) + 0.5
+    sb = torch.rand(N, generator=g).to(dev) + 0.5
+    bias = (torch.randn(N, generator=g) * 4).to(BF).to(dev) if with_bias else None
+    _abi.call("jo_set_launch_override", _abi.JO_KNOB_GEMM_SHAPE, shape)
+    try:
+        y = jo.fp8_scaled_mm(a, b, sa, sb, BF, bias)
+        # the same call through the C ABI, into a buffer filled with NaN
+        out = torch.full((M, N), float("nan"), dtype=BF, device=dev)
+        _abi.call("jo_fp8_scaled_mm", a.data_ptr(), 128, big_w.data_ptr(), 128, sa.data_ptr(),
+                  sb.data_ptr(), None if bias is None else bias.data_ptr(), out.data_ptr(), N,
+                  M, N, 0, _abi.JO_DTYPE_BF16, torch.cuda.current_stream(dev).cuda_stream)
+    finally:
+        _abi.call("jo_set_launch_override", _abi.JO_KNOB_GEMM_SHAPE, -1)
+    torch.cuda.synchronize()
+    want = (bias.float() if bias is not None else torch.zeros(N, device=dev)).expand(M, N)
+    assert y.shape == (M, N) and y.dtype == BF
+    assert torch.equal(y.float(), want), "K == 0 output is not the bias"
+    assert torch.equal(out.float(), want), "K == 0 output (C ABI) is not the bias"
