@@ -352,7 +352,9 @@ int jo_norm_scale_shift_quant_fp8(const void* x, int64_t x_stride, void* residua
  * scales_a fp32 [M]; scales_b fp32 [N]; bias [N] of out_dtype or NULL;
  * out: [M, N] row-major, row stride ldo elements, out_dtype BF16 or F16.
  * K % 16 == 0, N % 8 == 0, lda and ldb multiples of 16, operands 16-byte
- * aligned (the reference's alignment rules).
+ * aligned (the reference's alignment rules). K == 0 gives the epilogue of a
+ * zero accumulator (the bias, or zeros) and reads no operand byte; mat_a and
+ * mat_b may then be NULL.
  * ------------------------------------------------------------------------ */
 int jo_fp8_scaled_mm(const void* mat_a, int64_t lda, const void* mat_b, int64_t ldb,
                      const float* scales_a, const float* scales_b, const void* bias, void* out,

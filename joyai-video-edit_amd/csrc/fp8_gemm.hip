@@ -864,7 +864,9 @@ extern "C" int jo_fp8_scaled_mm(const void* mat_a, int64_t lda, const void* mat_
   JO_REQUIRE(lda >= K && ldb >= K && ldo >= N && lda % 16 == 0 && ldb % 16 == 0 && ldo % 8 == 0,
              "%s: row strides must cover the rows and keep 16-byte alignment", op);
   if (M == 0 || N == 0) return JO_OK;
-  JO_REQUIRE(mat_a && mat_b && scales_a && scales_b && out, "%s: null pointer", op);
+  // With K == 0 no operand byte is read (torch hands zero-size views over as
+  // null pointers), and the output is the epilogue of a zero accumulator.
+  JO_REQUIRE((K == 0 || (mat_a && mat_b)) && scales_a && scales_b && out, "%s: null pointer", op);
   JO_REQUIRE(aligned(mat_a, 16) && aligned(mat_b, 16) && aligned(out, 16),
              "%s: operands must be 16-byte aligned", op);
   GemmArgs g{static_cast<const uint8_t*>(mat_a), static_cast<const uint8_t*>(mat_b), scales_a,
