@@ -222,6 +222,22 @@ int jo_fused_norm_scale_shift(const void* x, int64_t x_stride, const void* gamma
                               int norm_type, float eps, void* stream);
 
 /* ------------------------------------------------------------------------
+ * jo_fused_norm_scale_shift with per-sample modulation rows: scale and shift
+ * row i serves rows [i * mod_rows, (i + 1) * mod_rows) of x (stride 0 still
+ * broadcasts one row to all). The DiT's [B, D] AdaLN vectors over x
+ * [B * L, D] are scale/shift with mod_rows = L, read in place — the
+ * reference's caller (deploy/xvideo/models/dit/sgl_fused_ops.py:44-51)
+ * expands them into [B * L, D] copies first. Same arithmetic and limits as
+ * jo_fused_norm_scale_shift; mod_rows >= 1 (1 = a row each).
+ * ------------------------------------------------------------------------ */
+int jo_fused_norm_scale_shift_per_sample(const void* x, int64_t x_stride, const void* gamma,
+                                         const void* beta, const void* scale,
+                                         int64_t scale_stride, const void* shift,
+                                         int64_t shift_stride, int64_t mod_rows, void* y,
+                                         int64_t y_stride, int64_t M, int64_t N, int dtype,
+                                         int norm_type, float eps, void* stream);
+
+/* ------------------------------------------------------------------------
  * RMSNorm: out = (x * r) * w, r = 1/sqrt(mean(x^2) + eps), fp32 arithmetic.
  * Replaces joyomni_ops::rmsnorm (deploy/joyomni_ops/csrc/rmsnorm.cu:76-95;
  * kernel :37-61). x, out: [M, N] with row strides; weight: [N]. Any N >= 1.

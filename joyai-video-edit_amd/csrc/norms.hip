@@ -578,12 +578,12 @@ int launch_rmsnorm_dt(int dtype, const RmsArgs& a, hipStream_t stream, const cha
 
 using namespace jo;
 
-extern "C" int jo_fused_norm_scale_shift(const void* x, int64_t x_stride, const void* gamma,
-                                         const void* beta, const void* scale,
-                                         int64_t scale_stride, const void* shift,
-                                         int64_t shift_stride, void* y, int64_t y_stride,
-                                         int64_t M, int64_t N, int dtype, int norm_type,
-                                         float eps, void* stream) {
+namespace {
+int norm_scale_shift_impl(const void* x, int64_t x_stride, const void* gamma, const void* beta,
+                          const void* scale, int64_t scale_stride, const void* shift,
+                          int64_t shift_stride, int64_t mod_rows, void* y, int64_t y_stride,
+                          int64_t M, int64_t N, int dtype, int norm_type, float eps,
+                          void* stream) {
   // Checks of fused_norm_scale_shift.cu:176-196.
   JO_REQUIRE(valid_dtype(dtype), "Unsupported dtype; use float32/float16/bfloat16");
   JO_REQUIRE(norm_type == JO_NORM_LAYER || norm_type == JO_NORM_RMS,
@@ -593,14 +593,37 @@ extern "C" int jo_fused_norm_scale_shift(const void* x, int64_t x_stride, const 
   JO_REQUIRE(N % 4 == 0, "N must be divisible by 4");
   JO_REQUIRE(x_stride >= N && y_stride >= N && scale_stride >= 0 && shift_stride >= 0,
              "fused_norm_scale_shift: bad row stride");
+  JO_REQUIRE(mod_rows >= 1 && mod_rows <= UINT32_MAX,
+             "fused_norm_scale_shift: mod_rows must be positive");
   if (M == 0 || N == 0) return JO_OK;
   JO_REQUIRE(x && y && scale && shift, "fused_norm_scale_shift: null pointer");
   NormArgs a{x, x_stride, nullptr, 0, nullptr, 0, gamma, beta, scale, scale_stride, shift,
              shift_stride, y, y_stride, M, static_cast<int>(N), eps};
+  a.mod_rows = static_cast<uint32_t>(mod_rows);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (norm_type == JO_NORM_LAYER)
     return launch_norm_mod_dt<kLayer, false>(dtype, a, st, "fused_norm_scale_shift");
   return launch_norm_mod_dt<kRms, false>(dtype, a, st, "fused_norm_scale_shift");
+}
+}  // namespace
+
+extern "C" int jo_fused_norm_scale_shift(const void* x, int64_t x_stride, const void* gamma,
+                                         const void* beta, const void* scale,
+                                         int64_t scale_stride, const void* shift,
+                                         int64_t shift_stride, void* y, int64_t y_stride,
+                                         int64_t M, int64_t N, int dtype, int norm_type,
+                                         float eps, void* stream) {
+  return norm_scale_shift_impl(x, x_stride, gamma, beta, scale, scale_stride, shift,
+                               shift_stride, 1, y, y_stride, M, N, dtype, norm_type, eps, stream);
+}
+
+extern "C" int jo_fused_norm_scale_shift_per_sample(
+    const void* x, int64_t x_stride, const void* gamma, const void* beta, const void* scale,
+    int64_t scale_stride, const void* shift, int64_t shift_stride, int64_t mod_rows, void* y,
+    int64_t y_stride, int64_t M, int64_t N, int dtype, int norm_type, float eps, void* stream) {
+  return norm_scale_shift_impl(x, x_stride, gamma, beta, scale, scale_stride, shift,
+                               shift_stride, mod_rows, y, y_stride, M, N, dtype, norm_type, eps,
+                               stream);
 }
 
 extern "C" int jo_rmsnorm(const void* x, int64_t x_stride, const void* weight, void* out,

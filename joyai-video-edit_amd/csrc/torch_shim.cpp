@@ -521,6 +521,49 @@ torch::Tensor fused_add_layernorm_scale_shift(const torch::Tensor& x, torch::Ten
   return y;
 }
 
+// fused_norm_scale_shift with scale / shift of [N], [M, N] or [B, N] (B
+// dividing M: one row per sample of M / B consecutive rows of x), read in
+// place: the per-sample AdaLN vectors of a [B, L, D] batch without the
+// [B * L, D] copies the reference's caller makes (sgl_fused_ops.py:44-51).
+torch::Tensor fused_norm_scale_shift_per_sample(const torch::Tensor& x,
+                                                const c10::optional<torch::Tensor>& gamma_opt,
+                                                const c10::optional<torch::Tensor>& beta_opt,
+                                                const torch::Tensor& scale,
+                                                const torch::Tensor& shift, int64_t norm_type,
+                                                double eps) {
+  JO_CHECK_CUDA(x);
+  TORCH_CHECK(x.dim() == 2 && x.stride(-1) == 1, "x must be 2D [M, N] with contiguous rows");
+  const int64_t M = x.size(0), N = x.size(1);
+  TORCH_CHECK(N % 4 == 0, "N must be divisible by 4");
+  TORCH_CHECK(scale.dtype() == x.dtype() && shift.dtype() == x.dtype(),
+              "x/scale/shift dtype must match");
+  TORCH_CHECK(norm_type == 0 || norm_type == 1, "norm_type must be 0 (layer) or 1 (rms)");
+  int64_t group = 0;
+  const int64_t sc_stride = mod_stride(scale, M, N, "scale", &group);
+  const int64_t sh_stride = mod_stride(shift, M, N, "shift", &group);
+  const bool has_gamma = gamma_opt.has_value() && gamma_opt->defined();
+  const bool has_beta = beta_opt.has_value() && beta_opt->defined();
+  if (has_gamma)
+    TORCH_CHECK(gamma_opt->is_cuda() && gamma_opt->numel() == N && gamma_opt->is_contiguous() &&
+                    gamma_opt->dtype() == x.dtype(),
+                "gamma must be [N] contiguous of x's dtype");
+  if (has_beta)
+    TORCH_CHECK(beta_opt->is_cuda() && beta_opt->numel() == N && beta_opt->is_contiguous() &&
+                    beta_opt->dtype() == x.dtype(),
+                "beta must be [N] contiguous of x's dtype");
+  const int dt = dtype_code(x);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  auto y = torch::empty({M, N}, x.options());
+  if (M == 0) return y;
+  check_status(jo_fused_norm_scale_shift_per_sample(
+                   x.data_ptr(), row_stride(x), has_gamma ? gamma_opt->data_ptr() : nullptr,
+                   has_beta ? beta_opt->data_ptr() : nullptr, scale.data_ptr(), sc_stride,
+                   shift.data_ptr(), sh_stride, group > 0 ? group : 1, y.data_ptr(), N, M, N, dt,
+                   static_cast<int>(norm_type), static_cast<float>(eps), current_stream(x)),
+               "fused_norm_scale_shift_per_sample");
+  return y;
+}
+
 void rmsnorm_quant_fp8(const torch::Tensor& x, const torch::Tensor& weight, double eps,
                        torch::Tensor output_q, torch::Tensor output_s, int64_t group_size) {
   JO_CHECK_CUDA(x);
@@ -797,6 +840,9 @@ TORCH_LIBRARY(joyomni_ops, m) {
       "Tensor(a!)? output_act=None) -> ()");
   m.def("apply_rotary_emb(Tensor x, Tensor cos, Tensor sin) -> Tensor");
   m.def("rmsnorm_heads(Tensor x, Tensor weight, float eps, int round_first) -> Tensor");
+  m.def(
+      "fused_norm_scale_shift_per_sample(Tensor x, Tensor? gamma_opt, Tensor? beta_opt, "
+      "Tensor scale, Tensor shift, int norm_type, float eps) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(joyomni_ops, CUDA, m) {
@@ -817,4 +863,5 @@ TORCH_LIBRARY_IMPL(joyomni_ops, CUDA, m) {
   m.impl("gelu_tanh_quant_fp8", &joyomni_ops::gelu_tanh_quant_fp8);
   m.impl("apply_rotary_emb", &joyomni_ops::apply_rotary_emb);
   m.impl("rmsnorm_heads", &joyomni_ops::rmsnorm_heads);
+  m.impl("fused_norm_scale_shift_per_sample", &joyomni_ops::fused_norm_scale_shift_per_sample);
 }

@@ -12,7 +12,8 @@ New ops (no reference signature): fused_qk_norm_rope_3d_grid,
 fused_qk_norm_rope_3d_kvcache, fused_qk_norm_rope_3d_paired_kstage,
 fused_qk_norm_rope_3d_grid_kstage, fused_add_layernorm_scale_shift,
 rmsnorm_quant_fp8, norm_scale_shift_quant_fp8, kv_commit_rope,
-apply_rotary_emb, rmsnorm_heads, plus rope_freqs() to build the
+apply_rotary_emb, rmsnorm_heads, gelu_tanh_quant_fp8,
+fused_norm_scale_shift_per_sample, plus rope_freqs() to build the
 [2, head_dim/2] frequency table the grid ops read.
 """
 from __future__ import annotations
@@ -53,6 +54,7 @@ __all__ = [
     "fused_qk_norm_rope_3d_paired_kstage",
     "fused_qk_norm_rope_3d_grid_kstage",
     "gelu_tanh_quant_fp8",
+    "fused_norm_scale_shift_per_sample",
 ]
 
 _ops = torch.ops.joyomni_ops
@@ -211,6 +213,15 @@ def fused_add_layernorm_scale_shift(x, residual, scale, shift, gate=None, gamma=
     per sample of M / B consecutive rows, the DiT's per-sample AdaLN vectors).
     """
     return _ops.fused_add_layernorm_scale_shift(x, residual, gate, gamma, beta, scale, shift, eps)
+
+
+def fused_norm_scale_shift_per_sample(x, gamma, beta, scale, shift, norm_type, eps=1e-5):
+    """fused_norm_scale_shift with scale/shift of [N], [M, N] or [B, N] (B
+    dividing M: row i serves rows i*M/B .. (i+1)*M/B - 1 of x), read in place
+    — the per-sample AdaLN vectors of a [B, L, D] batch flattened to
+    [B*L, D], without expanded copies."""
+    nt = 0 if norm_type == "layer" else 1 if norm_type == "rms" else -1
+    return _ops.fused_norm_scale_shift_per_sample(x, gamma, beta, scale, shift, nt, eps)
 
 
 def rmsnorm_quant_fp8(x, weight, eps, output_q, output_s, group_size=0):

@@ -59,6 +59,8 @@ SIGNATURES: dict[str, list] = {
         _F, _P, _P, _P, c_int32, c_int32, c_int32, c_int32, c_int32, _F, _P],
     "jo_fused_norm_scale_shift": [
         _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, c_int, c_int, _F, _P],
+    "jo_fused_norm_scale_shift_per_sample": [
+        _P, _I64, _P, _P, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, c_int, c_int, _F, _P],
     "jo_rmsnorm": [_P, _I64, _P, _P, _I64, _I64, _I64, c_int, _F, _P],
     "jo_rmsnorm_heads": [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, c_int, _F, c_int, _P],
     "jo_fused_add_layernorm_scale_shift": [

@@ -5,9 +5,9 @@ MMDoubleStreamBlock.forward calls, dit.py:351-476) and of the activation
 quantization step of Fp8Linear.forward (deploy/xvideo/models/dit/fp8_linear.py:138-169).
 Same arguments, same results; the differences are in the HBM traffic:
 
-  fused_layernorm_modulate  passes per-sample shift/scale as stride-0 rows
-                            instead of materialising [B*L, D] copies
-                            (sgl_fused_ops.py:44-51 expands and copies them).
+  fused_layernorm_modulate  reads per-sample shift/scale [B, D] in place, one
+                            row per sample, instead of materialising [B*L, D]
+                            copies (sgl_fused_ops.py:44-51 expands and copies them).
   fused_qk_norm_rope_3d     identical contract (contiguous copies of q/k, tables
                             halved and cast to bf16 as sgl_fused_ops.py:73-94).
   rmsnorm_qk_bf16           normalizes the K slice of the packed qkv in place of
@@ -48,7 +48,7 @@ from typing import Optional, Sequence, Tuple
 import torch
 
 from . import (fp8_scaled_mm, fused_add_layernorm_scale_shift, fused_norm_scale_shift,
-               fused_qk_norm_rope_3d_grid, fused_qk_norm_rope_3d_grid_kstage, gelu_tanh_quant_fp8,
+               fused_norm_scale_shift_per_sample, fused_qk_norm_rope_3d_grid, fused_qk_norm_rope_3d_grid_kstage, gelu_tanh_quant_fp8,
                fused_qk_norm_rope_3d_paired, fused_qk_norm_rope_3d_paired_kstage,
                kv_commit_rope, norm_scale_shift_quant_fp8, rmsnorm, rmsnorm_heads,
                rope_freqs, sgl_per_token_quant_fp8)
@@ -57,19 +57,6 @@ from . import (fp8_scaled_mm, fused_add_layernorm_scale_shift, fused_norm_scale_
 def available() -> bool:
     """The reference's availability probe (sgl_fused_ops.py:14-27): the ops load at import."""
     return True
-
-
-def _mod_rows(t: torch.Tensor, B: int, L: int, D: int) -> torch.Tensor:
-    """shift/scale as [B*L, D] without copying a per-sample vector: [B, D] or
-    [B, 1, D] with B == 1 becomes a stride-0 expanded view; per-token tensors
-    are reshaped (copied only if their layout needs it)."""
-    if t.dim() == 2:
-        t = t.unsqueeze(1)
-    if t.shape[1] == 1 and L != 1:
-        if B == 1:
-            return t.reshape(1, D).expand(L, D)
-        t = t.expand(B, L, D)
-    return t.reshape(B * L, D)
 
 
 def fused_layernorm_modulate(
@@ -82,11 +69,15 @@ def fused_layernorm_modulate(
     eps: float = 1e-6,
 ) -> torch.Tensor:
     """LayerNorm(x; weight, bias) * (1 + scale) + shift for x [B, L, D]
-    (sgl_fused_ops.py:30-54). shift/scale: [B, D], [B, 1, D] or [B, L, D]."""
+    (sgl_fused_ops.py:30-54). shift/scale: [B, D], [B, 1, D] or [B, L, D].
+
+    Per-sample vectors are read in place, one row per sample of L tokens
+    (fused_norm_scale_shift_per_sample), for any B: no [B*L, D] expanded
+    copies; per-token modulation is read a row each."""
     B, L, D = x.shape
-    x_2d = x.reshape(-1, D)
-    out = fused_norm_scale_shift(x_2d, weight, bias, _mod_rows(scale, B, L, D),
-                                 _mod_rows(shift, B, L, D), "layer", eps)
+    out = fused_norm_scale_shift_per_sample(x.reshape(-1, D), weight, bias,
+                                            _mod_per_sample(scale, B, L, D),
+                                            _mod_per_sample(shift, B, L, D), "layer", eps)
     return out.reshape(B, L, D)
 
 

@@ -1,7 +1,19 @@
 """Comparison helpers shared by the parity tests."""
 from __future__ import annotations
 
+import json
+import os
+
 import torch
+
+
+def record_audit(what: str, stats: dict) -> None:
+    """Append one parity-audit record (JSON line) to the file named by
+    JO_ULP_AUDIT, when that variable is set."""
+    path = os.environ.get("JO_ULP_AUDIT")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(dict(what=what, **stats)) + "\n")
 
 
 def bf16_ulp(ref: torch.Tensor) -> torch.Tensor:
@@ -11,7 +23,7 @@ def bf16_ulp(ref: torch.Tensor) -> torch.Tensor:
 
 
 def assert_bf16_within_ulp(out: torch.Tensor, ref_f32: torch.Tensor, floor_scale=None,
-                           n_ulp: float = 1.0, what: str = ""):
+                           n_ulp: float = 1.0, what: str = "", floor_cap: float | None = None):
     """|out - ref| <= n_ulp bf16 ulps of ref, element-wise.
 
     The fp32 reference and the kernel accumulate in different orders; where a
@@ -19,12 +31,19 @@ def assert_bf16_within_ulp(out: torch.Tensor, ref_f32: torch.Tensor, floor_scale
     the fp32 rounding of the terms dominates a tiny result. `floor_scale`
     (a tensor broadcastable to ref, e.g. the row/head max |ref|) floors the
     ulp at that of floor_scale * 2^-10 to absorb that cancellation.
+
+    Returns the audit of that floor: `floor_only`, the number of finite
+    elements within n_ulp of the floored ulp but not of their own bf16 ulp,
+    and `floor_only_max_ulps`, the largest error among them in bf16 ulps of
+    the element itself. With `floor_cap` set, at most that fraction of the
+    elements may pass through the floor alone.
     """
     out = out.float().cpu()
     ref = ref_f32.float().cpu()
-    ulp = bf16_ulp(ref)
+    own = bf16_ulp(ref)
+    ulp = own
     if floor_scale is not None:
-        ulp = torch.maximum(ulp, bf16_ulp(floor_scale.float().cpu() * 2.0 ** -10))
+        ulp = torch.maximum(own, bf16_ulp(floor_scale.float().cpu() * 2.0 ** -10))
     err = (out - ref).abs()
     nan_ok = torch.isnan(out) == torch.isnan(ref)
     assert bool(nan_ok.all()), f"{what}: NaN pattern differs"
@@ -36,6 +55,23 @@ def assert_bf16_within_ulp(out: torch.Tensor, ref_f32: torch.Tensor, floor_scale
             f"{what}: {int(bad.sum())} elements beyond {n_ulp} bf16 ulp; first at flat index {i}: "
             f"out={out.reshape(-1)[i].item()!r} ref={ref.reshape(-1)[i].item()!r} "
             f"ulp={ulp.reshape(-1)[i].item()!r}; max err/ulp={(err / ulp)[fin].max().item():.3f}")
+    floor_only = (err > n_ulp * own) & fin
+    n_floor = int(floor_only.sum())
+    stats = {"elements": ref.numel(), "floor_only": n_floor,
+             "floor_only_frac": n_floor / max(1, ref.numel()),
+             "floor_only_max_ulps": float((err / own)[floor_only].max()) if n_floor else 0.0}
+    if floor_scale is not None and n_floor:
+        # the same errors relative to the floor's scale (the head / row maximum):
+        # meaningful where the reference itself is 0 or nearly so
+        rel = err / floor_scale.float().cpu().expand_as(err).clamp_min(2.0 ** -126)
+        stats["floor_only_max_rel"] = float(rel[floor_only].max())
+    record_audit(what, stats)
+    if floor_cap is not None:
+        assert n_floor <= floor_cap * ref.numel(), (
+            f"{what}: {n_floor} of {ref.numel()} elements pass only through the 2^-10 floor "
+            f"(cap {floor_cap:g}); largest error among them {stats['floor_only_max_ulps']:.1f} "
+            "bf16 ulps of the element")
+    return stats
 
 
 def f32_ulp(v: torch.Tensor) -> torch.Tensor:

@@ -35,7 +35,7 @@ def test_header_declares_all_entry_points():
                  "jo_fused_qk_norm_rope_3d_kvcache", "jo_fused_norm_scale_shift", "jo_rmsnorm",
                  "jo_fused_add_layernorm_scale_shift", "jo_rmsnorm_quant_fp8",
                  "jo_rmsnorm_heads", "jo_norm_scale_shift_quant_fp8", "jo_fp8_scaled_mm",
-                 "jo_kv_commit_rope"):
+                 "jo_kv_commit_rope", "jo_fused_norm_scale_shift_per_sample"):
         assert name in fns, name
 
 
@@ -111,6 +111,12 @@ BAD_CALLS = [
      "divisible by 4"),
     ("jo_fused_norm_scale_shift", (16, 8, None, None, 16, 8, 16, 8, 16, 8, 4, 8, 7, 0, 1e-6, None),
      "dtype"),
+    ("jo_fused_norm_scale_shift_per_sample",
+     (16, 8, None, None, 16, 8, 16, 8, 0, 16, 8, 4, 8, 2, 0, 1e-6, None), "mod_rows"),
+    ("jo_fused_norm_scale_shift_per_sample",
+     (16, 8, None, None, 16, 8, 16, 8, 2, 16, 8, 4, 8, 2, 2, 1e-6, None), "norm_type"),
+    ("jo_fused_norm_scale_shift_per_sample",
+     (None, 8, None, None, 16, 8, 16, 8, 2, 16, 8, 4, 8, 2, 0, 1e-6, None), "null pointer"),
     # launch-size bounds: a launch's work-item count must stay below 2^32 (up to 8 waves of
     # 64 lanes per QK token, 2 waves per KV-pool row, one 256-thread workgroup per row)
     ("jo_fused_qk_norm_rope_3d_paired",
@@ -214,6 +220,8 @@ def test_empty_inputs_are_noops(abi):
                                 None) == abi.JO_OK
     assert lib.jo_fused_norm_scale_shift(None, 8, None, None, None, 0, None, 0, None, 8, 0, 8, 2,
                                          0, 1e-6, None) == abi.JO_OK
+    assert lib.jo_fused_norm_scale_shift_per_sample(None, 8, None, None, None, 0, None, 0, 4,
+                                                    None, 8, 0, 8, 2, 0, 1e-6, None) == abi.JO_OK
     assert lib.jo_fused_qk_norm_rope_3d_paired(None, None, 1, 0, 2, 128, 0, 256, 0, 256, 1e-6,
                                                None, None, None, None, None) == abi.JO_OK
     assert lib.jo_fused_add_layernorm_scale_shift(None, 8, None, 8, None, 0, None, None, None, 0,
@@ -264,7 +272,8 @@ def test_torch_ops_register_reference_schemas():
         assert getattr(torch.ops.joyomni_ops, name).default._schema == expected, name
     for name in ("fused_qk_norm_rope_3d_grid", "fused_qk_norm_rope_3d_kvcache",
                  "fused_add_layernorm_scale_shift", "rmsnorm_quant_fp8",
-                 "norm_scale_shift_quant_fp8", "kv_commit_rope", "apply_rotary_emb"):
+                 "norm_scale_shift_quant_fp8", "kv_commit_rope", "apply_rotary_emb",
+                 "fused_norm_scale_shift_per_sample"):
         assert hasattr(torch.ops.joyomni_ops, name)
     assert jo.has_fp8()
 

@@ -38,7 +38,7 @@ def test_deploy_qk_table(dev):
         ref = ops.qk_norm_rope_f32(x.reshape(d["B"], d["L"], d["H"], d["D"]), w, t["cos"], t["sin"],
                                    d["eps"])
         assert_bf16_within_ulp(out.cpu().reshape(ref.shape), ref, row_floor(ref),
-                               what=f"R_qk {name}")
+                               what=f"R_qk {name}", floor_cap=1e-4)
 
 
 def test_deploy_norm_scale_shift_rows(dev):

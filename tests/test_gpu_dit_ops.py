@@ -44,6 +44,67 @@ def test_fused_layernorm_modulate(dev, B, L, D, affine, mod_shape):
     assert_within_ulp(y.cpu(), ref, torch.bfloat16, rowmax(ref), what="layernorm_modulate")
 
 
+@pytest.mark.parametrize("mod_shape", ["BD", "B1D"])
+def test_fused_layernorm_modulate_per_sample_in_place(dev, mod_shape):
+    """B = 2 per-sample shift / scale: read in place (the only new allocation is
+    the output: no [B*L, D] expanded copies), bit-identical to the reference
+    op on the expanded copies the reference caller makes
+    (sgl_fused_ops.py:44-51), and within the bar of the oracle."""
+    import joyomni_ops as jo
+    from joyomni_ops import dit_ops
+    B, L, D = 2, 1560, 3072
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(B, L, D, generator=g).to(torch.bfloat16)
+    shp = (B, D) if mod_shape == "BD" else (B, 1, D)
+    shift = (0.2 * torch.randn(shp, generator=g)).to(torch.bfloat16)
+    scale = (0.2 * torch.randn(shp, generator=g)).to(torch.bfloat16)
+    xd, shd, scd = x.to(dev), shift.to(dev), scale.to(dev)
+    dit_ops.fused_layernorm_modulate(xd, shd, scd)  # warm the allocator's pools
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    y = dit_ops.fused_layernorm_modulate(xd, shd, scd)
+    torch.cuda.synchronize()
+    extra = torch.cuda.max_memory_allocated(dev) - base
+    out_bytes = y.numel() * y.element_size()
+    assert extra <= out_bytes + 4096, f"{extra} bytes allocated for a {out_bytes}-byte output"
+    sc2 = scd.reshape(B, 1, D).expand(B, L, D).reshape(-1, D).contiguous()
+    sh2 = shd.reshape(B, 1, D).expand(B, L, D).reshape(-1, D).contiguous()
+    y_ref_op = jo.fused_norm_scale_shift(xd.reshape(-1, D), None, None, sc2, sh2, "layer", 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(y.reshape(-1, D), y_ref_op), "differs from the op on expanded copies"
+    ref = ops.norm_scale_shift_f32(x.reshape(-1, D), None, None, sc2.cpu(), sh2.cpu(), 0, 1e-6)
+    assert_within_ulp(y.cpu().reshape(-1, D), ref, torch.bfloat16, rowmax(ref),
+                      what="per-sample layernorm_modulate")
+
+
+def test_norm_scale_shift_per_sample_op(dev):
+    """The per-sample op: [N], [M, N] and [B, N] modulation, LN and RMS, with
+    gamma / beta, each bit-identical to the reference op on the expanded rows;
+    shapes that do not divide M are refused."""
+    import joyomni_ops as jo
+    M, N, B = 96, 512, 4
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(M, N, generator=g).to(torch.bfloat16).to(dev)
+    gam = (1 + 0.1 * torch.randn(N, generator=g)).to(torch.bfloat16).to(dev)
+    bet = (0.1 * torch.randn(N, generator=g)).to(torch.bfloat16).to(dev)
+    for rows in (1, B, M):
+        sc = (0.2 * torch.randn(rows, N, generator=g)).to(torch.bfloat16).to(dev)
+        sh = (0.2 * torch.randn(rows, N, generator=g)).to(torch.bfloat16).to(dev)
+        sc_in, sh_in = (sc[0], sh[0]) if rows == 1 else (sc, sh)
+        full_sc = sc.repeat_interleave(M // rows, dim=0)
+        full_sh = sh.repeat_interleave(M // rows, dim=0)
+        for nt in ("layer", "rms"):
+            for gb in ((None, None), (gam, bet)):
+                y = jo.fused_norm_scale_shift_per_sample(x, gb[0], gb[1], sc_in, sh_in, nt, 1e-6)
+                r = jo.fused_norm_scale_shift(x, gb[0], gb[1], full_sc, full_sh, nt, 1e-6)
+                torch.cuda.synchronize()
+                assert torch.equal(y, r), (rows, nt, gb[0] is None)
+    bad = torch.zeros(5, N, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(RuntimeError, match="B dividing M"):
+        jo.fused_norm_scale_shift_per_sample(x, None, None, bad, bad, "layer", 1e-6)
+
+
 def test_fused_qk_norm_rope_3d_dit_tables(dev):
     """Reference contract: q/k views of qkv, fp32 [1, L, D] tables; returns new tensors."""
     from joyomni_ops import dit_ops

@@ -42,9 +42,18 @@ def rand_qk(B, L, H, D, seed):
     return q, k, qw, kw
 
 
+# Where at least this many elements are checked, at most FLOOR_CAP of them may
+# pass only through the 2^-10 head-max floor (the rest within 1 ulp of their
+# own value).
+FLOOR_CAP = 1e-4
+FLOOR_CAP_MIN_ELEMENTS = 1 << 20
+
+
 def check_qk(out, x, w, cos, sin, B, L, H, D, what, eps=1e-6):
     ref = ops.qk_norm_rope_f32(x.reshape(B, L, H, D), w, cos, sin, eps)
-    assert_bf16_within_ulp(out.reshape(B, L, H, D), ref, head_floor(ref), what=what)
+    cap = FLOOR_CAP if ref.numel() >= FLOOR_CAP_MIN_ELEMENTS else None
+    return assert_bf16_within_ulp(out.reshape(B, L, H, D), ref, head_floor(ref), what=what,
+                                  floor_cap=cap)
 
 
 # ---------------------------------------------------------------------------
@@ -207,6 +216,8 @@ def test_kvcache_mode(abi, dev, stream_handle, small):
     for f, slot in enumerate(ops.ring_slots(F, slots, slot0)):
         written.add(slot)
         r = ref_k[:, f * ft:(f + 1) * ft]
-        assert_bf16_within_ulp(c[:, slot], r, head_floor(r), what=f"cache slot {slot}")
+        cap = FLOOR_CAP if r.numel() >= FLOOR_CAP_MIN_ELEMENTS else None
+        assert_bf16_within_ulp(c[:, slot], r, head_floor(r), what=f"cache slot {slot}",
+                               floor_cap=cap)
     for slot in set(range(slots)) - written:
         assert bool((c[:, slot] == 7.0).all()), f"slot {slot} must be untouched"
