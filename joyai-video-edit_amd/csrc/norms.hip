@@ -48,6 +48,14 @@ __device__ __forceinline__ int64_t mod_row(const NormArgs& a, int64_t row) {
 constexpr int kLayer = JO_NORM_LAYER;
 constexpr int kRms = JO_NORM_RMS;
 
+// A chunk of 1.0 values of the element type.
+template <class Tag>
+__device__ __forceinline__ u32x4 ones_chunk() {
+  constexpr uint32_t w = Tag::kBytes == 4 ? 0x3F800000u
+                         : std::is_same_v<Tag, BF16> ? 0x3F803F80u : 0x3C003C00u;
+  return u32x4{w, w, w, w};
+}
+
 // residual + x * gate as torch.addcmul evaluates it: the product and the sum
 // are two separately rounded fp32 operations (no fused multiply-add).
 __device__ __forceinline__ float residual_update(float res, float x, float gate, bool gated) {
@@ -86,8 +94,14 @@ __device__ __forceinline__ u32x4 ld_mod(const void* base, int64_t stride, int64_
 // 56-82 (the input Fp8Linear.forward quantizes, fp8_linear.py:138-169)
 // instead of being written.
 // ---------------------------------------------------------------------------
+//
+// EXACT (N == LPR * CH * V, taken with BCAST): every lane's chunks lie inside
+// the row, so the per-lane bounds tests go; a row past M (in the last
+// workgroup) reads row M - 1 and stores nothing. With rows of one or more
+// whole waves the row index is made wave-uniform, so each row's base address
+// is scalar and the lanes add 32-bit offsets to it.
 template <class Tag, int LPR, int CH, int NT, bool ADD, bool QNT, bool BCAST = false,
-          bool EARLY = false>
+          bool EARLY = false, bool EXACT = false>
 __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
   constexpr int V = Tag::kVec;
   constexpr int RPB = kBlock / LPR;
@@ -97,10 +111,29 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
   __shared__ float red_c[kBlock / kWave];
   __shared__ float red_d[kBlock / kWave];
   const int lane = threadIdx.x % LPR;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
+  const int rib = (EXACT && LPR >= kWave)
+                      ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / LPR))
+                      : static_cast<int>(threadIdx.x / LPR);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + rib;
   const bool row_ok = row < a.M;
-  const int64_t mrow = mod_row(a, row);
+  const int64_t lrow = (EXACT && !row_ok) ? a.M - 1 : row;  // the row this thread reads
+  const int64_t mrow = mod_row(a, lrow);
   const int N = a.N;
+  // EXACT: the rows' base addresses, and chunk e of a row at base + e * bytes.
+  const void* xrow = byte_off(a.x, lrow * a.xs * Tag::kBytes);
+  void* rrow = ADD ? byte_off(a.res, lrow * a.rs * Tag::kBytes) : nullptr;
+  auto ld_x = [&](int e) {
+    return EXACT ? ld16_nt(byte_off(xrow, e * Tag::kBytes)) : ld_row<Tag>(a.x, row * a.xs, e);
+  };
+  auto ld_res = [&](int e) {
+    return EXACT ? ld16_nt(byte_off(rrow, e * Tag::kBytes)) : ld_row<Tag>(a.res, row * a.rs, e);
+  };
+  auto st_res = [&](int e, const u32x4& v) {
+    if constexpr (EXACT)
+      st16_nt(byte_off(rrow, e * Tag::kBytes), v);
+    else
+      st_row<Tag>(a.res, row * a.rs, e, v);
+  };
 
   // BCAST: one scale row and one shift row for all rows (stride 0, no
   // gamma), fetched before the row itself so that their (cached) latency is
@@ -112,7 +145,7 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int e = (i * LPR + lane) * V;
-      const int el = e < N ? e : 0;
+      const int el = (EXACT || e < N) ? e : 0;
       bsc[i] = ld_chunk<Tag>(a.scale, 0, el);
       bsh[i] = ld_chunk<Tag>(a.shift, 0, el);
     }
@@ -121,7 +154,7 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * V;
-    c[i] = (row_ok && e < N) ? ld_row<Tag>(a.x, row * a.xs, e) : u32x4{0u, 0u, 0u, 0u};
+    c[i] = (EXACT || (row_ok && e < N)) ? ld_x(e) : u32x4{0u, 0u, 0u, 0u};
   }
   if constexpr (ADD) {
     u32x4 rc[CH];
@@ -129,9 +162,12 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int e = (i * LPR + lane) * V;
-      const bool ok = row_ok && e < N;
-      rc[i] = ok ? ld_row<Tag>(a.res, row * a.rs, e) : u32x4{0u, 0u, 0u, 0u};
-      gc[i] = (ok && a.gate) ? ld_mod<Tag>(a.gate, a.gs, mrow, e) : u32x4{0u, 0u, 0u, 0u};
+      const bool ok = EXACT || (row_ok && e < N);
+      rc[i] = ok ? ld_res(e) : u32x4{0u, 0u, 0u, 0u};
+      // No gate is a gate of ones: x * 1 is x exactly, so res + x * 1 is
+      // res + x with its one rounding, and no per-element select is needed.
+      gc[i] = !a.gate ? ones_chunk<Tag>()
+                      : (ok ? ld_mod<Tag>(a.gate, a.gs, mrow, e) : u32x4{0u, 0u, 0u, 0u});
     }
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
@@ -140,9 +176,9 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
 #pragma unroll
       for (int j = 0; j < V; ++j)
         u[j] = residual_update(elem<Tag>(rc[i], j), elem<Tag>(c[i], j), elem<Tag>(gc[i], j),
-                               a.gate != nullptr);
+                               true);
       c[i] = pack<Tag>(u);  // the rounded residual is what gets normalized
-      if (row_ok && e < N) st_row<Tag>(a.res, row * a.rs, e, c[i]);
+      if (row_ok && (EXACT || e < N)) st_res(e, c[i]);
     }
   }
 
@@ -172,7 +208,7 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
 #pragma unroll
       for (int i = 0; i < CH; ++i) {
         const int e = (i * LPR + lane) * V;
-        const bool ok = row_ok && e < N;
+        const bool ok = EXACT || (row_ok && e < N);
         esc[i] = ok ? ld_mod<Tag>(a.scale, a.scs, mrow, e) : u32x4{0u, 0u, 0u, 0u};
         esh[i] = ok ? ld_mod<Tag>(a.shift, a.shs, mrow, e) : u32x4{0u, 0u, 0u, 0u};
       }
@@ -181,7 +217,7 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int e = (i * LPR + lane) * V;
-      if (e < N) {
+      if (EXACT || e < N) {
 #pragma unroll
         for (int j = 0; j < V; ++j) {
           const float t = elem<Tag>(c[i], j) - mean;
@@ -196,18 +232,21 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
   }
 
   // Output.
-  const bool affine = a.gamma != nullptr;
+  // BCAST is taken only without gamma: no weight loads in the output loop
+  // (a load on a branch there costs a wait for every memory operation in
+  // flight, the row's stores included, before each chunk).
+  const bool affine = !BCAST && a.gamma != nullptr;
   const bool has_beta = affine && a.beta != nullptr && NT == kLayer;
   float yq[QNT ? CH : 1][8];  // FP8 epilogue: the rounded y of this lane
   float ymax = 0.f;           // and its NaN-propagating maximum |y|
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int e = (i * LPR + lane) * V;
-    if constexpr (QNT) {
+    if constexpr (QNT && !EXACT) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) yq[i][j] = 0.f;
     }
-    if (!(row_ok && e < N)) continue;
+    if (!EXACT && !(row_ok && e < N)) continue;
     // Per-row scale and shift are loaded here rather than with the row:
     // issuing them with x measured slower at [3120, 4096] (20.0 -> 22.7 us).
     u32x4 sc, sh;
@@ -239,6 +278,8 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
         yq[i][j] = elem<Tag>(yr, j);
         ymax = nan_max_abs(ymax, yq[i][j]);
       }
+    } else if constexpr (EXACT) {
+      if (row_ok) st16_nt(byte_off(a.y, (row * a.ys) * Tag::kBytes + e * Tag::kBytes), pack<Tag>(o));
     } else {
       st_row<Tag>(a.y, row * a.ys, e, pack<Tag>(o));
     }
@@ -266,8 +307,8 @@ __global__ __launch_bounds__(kBlock) void norm_mod_kernel(const NormArgs a) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int e = (i * LPR + lane) * V;
-      if (row_ok && e < N)
-        st8_nt(a.q + row * a.qs + e, fast ? quant8<false>(yq[i], inv) : quant8<true>(yq[i], inv));
+      if (row_ok && (EXACT || e < N))
+        st8_nt((a.q + row * a.qs) + e, fast ? quant8<false>(yq[i], inv) : quant8<true>(yq[i], inv));
     }
   }
 }
@@ -357,15 +398,29 @@ int launch_norm_mod(const NormArgs& a, hipStream_t stream, const char* op) {
       // rounds of 8192 wave slots) 23.9 -> 23.4 us, while at [3120, 4096]
       // (1.5 rounds) the same kernel lost, 18.2 -> 18.7 us.
       constexpr bool kEarlyShape = LPR == 256 && CH == 2 && NT == kLayer && !ADD && !QNT;
-      if (a.scs == 0 && a.shs == 0 && !a.gamma)
-        hipLaunchKernelGGL((norm_mod_kernel<Tag, LPR, CH, NT, ADD, QNT, true>),
-                           dim3(row_blocks(a.M, LPR)), dim3(kBlock), 0, stream, a);
-      else if (kEarlyShape && a.M * (LPR / kWave) >= 2 * kFewRows)
+      const dim3 grid(static_cast<unsigned>(row_blocks(a.M, LPR)));
+      // Rows that fill the lanes exactly (N == LPR * CH * V, 16-bit types)
+      // with broadcast modulation drop the per-lane bounds tests ([10530,
+      // 3072] residual + LayerNorm + AdaLN 45.4 -> 43.9 us, with the FP8
+      // epilogue 41.6 -> 41.2 us; with per-row scale / shift, [3120, 4096] and
+      // [4096, 4096], the same change measured 1% slower, so those keep the
+      // tested form).
+      const bool exact = Tag::kVec == 8 && int64_t{LPR} * CH * Tag::kVec == a.N;
+      if (a.scs == 0 && a.shs == 0 && !a.gamma) {
+        if (exact)
+          hipLaunchKernelGGL((norm_mod_kernel<Tag, LPR, CH, NT, ADD, QNT, true, false,
+                                              Tag::kVec == 8>),
+                             grid, dim3(kBlock), 0, stream, a);
+        else
+          hipLaunchKernelGGL((norm_mod_kernel<Tag, LPR, CH, NT, ADD, QNT, true>), grid,
+                             dim3(kBlock), 0, stream, a);
+      } else if (kEarlyShape && a.M * (LPR / kWave) >= 2 * kFewRows) {
         hipLaunchKernelGGL((norm_mod_kernel<Tag, LPR, CH, NT, ADD, QNT, false, kEarlyShape>),
-                           dim3(row_blocks(a.M, LPR)), dim3(kBlock), 0, stream, a);
-      else
-        hipLaunchKernelGGL((norm_mod_kernel<Tag, LPR, CH, NT, ADD, QNT>),
-                           dim3(row_blocks(a.M, LPR)), dim3(kBlock), 0, stream, a);
+                           grid, dim3(kBlock), 0, stream, a);
+      } else {
+        hipLaunchKernelGGL((norm_mod_kernel<Tag, LPR, CH, NT, ADD, QNT>), grid, dim3(kBlock), 0,
+                           stream, a);
+      }
     }, a.M);
   }
   if (!launched)

@@ -188,10 +188,11 @@ int launch_quant(const void* x, int64_t M, int64_t N, int64_t xs, void* q, int64
 
 // ---------------------------------------------------------------------------
 // RMSNorm -> FP8. v = (x * r) * w in fp32 (rmsnorm.cu:41-60 without the
-// rounding to the input type), r = 1/sqrt(mean(x^2) + eps) with the mean
-// square rounded once from its exact value and IEEE sqrt and division; then
-// the per_token_quant_fp8.cu:56-82 rule over the row (per token) or over
-// each 1x128 block (16 lanes x 8 values of one chunk).
+// rounding to the input type), r = 1/sqrt(mean(x^2) + eps) with IEEE
+// division and sqrt, the sum of squares in fp32 in a fixed order (below, as
+// the reference sums in fp32 in its own order, rmsnorm.cu:47-53); then the
+// per_token_quant_fp8.cu:56-82 rule over the row (per token) or over each
+// 1x128 block (16 lanes x 8 values of one chunk).
 //
 // These kernels are bound by VALU issue as much as by HBM: a wave holds a
 // whole 3072-wide row (48 values per lane) and runs ~10 instructions per value
@@ -274,29 +275,33 @@ __device__ __forceinline__ void load_row_weight(const void* x, int64_t xs, const
   }
 }
 
-// This lane's sum of squares in fp64. The squares of bf16/fp16 values are
-// exact in fp32 and their fp64 sum carries ~29 more bits than the fp32 mean
-// square it is rounded to, so the mean does not depend on the summation order
-// (the launch shape) — only a sum within ~2^-50 of an fp32 rounding midpoint
-// could tell orders apart. Each chunk's part is issued before the next chunk
-// is waited for. KEEPX keeps the fp32 values of x for the product that
-// follows (48 more registers, 48 fewer instructions per row); otherwise the
-// unpacked values die here and are unpacked again.
+// This lane's sum of squares, in fp32 in a fixed order: two accumulators,
+// element j of each chunk (chunks in order, j = 0..7) into accumulator j % 2
+// with one fused multiply-add (x^2 of a bf16/fp16 value is exact in fp32, so
+// each step is the correctly rounded acc + x^2), then acc[0] + acc[1]. The
+// row's lanes are then added by allreduce's fixed butterfly (and, for rows
+// wider than a wave, the waves' sums in order), so the mean square is a
+// function of the row and its launch shape (LPR, CH), which the CPU oracle
+// restates step by step. (An fp64 exact sum instead measured 1-3% slower on
+// [10530, 3072] and [4725, 3072]: one more conversion per value and 64-bit
+// cross-lane steps.) Each chunk's part is issued before the next chunk is
+// waited for. KEEPX keeps the fp32 values of x for the product that follows
+// (48 more registers, 48 fewer instructions per row); otherwise the unpacked
+// values die here and are unpacked again.
 template <class Tag, int CH, bool KEEPX>
-__device__ __forceinline__ double lane_sum_squares(u32x4 (&c)[CH], float (&xf)[KEEPX ? CH : 1][8]) {
-  double acc[2] = {0.0, 0.0};
+__device__ __forceinline__ float lane_sum_squares(u32x4 (&c)[CH], float (&xf)[KEEPX ? CH : 1][8]) {
+  float acc[2] = {0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float f = elem<Tag>(c[i], j);
       if constexpr (KEEPX) xf[i][j] = f;
-      const double d = static_cast<double>(f);
-      acc[j & 1] = __builtin_fma(d, d, acc[j & 1]);
+      acc[j & 1] = __builtin_fmaf(f, f, acc[j & 1]);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
-  const double ss = acc[0] + acc[1];
+  const float ss = acc[0] + acc[1];
   if constexpr (!KEEPX) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) asm volatile("" : "+v"(c[i]));
@@ -313,9 +318,9 @@ __device__ __forceinline__ float x_at(const u32x4 (&c)[CH], const float (&xf)[KE
     return elem<Tag>(c[i], j);
 }
 
-// r = 1 / sqrt(ms + eps), ms the fp32 rounding of the exact mean square.
-__device__ __forceinline__ float rms_rstd(double ss, int N, float eps) {
-  const float ms = static_cast<float>(ss / static_cast<double>(N));
+// r = 1 / sqrt(ss / N + eps), each step an IEEE fp32 operation.
+__device__ __forceinline__ float rms_rstd(float ss, int N, float eps) {
+  const float ms = ss / static_cast<float>(N);
   return 1.0f / sqrtf(ms + eps);
 }
 
@@ -331,7 +336,7 @@ void rmsnorm_quant_tok_kernel(
     int64_t qs, float* __restrict__ s, int64_t M, int N, float eps) {
   static_assert(Tag::kVec == 8, "fp8 rows are built from 8-element chunks");
   constexpr int RPB = kBlock / LPR;
-  __shared__ double red_ss[kBlock / kWave];
+  __shared__ float red_ss[kBlock / kWave];
   __shared__ float red_max[kBlock / kWave];
   __shared__ float red_max2[kBlock / kWave];
   const int lane = threadIdx.x % LPR;
@@ -341,7 +346,7 @@ void rmsnorm_quant_tok_kernel(
   load_row_weight<Tag, LPR, CH, EXACT, false>(x, xs, w, row_ok ? row : M - 1, lane, N, c, wc);
   float xf[KEEPX ? CH : 1][8];
   const float r =
-      rms_rstd(row_reduce_sum64<LPR>(lane_sum_squares<Tag, CH, KEEPX>(c, xf), red_ss), N, eps);
+      rms_rstd(row_reduce<LPR, OpSum>(lane_sum_squares<Tag, CH, KEEPX>(c, xf), red_ss), N, eps);
 
   float v[CH][8];
   float amax = 0.f;
@@ -387,7 +392,7 @@ void rmsnorm_quant_blk_kernel(
     int64_t qs, float* __restrict__ s, int64_t M, int N, float eps) {
   static_assert(Tag::kVec == 8 && LPR >= 16, "block layout");
   constexpr int RPB = kBlock / LPR;
-  __shared__ double red_ss[kBlock / kWave];
+  __shared__ float red_ss[kBlock / kWave];
   const int lane = threadIdx.x % LPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
   const bool row_ok = row < M;
@@ -395,7 +400,7 @@ void rmsnorm_quant_blk_kernel(
   load_row_weight<Tag, LPR, CH, EXACT, SHARED>(x, xs, w, row_ok ? row : M - 1, lane, N, c, wc);
   float xf[KEEPX ? CH : 1][8];
   const float r =
-      rms_rstd(row_reduce_sum64<LPR>(lane_sum_squares<Tag, CH, KEEPX>(c, xf), red_ss), N, eps);
+      rms_rstd(row_reduce<LPR, OpSum>(lane_sum_squares<Tag, CH, KEEPX>(c, xf), red_ss), N, eps);
 
   float v[CH][8];
   float gmax[CH];

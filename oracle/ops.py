@@ -91,7 +91,8 @@ def f32_op(fn, *args: torch.Tensor) -> torch.Tensor:
 
 
 def rms_rstd_exact(x: torch.Tensor, eps: float) -> torch.Tensor:
-    """r = 1 / sqrt(ms + eps) with ms the exact mean square rounded once to fp32.
+    """r = 1 / sqrt(ms + eps) with ms the exact mean square rounded once to fp32
+    (the torch RMSNorm module's kernel, rms_norm_module below).
 
     The reference sums x^2 in fp32 in its kernel's own order (rmsnorm.cu:47-53);
     any fp32 sum lands within a few ulps of the exact value, in an
@@ -296,13 +297,100 @@ def ring_slots(num_frames: int, cache_slots: int, slot_start: int) -> list[int]:
 
 # ---------------------------------------------------------------------------
 # RMSNorm -> FP8 (per token / per 1x128 block): rmsnorm.cu:41-60 in fp32
-# (no rounding to the input type; exact mean square, see rms_rstd_exact)
-# followed by per_token_quant_fp8.cu:56-82 over each row or 1x128 block.
+# (no rounding to the input type) followed by per_token_quant_fp8.cu:56-82
+# over each row or 1x128 block. The reference sums the squares in fp32 in its
+# own block-reduction order (rmsnorm.cu:47-53); the build's kernels sum them
+# in fp32 in a fixed order of their own, which rms_sum_squares_fixed restates
+# step by step, so the CPU result is bit-exact with the kernels'.
 # ---------------------------------------------------------------------------
+# (chunks of 8 values, lanes per row, chunks per lane) of the kernels' row
+# shapes: the smallest shape whose lanes x chunks cover the row.
+_C4_ROW_SHAPES = [(8, 8, 1), (16, 16, 1), (32, 32, 1), (64, 64, 1), (128, 64, 2), (192, 64, 3),
+                  (256, 64, 4), (384, 64, 6), (512, 64, 8), (768, 64, 12), (1024, 64, 16),
+                  (2048, 256, 8), (3072, 256, 12), (4096, 256, 16)]
+
+
+def c4_row_shape(N: int, group_size: int = 0) -> tuple[int, int]:
+    """(lanes per row, 16-byte chunks per lane) of the RMSNorm -> FP8 kernels
+    for rows of N 16-bit values; the per-block kernel uses at least 16 lanes
+    (a 1x128 block is one chunk on each of 16 lanes)."""
+    chunks = -(-N // 8)
+    for limit, lpr, ch in _C4_ROW_SHAPES:
+        if chunks <= limit:
+            return (max(lpr, 16) if group_size else lpr), ch
+    raise ValueError(f"no row shape covers {N} values")
+
+
+def _lane_tree(a, W: int):
+    """Sum over aligned groups of W lanes of a [M, W*k] float32 array, in the
+    kernels' butterfly order: partner lane l^7 (W = 8) or l^8 then l^4 (W >= 16),
+    then l^2, l^1, l^16 (W >= 32), and for W = 64 lane 0's value plus lane 32's.
+    Each step is one IEEE fp32 addition (a + b == b + a). Returns [M, k]."""
+    import numpy as np
+    M, L = a.shape
+    g = a.reshape(M, L // W, W)
+    idx = np.arange(W)
+    steps = ([7] if W == 8 else [8, 4]) + [2, 1] + ([16] if W >= 32 else [])
+    for d in steps:
+        g = (g + g[:, :, idx ^ d]).astype(np.float32)
+    if W == 64:
+        return (g[:, :, 0] + g[:, :, 32]).astype(np.float32)
+    return g[:, :, 0]
+
+
+def rms_sum_squares_fixed(x: torch.Tensor, lpr: int, ch: int) -> torch.Tensor:
+    """Sum of x^2 over each row in fp32, in the RMSNorm -> FP8 kernels' order.
+
+    Element e of a row sits on lane (e // 8) % lpr as value j = e % 8 of that
+    lane's chunk i = e // (8 * lpr); values past the row are 0. Each lane keeps
+    two fp32 accumulators, chunks in order and j = 0..7 within a chunk, value j
+    going to accumulator j % 2 as acc + x^2 rounded once (a fused multiply-add;
+    x^2 of a 16-bit value is exact in fp32, and float64 carries the sum of two
+    fp32 values exactly enough for one correct rounding); the lane's sum is
+    acc0 + acc1; lanes are summed per wave (64 lanes, fewer when lpr < 64) by
+    _lane_tree, and the waves of a wider row in order."""
+    import numpy as np
+    xf = x.float().numpy().astype(np.float64)
+    M, N = xf.shape
+    pad = np.zeros((M, lpr * ch * 8), dtype=np.float64)
+    pad[:, :N] = xf
+    sq = (pad * pad).reshape(M, ch, lpr, 8)
+    acc = [np.zeros((M, lpr), dtype=np.float32), np.zeros((M, lpr), dtype=np.float32)]
+    for i in range(ch):
+        for j in range(8):
+            acc[j & 1] = (acc[j & 1].astype(np.float64) + sq[:, i, :, j]).astype(np.float32)
+    lane = (acc[0] + acc[1]).astype(np.float32)
+    W = min(lpr, 64)
+    waves = _lane_tree(lane, W)           # [M, lpr // W] (one group per row when lpr <= 64)
+    total = waves[:, 0]
+    for k in range(1, waves.shape[1]):
+        total = (total + waves[:, k]).astype(np.float32)
+    return torch.from_numpy(np.ascontiguousarray(total))
+
+
+def rms_rstd_fixed(x: torch.Tensor, eps: float, lpr: int, ch: int) -> torch.Tensor:
+    """r = 1 / sqrt(ss / N + eps) [M, 1], ss = rms_sum_squares_fixed, each step an
+    IEEE fp32 operation (eps taken as fp32)."""
+    ss = rms_sum_squares_fixed(x, lpr, ch)[:, None]
+    n = torch.tensor(float(x.shape[-1]), dtype=torch.float32)
+    ms = f32_op(torch.div, ss, n)
+    t = f32_op(torch.add, ms, torch.tensor(eps, dtype=torch.float32))
+    sq = f32_op(torch.sqrt, t)
+    return f32_op(torch.div, torch.ones_like(sq), sq)
+
+
+def rmsnorm_quant_f32(x, w, eps: float, group_size: int = 0) -> torch.Tensor:
+    """v = (x * r) * w in fp32 as the RMSNorm -> FP8 kernels compute it (r from
+    rms_rstd_fixed with the kernels' row shape for N)."""
+    lpr, ch = c4_row_shape(x.shape[-1], group_size)
+    xr = f32_op(torch.mul, x.float(), rms_rstd_fixed(x, eps, lpr, ch))
+    return f32_op(torch.mul, xr, w.float())
+
+
 def rmsnorm_quant_fp8(x, w, eps: float, group_size: int = 0, v: torch.Tensor | None = None):
     """Returns (q uint8 [M, N], s fp32 [M] or [M, N/128], v fp32 [M, N])."""
     if v is None:
-        v = rmsnorm_exact_f32(x, w, eps)
+        v = rmsnorm_quant_f32(x, w, eps, group_size)
     M, N = v.shape
     if group_size == 0:
         scale, inv = scale_and_inv(nan_ignoring_amax(v))

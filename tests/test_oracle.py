@@ -115,6 +115,65 @@ def test_exact_mean_square_rstd():
     assert not torch.allclose(rw, r, rtol=1e-5, atol=0)
 
 
+def _row_with(N, vals):
+    x = torch.zeros(1, N)
+    for e, v in vals:
+        x[0, e] = v
+    return x.to(torch.bfloat16)
+
+
+def test_fixed_order_sum_known_answers():
+    """rms_sum_squares_fixed against hand-derived sums where the order decides
+    the fp32 result (fp32 spacing is 2 at 2^24, ties go to even):
+      one lane, x = 2^12 then seven 1s: accumulator 0 takes 2^24 and three 1s
+        (each lost: 2^24 + 1 ties to 2^24), accumulator 1 four 1s -> 2^24 + 4;
+      16 lanes (l^8, l^4, l^2, l^1), lane 0 = 2^24, 15 lanes of 1:
+        2^24+1 -> 2^24; +2 -> 2^24+2; +4 -> 2^24+6; +8 -> 2^24+14;
+      64 lanes (then l^16, then lane 0 + lane 32): 2^24+14 + 16 = 2^24+30 on
+        lanes 0-31, 32 on lanes 32-63 -> 2^24+62.
+    The exact sums (2^24 + 7, + 15, + 63) and a left-to-right sum (2^24)
+    differ from each."""
+    cases = [(16, [(0, 2.0 ** 12)] + [(j, 1.0) for j in range(1, 8)], 4.0),
+             (128, [(0, 2.0 ** 12)] + [(8 * l, 1.0) for l in range(1, 16)], 14.0),
+             (512, [(0, 2.0 ** 12)] + [(8 * l, 1.0) for l in range(1, 64)], 62.0)]
+    for N, vals, extra in cases:
+        x = _row_with(N, vals)
+        got = ops.rms_sum_squares_fixed(x, *ops.c4_row_shape(N)).double().item()
+        assert got == 2.0 ** 24 + extra, (N, got - 2.0 ** 24)
+        # planted slips: one accumulator per lane, or a left-to-right row sum
+        seq = torch.tensor(0.0)
+        for v in x.float()[0]:
+            seq = (seq + v * v).float()
+        assert seq.item() != got
+
+
+def test_fixed_order_sum_shapes_and_closeness():
+    """The row shapes follow the kernels' dispatch (smallest lanes x chunks
+    covering the row; per block at least 16 lanes), and for every shape the
+    fixed-order mean square lies within (log2 N + 2) fp32 ulps of the exact
+    one; a planted slip (mean over N - 1) lies far outside."""
+    assert ops.c4_row_shape(3072) == (64, 6) and ops.c4_row_shape(3072, 128) == (64, 6)
+    assert ops.c4_row_shape(64) == (8, 1) and ops.c4_row_shape(64, 128) == (16, 1)
+    assert ops.c4_row_shape(4096) == (64, 8) and ops.c4_row_shape(16384) == (256, 8)
+    assert ops.c4_row_shape(24576) == (256, 12) and ops.c4_row_shape(32768) == (256, 16)
+    with pytest.raises(ValueError):
+        ops.c4_row_shape(32776)
+    from joyomni_ops.workloads import with_outliers
+    g = torch.Generator().manual_seed(41)
+    for N in (8, 100, 128, 512, 1000, 3072, 6144, 16384, 20000):
+        x = with_outliers(torch.randn(24, N, generator=g), g).to(torch.bfloat16)
+        lpr, ch = ops.c4_row_shape(N)
+        ss = ops.rms_sum_squares_fixed(x, lpr, ch).double()
+        exact = x.double().pow(2).sum(-1)
+        ulp = torch.exp2(torch.floor(torch.log2(exact)) - 23)
+        bound = (torch.log2(torch.tensor(float(N))).ceil() + 2) * ulp
+        assert bool(((ss - exact).abs() <= bound).all()), N
+        assert bool(((exact * N / (N - 1) - ss).abs() > bound).all()), N
+    r = ops.rms_rstd_fixed(x, 1e-6, lpr, ch)
+    r64 = 1.0 / torch.sqrt(x.double().pow(2).mean(-1, keepdim=True) + 1e-6)
+    assert bool(((r.double() - r64).abs() <= 24 * torch.exp2(torch.floor(torch.log2(r64)) - 23)).all())
+
+
 def test_group_quant_oracle_matches_c():
     g = torch.Generator().manual_seed(3)
     x = torch.randn(40, 1024, generator=g).to(torch.bfloat16)
