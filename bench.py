@@ -632,7 +632,10 @@ def cpu_fn(cfg):
     if cfg.op == "quant":
         return lambda t: ops.per_token_quant_fp8(t["x"])
     if cfg.op == "rms_quant":
-        return lambda t: ops.rmsnorm_quant_fp8(t["x"], t["weight"], d["eps"], d["group"])
+        # the reference's torch RMSNorm formula (test_parity_light.py:31-32),
+        # then the per-token / per-block quantization rule
+        return lambda t: ops.rmsnorm_quant_fp8(t["x"], t["weight"], d["eps"], d["group"],
+                                               v=ops.rmsnorm_f32(t["x"], t["weight"], d["eps"]))
     if cfg.op == "add_ln":
         return lambda t: ops.add_layernorm_scale_shift(t["x"], t["residual"], None, None, None,
                                                        t["scale"], t["shift"], d["eps"])
