@@ -261,3 +261,27 @@ def test_torch_op_and_dit_shims(dev):
     assert torch.equal(s3, s3r)
     with pytest.raises(RuntimeError, match="output_s"):
         jo.norm_scale_shift_quant_fp8(xr, sc, sh, q3, torch.empty(M + 1, device=dev))
+
+
+@pytest.mark.parametrize("M,N", [(17, 3072), (33, 512)])
+@pytest.mark.parametrize("norm", ["layer", "rms"])
+def test_norm_quant_per_row_gate_broadcast_modulation(abi, dev, stream_handle, M, N, norm):
+    """A gate with a row per row of x beside broadcast scale / shift (the
+    bounds-free kernel for rows that fill the lanes exactly; M leaves a partly
+    filled last workgroup): residual bit-exact, bytes and scales those of the
+    unfused pair, and nothing written past row M."""
+    dtype = torch.bfloat16
+    t = make_case(M, N, dtype, "add_gate", False, False, M * 7 + N)
+    g = torch.Generator().manual_seed(M + N)
+    t["gate"] = torch.randn(M, N, generator=g).to(dtype)
+    d = to_dev(t, dev)
+    q = torch.full((M + 2, N), 0x55, dtype=torch.uint8, device=dev)
+    s = torch.full((M + 2,), -1.0, dtype=torch.float32, device=dev)
+    abi.call("jo_norm_scale_shift_quant_fp8", d["x"].data_ptr(), N, d["residual"].data_ptr(), N,
+             d["gate"].data_ptr(), N, None, None, d["scale"].data_ptr(), 0, d["shift"].data_ptr(),
+             0, 1, q.data_ptr(), N, s.data_ptr(), M, N, abi.dtype_code(dtype), NORM[norm], 1e-6,
+             stream_handle)
+    y = run_unfused_y(abi, stream_handle, d["residual"], d, M, N, dtype, norm, 1e-6)
+    torch.cuda.synchronize()
+    check_case(t, d, q[:M], s[:M], y.cpu(), norm, 1e-6, f"per-row gate [{M},{N}] {norm}")
+    assert bool((q[M:] == 0x55).all()) and bool((s[M:] == -1.0).all()), "rows past M written"

@@ -188,6 +188,37 @@ def test_add_layernorm_per_sample_modulation(abi, dev, stream_handle, B, L, N):
                  f"add_ln per sample B={B} L={L} N={N}")
 
 
+@pytest.mark.parametrize("M,N", [(17, 3072), (33, 512), (7, 64), (3, 16384)])
+@pytest.mark.parametrize("gate_rows", ["per_row", "per_sample"])
+def test_add_layernorm_mixed_modulation(abi, dev, stream_handle, M, N, gate_rows):
+    """Broadcast scale / shift (the rows that fill the lanes exactly take the
+    bounds-free kernel) with a gate of its own rows: one per row of x, or one
+    per sample of M rows (mod_rows = M, a single sample); M leaves a partly
+    filled last workgroup (its rows past M read row M - 1 and store nothing:
+    the rows after the output must stay untouched)."""
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(M + N + (gate_rows == "per_row"))
+    x = torch.randn(M, N, generator=g).to(dtype)
+    res = torch.randn(M, N, generator=g).to(dtype)
+    gate = torch.randn((M if gate_rows == "per_row" else 1), N, generator=g).to(dtype)
+    sc = (0.2 * torch.randn(N, generator=g)).to(dtype)
+    sh = (0.2 * torch.randn(N, generator=g)).to(dtype)
+    xd, gd, scd, shd = (t.to(dev) for t in (x, gate, sc, sh))
+    # residual and y inside larger buffers: the rows after M are sentinels
+    rbuf = torch.full((M + 3, N), 5.0, dtype=dtype, device=dev)
+    rbuf[:M] = res.to(dev)
+    ybuf = torch.full((M + 3, N), 7.0, dtype=dtype, device=dev)
+    mod_rows = 1 if gate_rows == "per_row" else M
+    abi.call("jo_fused_add_layernorm_scale_shift", xd.data_ptr(), N, rbuf.data_ptr(), N,
+             gd.data_ptr(), N, None, None, scd.data_ptr(), 0, shd.data_ptr(), 0, mod_rows,
+             ybuf.data_ptr(), N, M, N, abi.dtype_code(dtype), 1e-6, stream_handle)
+    torch.cuda.synchronize()
+    full_gate = gate if gate_rows == "per_row" else gate.expand(M, N)
+    check_add_ln(rbuf[:M].cpu(), ybuf[:M].cpu(), x, res, full_gate, None, None, sc, sh, 1e-6,
+                 dtype, f"add_ln mixed [{M},{N}] gate {gate_rows}")
+    assert bool((rbuf[M:] == 5.0).all()) and bool((ybuf[M:] == 7.0).all()), "rows past M written"
+
+
 def test_add_layernorm_full_c2_and_torch_op(dev):
     import joyomni_ops as jo
     cfg = W.CONFIGS["C2"]
