@@ -147,8 +147,9 @@ def rms_quant_gpu(abi, stream, x_dev, w_dev, eps, group):
 
 
 def check_rms_quant(q, s, x, w, eps, group, what):
-    """Scales and e4m3fn bytes bit-exact against the oracle (exact mean square,
-    IEEE sqrt/div, (x*r)*w, then the per_token_quant_fp8 rule per row/block)."""
+    """Scales and e4m3fn bytes bit-exact against the oracle (the kernels' fixed
+    fp32 summation order of the squares, IEEE sqrt/div, (x*r)*w, then the
+    per_token_quant_fp8 rule per row/block)."""
     qo, so, _ = ops.rmsnorm_quant_fp8(x, w, eps, group)
     ds = (s - so).abs()
     assert torch.equal(s, so), \
@@ -173,6 +174,24 @@ def test_rmsnorm_quant_random(abi, dev, stream_handle, group, M, N):
     w = (1 + 0.1 * torch.randn(N, generator=g)).to(torch.bfloat16)
     q, s = rms_quant_gpu(abi, stream_handle, x.to(dev), w.to(dev), 1e-6, group)
     check_rms_quant(q, s, x, w, 1e-6, group, f"[{M},{N}] g{group}")
+
+
+ROW_SHAPE_CASES = [(N, 0) for N in (8, 40, 64, 512, 1536, 2048, 6144, 8192, 32768)] + \
+    [(N, 128) for N in (512, 1536, 2048, 6144, 8192, 32768)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("N,group", ROW_SHAPE_CASES)
+def test_rmsnorm_quant_every_row_shape(abi, dev, stream_handle, dtype, N, group):
+    """Every row shape of the fixed-order sum (8-, 16-, 32- and 64-lane rows
+    with 1 to 16 chunks per lane, 256-lane rows of four waves), bf16 and fp16,
+    a ragged row count: bit-exact against the oracle's restatement."""
+    M = 11
+    g = torch.Generator().manual_seed(N * 3 + group + (dtype == torch.float16))
+    x = W.with_outliers(torch.randn(M, N, generator=g), g).to(dtype)
+    w = (1 + 0.1 * torch.randn(N, generator=g)).to(dtype)
+    q, s = rms_quant_gpu(abi, stream_handle, x.to(dev), w.to(dev), 1e-6, group)
+    check_rms_quant(q, s, x, w, 1e-6, group, f"[{M},{N}] {dtype} g{group}")
 
 
 @pytest.mark.parametrize("group", [0, 128])
