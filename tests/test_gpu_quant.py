@@ -167,9 +167,17 @@ def check_rms_quant(q, s, x, w, eps, group, what):
                                  # width that is not a whole number of blocks
                                  (9, 2688), (9, 2176), (8200, 2688), (9, 2696)])
 def test_rmsnorm_quant_random(abi, dev, stream_handle, group, M, N):
-    if group and N % group:
-        pytest.skip("per-block scales need whole blocks")
     g = torch.Generator().manual_seed(M * 7 + N + group)
+    if group and N % group:
+        # per-block scales need whole blocks: refused before any launch
+        x = torch.zeros(M, N, dtype=torch.bfloat16, device=dev)
+        q = torch.empty(M, N, dtype=torch.uint8, device=dev)
+        s = torch.empty(M * (N // group + 1), dtype=torch.float32, device=dev)
+        st = abi.lib().jo_rmsnorm_quant_fp8(x.data_ptr(), N, x.data_ptr(), q.data_ptr(), N,
+                                            s.data_ptr(), M, N, abi.JO_DTYPE_BF16, 1e-6, group,
+                                            stream_handle)
+        assert st == abi.JO_ERR_INVALID and "divisible by 128" in abi.last_error()
+        return
     x = W.with_outliers(torch.randn(M, N, generator=g), g).to(torch.bfloat16)
     w = (1 + 0.1 * torch.randn(N, generator=g)).to(torch.bfloat16)
     q, s = rms_quant_gpu(abi, stream_handle, x.to(dev), w.to(dev), 1e-6, group)
