@@ -45,6 +45,10 @@ HIP_FLAGS = [
     "-fPIC",
     # Packed fp32 VALU forms are kept out of every kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # The first 16 kernel-argument dwords arrive in SGPRs at wave launch (gfx950
+    # kernarg preload), so a row kernel's first loads do not wait on an s_load of
+    # its argument struct: 1-3 % on the RMSNorm->FP8 kernels, level elsewhere.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-command-line-argument",
     f"-I{INCLUDE}",
