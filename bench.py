@@ -259,8 +259,10 @@ STREAMS = {
     "S_C4_4725_blk@no-weight": _S("C4_4725_blk", 4725, 64, 6, 1, 1, 8, 24, False),
     "S_C4_10530_tok": _S("C4_10530_tok", 10530, 64, 6, 1, 1, 8, 1, False, 1),
     "S_C4_10530_tok@no-weight": _S("C4_10530_tok", 10530, 64, 6, 1, 1, 8, 1, False),
+    "S_C4_10530_tok@128x3": _S("C4_10530_tok", 10530, 128, 3, 1, 1, 8, 1, False, 1),
     "S_C4_10530_blk": _S("C4_10530_blk", 10530, 64, 6, 1, 1, 8, 24, False, 1),
     "S_C4_10530_blk@no-weight": _S("C4_10530_blk", 10530, 64, 6, 1, 1, 8, 24, False),
+    "S_C4_10530_blk@128x3": _S("C4_10530_blk", 10530, 128, 3, 1, 1, 8, 24, False, 1),
     "S_R_q4k": _S("R_q4k", 3120, 128, 4, 1, 1, 8, 1, False),
     "S_R_q4k@64x8": _S("R_q4k", 3120, 64, 8, 1, 1, 8, 1, False),
     "S_R_q16k": _S("R_q16k", 3120, 256, 8, 1, 1, 8, 1, False),

@@ -211,6 +211,7 @@ extern "C" int jo_stream_rows(const void* const* in, void* const* out, float* sc
       TRY(64, 8, 1, 1, 16) ||
       // the same with the row-invariant weight row the kernels read per row
       TRY(64, 6, 1, 1, 8, 1) ||    // RMSNorm -> FP8, hidden 3072
+      TRY(128, 3, 1, 1, 8, 1) ||   // the same rows, two waves per row
       TRY(16, 1, 1, 1, 16, 1) ||   // rmsnorm rows of 128 (also per-head rows of a strided view)
       TRY(64, 8, 1, 1, 16, 1);     // rmsnorm rows of 4096
 #undef TRY
