@@ -450,9 +450,11 @@ int launch_norm_mod_quant_dt(int dtype, const NormArgs& a, hipStream_t stream, c
 //     the sum of squares in fp32 like the reference kernel.
 //   MODE kModuleRms: out = round(round(x * r) * w), the torch RMSNorm module
 //     (dit.py:244-249: the normalized row is cast back to the input type
-//     before the weight multiply). Its mean square is taken exactly (fp64
-//     sum of the exact squares, rounded once), as rmsnorm_quant_kernel does,
-//     so the intermediate rounding does not depend on a summation order.
+//     before the weight multiply). Its mean square is an fp64 sum of the
+//     (exact) squares rounded once to fp32; two summation orders give fp64
+//     sums within ~2^-52 of each other, so the fp32 value, and with it the
+//     intermediate rounding, depends on the order only for sums that fall on
+//     an fp32 rounding boundary to that precision.
 //   r = 1 / sqrt(mean(x^2) + eps) with IEEE sqrt and division.
 // HEADS: row m is head m % heads of token m / heads, read at
 // x + token * xs + head * xhs (a per-head norm straight from a packed qkv

@@ -91,8 +91,9 @@ def f32_op(fn, *args: torch.Tensor) -> torch.Tensor:
 
 
 def rms_rstd_exact(x: torch.Tensor, eps: float) -> torch.Tensor:
-    """r = 1 / sqrt(ms + eps) with ms the exact mean square rounded once to fp32
-    (the torch RMSNorm module's kernel, rms_norm_module below).
+    """r = 1 / sqrt(ms + eps) with ms the mean square summed in float64 and
+    rounded once to fp32 (the torch RMSNorm module's kernel, rms_norm_module
+    below).
 
     The reference sums x^2 in fp32 in its kernel's own order (rmsnorm.cu:47-53);
     any fp32 sum lands within a few ulps of the exact value, in an
