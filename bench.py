@@ -3,8 +3,8 @@
 `python bench.py [--gpus 1] [--steps K] [--warmup W] [--only C1,C0,...]`
 
 A "step" is one call of an op over one batch of synthetic input. The headline
-workload (`value`) is BASELINE config 1: per-token FP8 e4m3 quantization of a
-bf16 [10530, 3072] activation. Every other BASELINE config is timed the same
+workload (`value`) is benchmark config C1: per-token FP8 e4m3 quantization of a
+bf16 [10530, 3072] activation. Every other benchmark config is timed the same
 way and reported under "ops", as are the next-row workloads N3 (the gated
 residual + LayerNorm + AdaLN with the per-token FP8 epilogue, C2 shape) and
 N4 (the graph runner's 40-layer KV-pool commit at the deployment shape), and
@@ -56,7 +56,7 @@ time). Alternative shapes of the same bytes (S_*@LPRxCH) show whether another
 launch shape would stream faster.
 
 cpu_baseline: the CPU oracle's restatement of the reference formula of every
-BASELINE config (C0-C4), timed on the host's cores with the same inputs:
+benchmark config (C0-C4), timed on the host's cores with the same inputs:
 3 warmups, then at least 10 timed calls (more while under ~2 s), median
 (`cpu_us_per_call` in each config's line; the headline one in cpu_baseline).
 
@@ -670,7 +670,7 @@ def cpu_threads() -> int:
     return max(1, n)
 
 
-BASELINE_CONFIGS = ("C0", "C1", "C2", "C3", "C4_4725_tok", "C4_4725_blk", "C4_10530_tok",
+BENCH_CONFIGS = ("C0", "C1", "C2", "C3", "C4_4725_tok", "C4_4725_blk", "C4_10530_tok",
                     "C4_10530_blk")
 
 
@@ -830,7 +830,7 @@ def main() -> int:
     if not args.no_cpu:
         threads = cpu_threads()
         torch.set_num_threads(threads)
-        for n in BASELINE_CONFIGS:
+        for n in BENCH_CONFIGS:
             if n not in results:
                 continue
             log(f"cpu baseline {n}: oracle restatement on the full input, {threads} threads")
@@ -903,13 +903,13 @@ def summary_line(results: dict, cpu, steps: int, warmup: int, host_cpu: str = ""
                  detail: str | None = None) -> dict:
     """The one JSON line bench.py prints: the headline (C1) with its roofline
     and CPU baseline, and a compact entry for every other line that ran (the
-    BASELINE configs under "configs", the rest under "ops"). It is kept under
+    C0-C4 configs under "configs", the rest under "ops"). It is kept under
     SUMMARY_MAX_BYTES so that a reader that keeps only the tail of stdout
     still gets it whole; the full record goes to the detail file."""
     from joyomni_ops import workloads as W
     h = results[HEADLINE]
     cfg = W.CONFIGS[HEADLINE]
-    configs = {n: compact_entry(n, results[n]) for n in BASELINE_CONFIGS if n in results}
+    configs = {n: compact_entry(n, results[n]) for n in BENCH_CONFIGS if n in results}
     ops = {n: compact_entry(n, r) for n, r in results.items()
            if n not in configs and not n.startswith("S_")}
     line = {

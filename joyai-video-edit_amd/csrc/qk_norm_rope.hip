@@ -331,7 +331,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(const QKArgs a) {
 }
 
 // Waves per token. Two (q and k on separate waves) measured faster on MI355X
-// than one at every BASELINE shape (3510 tokens: 19.0 -> 17.5 us; 10530
+// than one at every benchmark shape (3510 tokens: 19.0 -> 17.5 us; 10530
 // tokens: 46.4 -> 45.2 us): the extra waves hide HBM latency better than the
 // saved rotation-coefficient work. Four (each of q and k split into halves of
 // its head groups) is faster again, at 3510 tokens (17.3 -> 17.0 us) and, once

@@ -1,4 +1,4 @@
-"""The BASELINE workloads of the joyomni_ops hot path: shapes, seeded synthetic
+"""The benchmark workloads (C0-C4) of the joyomni_ops hot path: shapes, seeded synthetic
 inputs, launch helpers through the C ABI, and algorithmic HBM bytes.
 
 Configs (720p 3-latent-frame chunk shapes, hidden 3072, 24 heads x 128):
@@ -8,7 +8,7 @@ Configs (720p 3-latent-frame chunk shapes, hidden 3072, 24 heads x 128):
   C3   QK RMSNorm + RoPE with K into a 7-slot ring cache: q,k [1, 10530, 24, 128]
   C4*  RMSNorm -> FP8, T in {4725, 10530}, per-token or per-1x128-block scales
 
-Next-row workloads (not BASELINE configs; same shapes):
+Next-row workloads (beyond C0-C4; same shapes):
   N3   gated residual add + LayerNorm + AdaLN with the per-token FP8 epilogue
        (the y of C2 quantized for the next Fp8Linear instead of written):
        x, residual bf16 [10530, 3072], gate/scale/shift bf16 [3072]

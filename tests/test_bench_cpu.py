@@ -51,7 +51,7 @@ def test_streams_name_configs_and_one_own_shape(bench):
             own[s.cfg] = name
     for cfg in ("C0", "C1", "C2", "C3", "C4_4725_tok", "C4_4725_blk", "C4_10530_tok",
                 "C4_10530_blk"):
-        assert cfg in own, f"BASELINE config {cfg} has no stream ceiling"
+        assert cfg in own, f"benchmark config {cfg} has no stream ceiling"
 
 
 def test_own_shape_streams_move_the_config_bytes(bench):
@@ -155,7 +155,7 @@ def test_summary_line_fits_the_driver_tail(bench):
     """The stdout line stays whole for a reader that keeps only the last 16 KB
     of stdout: a full-size results dict (every config, stream ceiling and
     comparison field) gives a line under 4 KB that still carries the headline,
-    its roofline (with traffic), the CPU baseline and every BASELINE config."""
+    its roofline (with traffic), the CPU baseline and every C0-C4 config."""
     import json
     results = _synthetic_results(bench)
     cpu = {"gbps": 1.83, "us_per_call": 53100.2, "threads": 16, "iters": 38, "seconds": 2.1}
@@ -175,7 +175,7 @@ def test_summary_line_fits_the_driver_tail(bench):
     assert "traffic" in rf
     cb = back["cpu_baseline"]
     assert cb["kind"] == "port" and cb["cores"] == 16 and cb["unit"] == "GB/s"
-    for n in bench.BASELINE_CONFIGS:
+    for n in bench.BENCH_CONFIGS:
         e = back["configs"][n]
         assert {"us", "frac", "S_us", "fS", "cpu_us"} <= set(e), (n, e)
     for n in ("N3", "N4", "G1", "G3", "G4", "R_qks", "T_ln", "B_img"):

@@ -1,6 +1,6 @@
 """GPU parity of the QK RMSNorm + RoPE ops through the C ABI and torch ops.
 
-Bar (BASELINE): bf16 outputs within 1 bf16 ulp of the fp32-accumulated
+Bar (the benchmark contract): bf16 outputs within 1 bf16 ulp of the fp32-accumulated
 oracle (fused_qknorm_rope_3d_kernel.cu:98-142 / test_parity_light.py:77-87
 restated in oracle/ops.py), the ulp floored at 2^-10 of the head's largest
 |value| to absorb fp32 cancellation in rotated pairs.
