@@ -8,7 +8,8 @@ bf16 [10530, 3072] activation. Every other benchmark config is timed the same
 way and reported under "ops", as are the next-row workloads N3 (the gated
 residual + LayerNorm + AdaLN with the per-token FP8 epilogue, C2 shape) and
 N4 (the graph runner's 40-layer KV-pool commit at the deployment shape), and
-the FP8 GEMMs G1-G4 (fp8_scaled_mm at Fp8Linear's deployment shapes), whose
+the FP8 GEMMs G1-G6 (fp8_scaled_mm at Fp8Linear's deployment shapes: the
+image stream's G1-G4, the text stream's G5-G6 at 256 prompt tokens), whose
 lines add TFLOP/s against the 5.0 PFLOP/s dense fp8 matrix-core peak and the
 time of torch._scaled_mm (hipBLASLt) on the same operands (both launched
 eagerly in alternating blocks over the same rotating operand sets:

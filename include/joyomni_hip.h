@@ -66,8 +66,10 @@ int jo_abi_version(void);
  *   JO_KNOB_KV_SPLIT    1 = K and V of a KV-pool row on one wave, 2 = on two
  *                       (env JO_KV_SPLIT)
  *   JO_KNOB_GEMM_SHAPE  FP8 GEMM tile: 0 = 256x256, 1 = 256x128, 2 = the
- *                       register-staged kernel, 3 = 224x256, 4 = 224x128
- *                       (env JO_GEMM_SHAPE)
+ *                       register-staged kernel, 3 = 224x256, 4 = 224x128,
+ *                       5 = 128x128 and 6 = 64x64 (four waves), 7 = 128x256
+ *                       (eight waves; 5-7 need K % 128 == 0, else the
+ *                       register-staged kernel runs) (env JO_GEMM_SHAPE)
  * No reference counterpart (tuning and test hook). */
 #define JO_KNOB_QK_SPLIT 0
 #define JO_KNOB_KV_SPLIT 1

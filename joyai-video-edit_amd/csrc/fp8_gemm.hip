@@ -786,6 +786,190 @@ void launch_pair(const GemmArgs& g, hipStream_t stream) {
                      dim3((g.N + BN - 1) / BN, (g.M + BM - 1) / BM), dim3(NW * 64), 0, stream, g);
 }
 
+// ---------------------------------------------------------------------------
+// Small-tile kernel, for grids the 8-wave 224/256-row tiles would leave
+// mostly idle (a few hundred rows: the text stream's Fp8Linear calls; 224x256
+// tiles give [256, 4096] 32 tiles for 256 CUs). NW waves on a BM x BN tile
+// (64x64 or 128x128 with four, 128x256 with eight) in a 2 x NW/2 grid of wave
+// tiles; K advances in 128-byte stages (whole lines, the LDS layout of the
+// 128-byte-stage kernel) through a ring of NST slots that direct loads fill
+// NST-1 stages ahead; one barrier a stage.
+// Its K loop streams (BM + BN) x 128 bytes a stage for BM x BN x 128 MACs, so
+// it only pays where it brings CUs into play that the large tiles leave idle.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int NW>
+struct SmallLoads {
+  static constexpr int kSlots = (BM + BN) / 8;  // 1 KB wave loads (8 rows) a stage
+  static constexpr int kPerWave = kSlots / NW;
+  static_assert(kSlots % NW == 0, "load slots spread evenly over the waves");
+  const uint8_t* base[kPerWave];  // wave-uniform: the tile's first row of A or B^T
+  uint32_t off[kPerWave];         // this lane's 16-byte chunk of each slot at K offset 0
+};
+
+template <class OutTag, int BM, int BN, int NW, int NST>
+__device__ __forceinline__ void fp8_gemm_small_body(const GemmArgs& g) {
+  constexpr int WROWS = BM / 2, WCOLS = BN / (NW / 2);  // wave tile
+  constexpr int MI = WROWS / 32, J = WCOLS / 32;
+  constexpr int kStage = (BM + BN) * kQBK;
+  constexpr int kRowBytes = BN * 2 + 16;  // padded LDS row of the staged output tile
+  constexpr int kChunksPerRow = BN * 2 / 16;
+  using Loads = SmallLoads<BM, BN, NW>;
+  constexpr int PER = Loads::kPerWave;
+  static_assert(MI >= 1 && J >= 1 && BM * kRowBytes <= NST * kStage && NST >= 2 && NST <= 5,
+                "tile shape");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * kStage];
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int wm = wave & 1, wn = wave >> 1;
+  int m0, n0;
+  xcd_grouped_tile(BM, BN, m0, n0);
+
+  // Lane p of load slot L fills row 8L + p/8 of the stage (A rows, then B^T
+  // rows), chunk position p%8, with the global chunk that belongs there; rows
+  // beyond M (N) read row M-1 (N-1) and are never stored.
+  Loads ld;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int slot = wave + i * NW;
+    const bool is_a = slot < BM / 8;
+    const int r = (is_a ? slot : slot - BM / 8) * 8 + lane / 8;
+    const int row = is_a ? min(m0 + r, g.M - 1) - m0 : min(n0 + r, g.N - 1) - n0;
+    ld.base[i] = is_a ? g.a + static_cast<int64_t>(m0) * g.lda : g.b + static_cast<int64_t>(n0) * g.ldb;
+    ld.off[i] = static_cast<uint32_t>(row) * static_cast<uint32_t>(is_a ? g.lda : g.ldb) +
+                (((lane & 7) ^ qswz(r)) * 16);
+  }
+  const int stages = g.K / kQBK;
+  auto issue = [&](int s) {
+    uint8_t* dst = smem + (s % NST) * kStage;
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      __builtin_amdgcn_global_load_lds(ld.base[i] + (ld.off[i] + s * kQBK),
+                                       (__attribute__((address_space(3))) void*)(dst + (wave + i * NW) * 1024),
+                                       16, 0, 0);
+  };
+
+  // Fragment rows wm*WROWS + i*32 + lane%32 (A) and wn*WCOLS + j*32 +
+  // lane%32 (B): multiples of 32 apart, so they share lane%32's swizzle.
+  const int fr = lane & 31, fh = lane >> 5;
+  const int q = qswz(fr);
+  int offa[2][2], offb[2][2];  // [half of the stage][chunk of the pair]
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int pos = ((k * 4 + fh * 2 + h) ^ q) << 4;
+      offa[k][h] = (wm * WROWS + fr) * kQBK + pos;
+      offb[k][h] = BM * kQBK + (wn * WCOLS + fr) * kQBK + pos;
+    }
+  f32x16 acc[MI][J];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  auto compute = [&](int s) {
+    const uint8_t* st = smem + (s % NST) * kStage;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      i32x8 af[MI], bf[J];
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(st + offb[k][0] + j * 32 * kQBK);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(st + offb[k][1] + j * 32 * kQBK);
+        bf[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      }
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(st + offa[k][0] + i * 32 * kQBK);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(st + offa[k][1] + i * 32 * kQBK);
+        af[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      }
+      // B first: the accumulator is the transposed tile (as in store_tile).
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < J; ++j) acc[i][j] = mfma32(bf[j], af[i], acc[i][j]);
+    }
+  };
+
+  // At stage s the wave waits for its LDS reads (of stage s-1) and its own
+  // loads of stage s (the younger stages stay in flight), then meets the other
+  // waves: stage s is complete in LDS and every wave is done with the slot of
+  // stage s-1, which then takes stage s+NST-1.
+  for (int s = 0; s < NST - 1 && s < stages; ++s) issue(s);
+  for (int s = 0; s < stages; ++s) {
+    JO_WAIT_LDS0();
+    wait_loads<PER>(min(stages - 1 - s, NST - 2));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (s + NST - 1 < stages) issue(s + NST - 1);
+    compute(s);
+  }
+
+  // Epilogue: the finished tile goes through LDS (free once every wave is past
+  // the barrier) so that rows leave as whole 16-byte lane stores.
+  float sam[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) sam[i] = g.sa[min(m0 + wm * WROWS + i * 32 + fr, g.M - 1)];
+  float sbq[J][4][4], bq[J][4][4];
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int n = min(n0 + wn * WCOLS + j * 32 + qq * 8 + fh * 4, g.N - 4);  // N % 8 == 0
+      const u32x4 sbv = ld16(g.sb + n);
+      u32x4 b4{0u, 0u, 0u, 0u};
+      if (g.bias) {
+        const u32x2 braw = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(g.bias) + n);
+        b4 = u32x4{braw.x, braw.y, 0u, 0u};
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        sbq[j][qq][t] = elem<F32>(sbv, t);
+        bq[j][qq][t] = g.bias ? elem<OutTag>(b4, t) : 0.f;
+      }
+    }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        float o[8];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          o[t] = __builtin_fmaf(sam[i], acc[i][j][qq * 4 + t] * sbq[j][qq][t], bq[j][qq][t]);
+          o[t + 4] = 0.f;
+        }
+        const u32x4 pk = pack<OutTag>(o);
+        const int rl = wm * WROWS + i * 32 + fr, cl = wn * WCOLS + j * 32 + qq * 8 + fh * 4;
+        *reinterpret_cast<u32x2*>(smem + rl * kRowBytes + cl * 2) = u32x2{pk.x, pk.y};
+      }
+  __syncthreads();
+  for (int c = tid; c < BM * kChunksPerRow; c += NW * kWave) {
+    const int rl = c / kChunksPerRow, ch = c % kChunksPerRow;
+    const int m = m0 + rl, n = n0 + ch * 8;
+    if (m < g.M && n < g.N)
+      st16_nt(static_cast<uint16_t*>(g.out) + static_cast<int64_t>(m) * g.ldo + n,
+              *reinterpret_cast<const u32x4*>(smem + rl * kRowBytes + ch * 16));
+  }
+}
+
+template <class OutTag, int BM, int BN, int NW, int NST>
+__global__ __launch_bounds__(NW * 64) void fp8_gemm_small_kernel(const GemmArgs g) {
+  fp8_gemm_small_body<OutTag, BM, BN, NW, NST>(g);
+}
+
+template <class OutTag, int BM, int BN, int NW, int NST>
+void launch_small(const GemmArgs& g, hipStream_t stream) {
+  hipLaunchKernelGGL((fp8_gemm_small_kernel<OutTag, BM, BN, NW, NST>),
+                     dim3((g.N + BN - 1) / BN, (g.M + BM - 1) / BM), dim3(NW * 64), 0, stream, g);
+}
+
 // CUs of the current device (queried once per device; 256, MI355X's count,
 // if the query fails).
 int cu_count() {
@@ -812,6 +996,35 @@ int pick_tile_rows(int M, int N) {
   return cost(224) < cost(256) ? 224 : 256;
 }
 
+// The default launch shape. The K loops are bound by the operand bytes each
+// CU streams from L2 (~45 KB/us per CU for every kernel here), so the cost of
+// a shape is (tiles per CU, rounded up) x (BM + BN) bytes per K byte: the 8-wave
+// 224x256 or 256x256 tiles (pick_tile_rows) unless the small-tile kernel at
+// 128x256, 128x128 or 64x64 streams fewer bytes on the busiest CU, as where
+// the large tiles leave most CUs idle (ties go to the smaller tile: two 64x64
+// workgroups share a CU). Measured on MI355X, M = 256: [256, 4096] x 4096
+// 34.2 -> 11.4 us (64x64), [256, 12288] x 4096 42.4 -> 24.3 us (128x128);
+// M = 1024, [1024, 4096] x 16384 155.4 -> 86.4 us (128x128).
+int auto_shape(int M, int N) {
+  const int64_t cus = cu_count();
+  auto cost = [&](int64_t bm, int64_t bn) {
+    return ((M + bm - 1) / bm * ((N + bn - 1) / bn) + cus - 1) / cus * (bm + bn);
+  };
+  const int bm = pick_tile_rows(M, N);
+  int shape = bm == 224 ? 3 : 0;
+  int64_t best = cost(bm, 256);
+  if (cost(128, 256) <= best) {
+    best = cost(128, 256);
+    shape = 7;
+  }
+  if (cost(128, 128) <= best) {
+    best = cost(128, 128);
+    shape = 5;
+  }
+  if (cost(64, 64) <= best) shape = 6;
+  return shape;
+}
+
 template <class OutTag>
 int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   const dim3 grid((g.N + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
@@ -822,11 +1035,12 @@ int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   // 8-wave 256-column tiles measured faster than two 4-wave 128-column
   // workgroups per CU at every deployment shape (3120x12288x4096: 199 -> 185
   // us, 3120x16384x4096: 257 -> 233 us). The JO_KNOB_GEMM_SHAPE override
-  // 0|1|2|3|4 forces 256x256, 256x128, the register-staged kernel, 224x256 or
-  // 224x128 (results are the same up to the fp32 accumulation order inside
-  // the matrix cores).
+  // 0|1|2|3|4|5|6|7 forces 256x256, 256x128, the register-staged kernel,
+  // 224x256, 224x128, or the small-tile kernel at 128x128, 64x64 or 128x256
+  // (results are the same up to the fp32 accumulation order inside the
+  // matrix cores).
   const int forced = launch_knob(JO_KNOB_GEMM_SHAPE);
-  const int shape = forced >= 0 ? forced : (pick_tile_rows(g.M, g.N) == 224 ? 3 : 0);
+  const int shape = forced >= 0 ? forced : auto_shape(g.M, g.N);
   const bool pair_ok = pipe_ok && g.K % kQBK == 0;
   if (pipe_ok && shape == 1)
     launch_pipe<OutTag, 256, 128, 4, 3>(g, stream);
@@ -840,6 +1054,12 @@ int launch_gemm(const GemmArgs& g, hipStream_t stream) {
     launch_pipe<OutTag, 224, 256, 8, 4>(g, stream);
   else if (pipe_ok && shape == 4)
     launch_pipe<OutTag, 224, 128, 4, 3>(g, stream);
+  else if (pair_ok && shape == 5)
+    launch_small<OutTag, 128, 128, 4, 4>(g, stream);
+  else if (pair_ok && shape == 6)
+    launch_small<OutTag, 64, 64, 4, 4>(g, stream);
+  else if (pair_ok && shape == 7)
+    launch_small<OutTag, 128, 256, 8, 3>(g, stream);
   else
     hipLaunchKernelGGL((fp8_gemm_kernel<OutTag>), grid, dim3(kBlock), 0, stream, g);
   return launch_status("fp8_scaled_mm");

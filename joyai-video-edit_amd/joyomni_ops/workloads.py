@@ -16,6 +16,9 @@ Next-row workloads (beyond C0-C4; same shapes):
   G2   4096): G1 qkv [3120 x 4096] x [4096 x 12288], G2 MLP up x [4096 x 16384],
   G3   G3 MLP down [3120 x 16384] x [16384 x 4096], G4 attention output
   G4   projection [3120 x 4096] x [4096 x 4096]; bf16 output with bias
+  G5   the text stream's Fp8Linear GEMMs at 256 prompt tokens: G5 qkv
+  G6   [256 x 4096] x [4096 x 12288], G6 MLP down [256 x 16384] x [16384 x 4096]
+       (grids the 224x256 tiles would leave mostly idle: the small-tile kernel)
   N4   KV-pool commit of the graph runner at the deployment shape: RoPE'd K and
        V of 40 layers x 1560 tokens x 32 heads x 128 into a [40, 1, 3120, 32, 128]
        pool at token offset 1560, fp32 [1560, 128] tables
@@ -83,6 +86,8 @@ CONFIGS: dict[str, Config] = {
     "G2": Config("G2", "gemm", 8, dict(M=3120, N=16384, K=4096)),
     "G3": Config("G3", "gemm", 9, dict(M=3120, N=4096, K=16384)),
     "G4": Config("G4", "gemm", 15, dict(M=3120, N=4096, K=4096)),
+    "G5": Config("G5", "gemm", 24, dict(M=256, N=12288, K=4096)),
+    "G6": Config("G6", "gemm", 25, dict(M=256, N=4096, K=16384)),
     # Deployment shapes of the DiT block (hidden 4096, 32 heads, 3120 tokens)
     # through the reference-signature entry points; reported, not gated.
     "R_qk": Config("R_qk", "qk_table", 10, dict(B=1, L=3120, H=32, D=128, eps=1e-6)),

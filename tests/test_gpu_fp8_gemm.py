@@ -18,11 +18,12 @@ from oracle import ops
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["auto", "0", "1", "2", "3", "4"], autouse=True)
+@pytest.fixture(params=["auto", "0", "1", "2", "3", "4", "5", "6", "7"], autouse=True)
 def gemm_shape(request):
     """Every kernel variant: the default choice, 256x256 (8 waves), 256x128
     (4 waves), the register-staged kernel (also the K % 64 != 0 path), 224x256
-    (8 waves, 4 and 3 row blocks) and 224x128 (4 waves)."""
+    (8 waves, 4 and 3 row blocks), 224x128 (4 waves), and the small-tile
+    kernel at 128x128 and 64x64 (4 waves) and 128x256 (8 waves)."""
     from joyomni_ops import _abi
     value = -1 if request.param == "auto" else int(request.param)
     _abi.call("jo_set_launch_override", _abi.JO_KNOB_GEMM_SHAPE, value)
@@ -136,6 +137,33 @@ def test_fp8_scaled_mm_deployment_shapes_sampled_rows(dev, N, K):
     g = torch.Generator().manual_seed(1)
     rows = torch.cat([torch.randperm(3072, generator=g)[:24], torch.arange(3104, 3120)])
     check(out.cpu()[rows], a, w.t(), sa, sb, bias, f"[{M},{N},{K}] sampled", rows=rows)
+
+
+_TEXT_ORACLE = {}
+
+
+@pytest.mark.parametrize("M,N,K", [(77, 12288, 4096), (256, 4096, 16384), (512, 16384, 4096),
+                                   (1000, 4096, 4096)])
+def test_fp8_scaled_mm_text_stream_shapes(dev, M, N, K):
+    """The text stream's Fp8Linear shapes (a few hundred prompt tokens against
+    the hidden 4096 / MLP 16384 weights), where the automatic choice takes the
+    small-tile kernel (64x64, 128x128 or, at 512 x 16384, 128x256);
+    every output against the exact oracle (computed once per shape, reused
+    under every launch shape)."""
+    import joyomni_ops as jo
+    a, w, sa, sb, bias = operands(M, N, K, M * 7 + K)
+    out = jo.fp8_scaled_mm(a.to(dev), w.to(dev).t(), sa.to(dev), sb.to(dev), torch.bfloat16,
+                           bias.to(dev))
+    torch.cuda.synchronize()
+    key = (M, N, K)
+    if key not in _TEXT_ORACLE:
+        _, acc, mag = ops.fp8_scaled_mm(a, w.t(), sa, sb, torch.bfloat16, bias)
+        ref = acc * sa.double().reshape(-1, 1) * sb.double().reshape(1, -1) + bias.double().reshape(1, -1)
+        _TEXT_ORACLE[key] = (ref, ulp(ref, torch.bfloat16) + mag * 2.0 ** -13)
+    ref, tol = _TEXT_ORACLE[key]
+    err = (out.cpu().double() - ref).abs()
+    bad = (err > tol).nonzero()
+    assert bad.numel() == 0, f"[{M},{N},{K}]: {bad.shape[0]} outputs off, first {bad[0].tolist()}"
 
 
 def test_fp8_linear_reference_bench_shape(dev):
