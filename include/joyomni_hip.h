@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define JO_ABI_VERSION 3
+#define JO_ABI_VERSION 4
 
 /* Status codes. */
 #define JO_OK 0
@@ -70,10 +70,15 @@ int jo_abi_version(void);
  *                       5 = 128x128 and 6 = 64x64 (four waves), 7 = 128x256
  *                       (eight waves; 5-7 need K % 128 == 0, else the
  *                       register-staged kernel runs) (env JO_GEMM_SHAPE)
+ *   JO_KNOB_GEMM_SPLIT  FP8 GEMM K split: 1 (none), 2, 4 or 8 workgroups per
+ *                       tile, taken by the 128x128 and 64x64 tiles when
+ *                       jo_fp8_scaled_mm_ws has the workspace for it and
+ *                       K % (128 x split) == 0 (env JO_GEMM_SPLIT)
  * No reference counterpart (tuning and test hook). */
 #define JO_KNOB_QK_SPLIT 0
 #define JO_KNOB_KV_SPLIT 1
 #define JO_KNOB_GEMM_SHAPE 2
+#define JO_KNOB_GEMM_SPLIT 3
 
 /* Sets knob `knob` to `value` (-1 restores the automatic choice) for every
  * later launch in the process. Returns JO_ERR_INVALID for an unknown knob or
@@ -377,6 +382,29 @@ int jo_norm_scale_shift_quant_fp8(const void* x, int64_t x_stride, void* residua
 int jo_fp8_scaled_mm(const void* mat_a, int64_t lda, const void* mat_b, int64_t ldb,
                      const float* scales_a, const float* scales_b, const void* bias, void* out,
                      int64_t ldo, int64_t M, int64_t N, int64_t K, int out_dtype, void* stream);
+
+/* jo_fp8_scaled_mm with a caller-owned device workspace (16-byte aligned).
+ * With few output tiles and a long K (a few hundred rows: the text stream's
+ * Fp8Linear calls, dit.py:59-92,381,438-444) the library may split K over
+ * several workgroups per tile, which write fp32 partial products to the
+ * workspace that a second kernel adds up in a fixed order: results are the
+ * same on every run, and equal to jo_fp8_scaled_mm's up to fp32 summation
+ * order. A workspace smaller than jo_fp8_scaled_mm_workspace_bytes(M, N, K)
+ * (NULL with 0 bytes included) runs exactly as jo_fp8_scaled_mm. The
+ * workspace is in use until the work queued on `stream` finishes; two calls
+ * in flight at once need two workspaces. The torch op fp8_scaled_mm takes
+ * it from the caching allocator. Reference counterpart: the same
+ * fp8_scaled_mm (fp8_gemm.cu:1450-1546), whose CUTLASS kernel allocates its
+ * own workspace. */
+int jo_fp8_scaled_mm_ws(const void* mat_a, int64_t lda, const void* mat_b, int64_t ldb,
+                        const float* scales_a, const float* scales_b, const void* bias, void* out,
+                        int64_t ldo, int64_t M, int64_t N, int64_t K, int out_dtype,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes jo_fp8_scaled_mm_ws uses for an [M, K] x [K, N] product
+ * under the current launch knobs: splits x M x N x 4, or 0 when it does not
+ * split K (then no workspace is needed). A host-side computation. */
+int64_t jo_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* ------------------------------------------------------------------------
  * RoPE'd K and copied V into a KV pool, every layer in one launch:

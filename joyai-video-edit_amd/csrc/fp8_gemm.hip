@@ -44,6 +44,7 @@ struct GemmArgs {
   void* out;         // [M, N] out dtype, row stride ldo (elements)
   int64_t lda, ldb, ldo;
   int M, N, K;
+  float* ws = nullptr;  // split K: fp32 partial products [splits, M, N]
 };
 
 __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
@@ -806,7 +807,7 @@ struct SmallLoads {
   uint32_t off[kPerWave];         // this lane's 16-byte chunk of each slot at K offset 0
 };
 
-template <class OutTag, int BM, int BN, int NW, int NST>
+template <class OutTag, int BM, int BN, int NW, int NST, bool SPLIT>
 __device__ __forceinline__ void fp8_gemm_small_body(const GemmArgs& g) {
   constexpr int WROWS = BM / 2, WCOLS = BN / (NW / 2);  // wave tile
   constexpr int MI = WROWS / 32, J = WCOLS / 32;
@@ -839,12 +840,15 @@ __device__ __forceinline__ void fp8_gemm_small_body(const GemmArgs& g) {
     ld.off[i] = static_cast<uint32_t>(row) * static_cast<uint32_t>(is_a ? g.lda : g.ldb) +
                 (((lane & 7) ^ qswz(r)) * 16);
   }
-  const int stages = g.K / kQBK;
+  // SPLIT: workgroup z of the grid's gridDim.z takes the z-th equal share of
+  // the K stages and writes its partial product for the reduction kernel.
+  const int stages = SPLIT ? g.K / kQBK / static_cast<int>(gridDim.z) : g.K / kQBK;
+  const int s0 = SPLIT ? static_cast<int>(blockIdx.z) * stages : 0;
   auto issue = [&](int s) {
     uint8_t* dst = smem + (s % NST) * kStage;
 #pragma unroll
     for (int i = 0; i < PER; ++i)
-      __builtin_amdgcn_global_load_lds(ld.base[i] + (ld.off[i] + s * kQBK),
+      __builtin_amdgcn_global_load_lds(ld.base[i] + (ld.off[i] + (s0 + s) * kQBK),
                                        (__attribute__((address_space(3))) void*)(dst + (wave + i * NW) * 1024),
                                        16, 0, 0);
   };
@@ -909,6 +913,31 @@ __device__ __forceinline__ void fp8_gemm_small_body(const GemmArgs& g) {
     compute(s);
   }
 
+  if constexpr (SPLIT) {
+    // The partial tile as fp32: a lane's four consecutive columns per group
+    // are one 16-byte store, and a row's 32 columns of a block (128 bytes)
+    // leave in the four stores of one (i, j) back to back. Plain stores: the
+    // reduction reads them back right away.
+    float* wz = g.ws + static_cast<int64_t>(blockIdx.z) * g.M * g.N;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const int m = m0 + wm * WROWS + i * 32 + fr;
+          const int n = n0 + wn * WCOLS + j * 32 + qq * 8 + fh * 4;
+          // Each element through a scalar first: a bit_cast of a vector
+          // element expression reads element 0 with this compiler.
+          const float v0 = acc[i][j][qq * 4 + 0], v1 = acc[i][j][qq * 4 + 1];
+          const float v2 = acc[i][j][qq * 4 + 2], v3 = acc[i][j][qq * 4 + 3];
+          if (m < g.M && n < g.N)
+            st16(wz + static_cast<int64_t>(m) * g.N + n,
+                 u32x4{__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
+                       __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3)});
+        }
+    return;
+  }
   // Epilogue: the finished tile goes through LDS (free once every wave is past
   // the barrier) so that rows leave as whole 16-byte lane stores.
   float sam[MI];
@@ -959,15 +988,66 @@ __device__ __forceinline__ void fp8_gemm_small_body(const GemmArgs& g) {
   }
 }
 
-template <class OutTag, int BM, int BN, int NW, int NST>
+template <class OutTag, int BM, int BN, int NW, int NST, bool SPLIT>
 __global__ __launch_bounds__(NW * 64) void fp8_gemm_small_kernel(const GemmArgs g) {
-  fp8_gemm_small_body<OutTag, BM, BN, NW, NST>(g);
+  fp8_gemm_small_body<OutTag, BM, BN, NW, NST, SPLIT>(g);
+}
+
+// Split K, second pass: out[m, n] = epilogue of the sum over z of the
+// partials ws[z, m, n], added in z order (so every run gives the same bits),
+// eight columns a thread.
+template <class OutTag>
+__global__ __launch_bounds__(kBlock) void fp8_gemm_splitk_reduce(const GemmArgs g, int splits) {
+  const int64_t cpr = g.N / 8;  // N % 8 == 0
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (c >= static_cast<int64_t>(g.M) * cpr) return;
+  const int64_t m = c / cpr;
+  const int n = static_cast<int>(c - m * cpr) * 8;
+  const int64_t plane = static_cast<int64_t>(g.M) * g.N;
+  const float* p = g.ws + m * g.N + n;
+  float acc[8];
+  {
+    const u32x4 lo = ld16(p), hi = ld16(p + 4);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      acc[t] = elem<F32>(lo, t);
+      acc[t + 4] = elem<F32>(hi, t);
+    }
+  }
+  for (int z = 1; z < splits; ++z) {
+    const u32x4 lo = ld16(p + z * plane), hi = ld16(p + z * plane + 4);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      acc[t] += elem<F32>(lo, t);
+      acc[t + 4] += elem<F32>(hi, t);
+    }
+  }
+  const float sa = g.sa[m];
+  const u32x4 s0 = ld16(g.sb + n), s1 = ld16(g.sb + n + 4);
+  u32x4 braw{0u, 0u, 0u, 0u};
+  if (g.bias) braw = ld16(static_cast<const uint16_t*>(g.bias) + n);
+  float o[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const float sb = t < 4 ? elem<F32>(s0, t) : elem<F32>(s1, t - 4);
+    o[t] = __builtin_fmaf(sa, acc[t] * sb, g.bias ? elem<OutTag>(braw, t) : 0.f);
+  }
+  st16_nt(static_cast<uint16_t*>(g.out) + m * g.ldo + n, pack<OutTag>(o));
 }
 
 template <class OutTag, int BM, int BN, int NW, int NST>
-void launch_small(const GemmArgs& g, hipStream_t stream) {
-  hipLaunchKernelGGL((fp8_gemm_small_kernel<OutTag, BM, BN, NW, NST>),
-                     dim3((g.N + BN - 1) / BN, (g.M + BM - 1) / BM), dim3(NW * 64), 0, stream, g);
+void launch_small(const GemmArgs& g, hipStream_t stream, int splits = 1) {
+  const dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM, splits);
+  if (splits == 1) {
+    hipLaunchKernelGGL((fp8_gemm_small_kernel<OutTag, BM, BN, NW, NST, false>), grid,
+                       dim3(NW * 64), 0, stream, g);
+    return;
+  }
+  hipLaunchKernelGGL((fp8_gemm_small_kernel<OutTag, BM, BN, NW, NST, true>), grid, dim3(NW * 64),
+                     0, stream, g);
+  const int64_t chunks = static_cast<int64_t>(g.M) * (g.N / 8);
+  hipLaunchKernelGGL((fp8_gemm_splitk_reduce<OutTag>), dim3(static_cast<unsigned>((chunks + kBlock - 1) / kBlock)),
+                     dim3(kBlock), 0, stream, g, splits);
 }
 
 // CUs of the current device (queried once per device; 256, MI355X's count,
@@ -1025,8 +1105,81 @@ int auto_shape(int M, int N) {
   return shape;
 }
 
+// Split K, for few tiles and a long K (the text stream's MLP down: [256,
+// 16384] x [16384, 4096] is 64 tiles of 128x128): S workgroups share each
+// tile's K stages and write fp32 partials that a second kernel adds up in a
+// fixed order (the same bits on every run) under the epilogue. Taken by the
+// small-tile kernel at 128x128 or 64x64 when the caller passes a workspace of
+// S x M x N x 4 bytes and it cuts the cost above by 15% or more: the busiest
+// CU's operand bytes, plus the partials written and read back (they stay in
+// the caches: counted at half an operand byte) and a fixed ~9 us for the
+// second launch and the first one's tail (405 KB at the operand rate), fitted
+// on MI355X: [64, 4096] x 16384 38.8 -> 22.5 us, [256, 4096] x 16384 39.2 ->
+// 34.4 us, [512, 4096] x 16384 65.9 -> 51.7 us; [512, 4096] x 4096 stays
+// unsplit (16.5 us; split in two, 20.6).
+constexpr int64_t kSplitCap = int64_t{1} << 30;  // largest partial buffer a split uses
+
+struct GemmPlan {
+  int shape;
+  int splits;
+};
+
+void shape_dims(int shape, int M, int N, int& bm, int& bn) {
+  switch (shape) {
+    case 5: bm = 128; bn = 128; break;
+    case 6: bm = 64; bn = 64; break;
+    case 7: bm = 128; bn = 256; break;
+    default: bm = shape == 3 ? 224 : 256; bn = 256; break;
+  }
+  (void)M;
+  (void)N;
+}
+
+int64_t split_bytes(int M, int N, int splits) {
+  return splits > 1 ? static_cast<int64_t>(splits) * M * N * 4 : 0;
+}
+
+int64_t plan_cost(int M, int N, int K, int bm, int bn, int splits) {
+  const int64_t cus = cu_count();
+  const int64_t tiles = static_cast<int64_t>((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+  int64_t c = (tiles * splits + cus - 1) / cus * (bm + bn) * (K / splits);
+  if (splits > 1) c += split_bytes(M, N, splits) / cus + 405 * 1024;
+  return c;
+}
+
+GemmPlan plan_gemm(const GemmArgs& g, int64_t ws_bytes) {
+  const int forced = launch_knob(JO_KNOB_GEMM_SHAPE);
+  const int fsplit = launch_knob(JO_KNOB_GEMM_SPLIT);
+  GemmPlan p{forced >= 0 ? forced : auto_shape(g.M, g.N), 1};
+  const int64_t room = ws_bytes < kSplitCap ? ws_bytes : kSplitCap;
+  auto split_ok = [&](int sp) {
+    return g.K > 0 && g.K % (kQBK * sp) == 0 && split_bytes(g.M, g.N, sp) <= room;
+  };
+  if (fsplit >= 1) {
+    if ((p.shape == 5 || p.shape == 6) && split_ok(fsplit)) p.splits = fsplit;
+    return p;
+  }
+  if (forced >= 0) return p;
+  int bm, bn;
+  shape_dims(p.shape, g.M, g.N, bm, bn);
+  const int64_t unsplit = plan_cost(g.M, g.N, g.K, bm, bn, 1);
+  int64_t best = -1;
+  GemmPlan split{p.shape, 1};
+  const int cand[2][3] = {{5, 128, 128}, {6, 64, 64}};
+  for (const auto& c : cand)
+    for (int sp = 2; sp <= 8; sp *= 2)
+      if (split_ok(sp)) {
+        const int64_t cost = plan_cost(g.M, g.N, g.K, c[1], c[2], sp);
+        if (best < 0 || cost < best) {
+          best = cost;
+          split = GemmPlan{c[0], sp};
+        }
+      }
+  return (best >= 0 && best * 20 < unsplit * 17) ? split : p;
+}
+
 template <class OutTag>
-int launch_gemm(const GemmArgs& g, hipStream_t stream) {
+int launch_gemm(const GemmArgs& g, hipStream_t stream, int64_t ws_bytes) {
   const dim3 grid((g.N + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
   // K == 0 takes the register-staged kernel, which loads no operand bytes
   // when K is 0 and stores the epilogue of a zero accumulator (the bias).
@@ -1039,8 +1192,8 @@ int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   // 224x256, 224x128, or the small-tile kernel at 128x128, 64x64 or 128x256
   // (results are the same up to the fp32 accumulation order inside the
   // matrix cores).
-  const int forced = launch_knob(JO_KNOB_GEMM_SHAPE);
-  const int shape = forced >= 0 ? forced : auto_shape(g.M, g.N);
+  const GemmPlan plan = plan_gemm(g, ws_bytes);
+  const int shape = plan.shape;
   const bool pair_ok = pipe_ok && g.K % kQBK == 0;
   if (pipe_ok && shape == 1)
     launch_pipe<OutTag, 256, 128, 4, 3>(g, stream);
@@ -1055,9 +1208,9 @@ int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   else if (pipe_ok && shape == 4)
     launch_pipe<OutTag, 224, 128, 4, 3>(g, stream);
   else if (pair_ok && shape == 5)
-    launch_small<OutTag, 128, 128, 4, 4>(g, stream);
+    launch_small<OutTag, 128, 128, 4, 4>(g, stream, plan.splits);
   else if (pair_ok && shape == 6)
-    launch_small<OutTag, 64, 64, 4, 4>(g, stream);
+    launch_small<OutTag, 64, 64, 4, 4>(g, stream, plan.splits);
   else if (pair_ok && shape == 7)
     launch_small<OutTag, 128, 256, 8, 3>(g, stream);
   else
@@ -1070,10 +1223,11 @@ int launch_gemm(const GemmArgs& g, hipStream_t stream) {
 
 using namespace jo;
 
-extern "C" int jo_fp8_scaled_mm(const void* mat_a, int64_t lda, const void* mat_b, int64_t ldb,
-                                const float* scales_a, const float* scales_b, const void* bias,
-                                void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
-                                int out_dtype, void* stream) {
+namespace {
+int fp8_scaled_mm_impl(const void* mat_a, int64_t lda, const void* mat_b, int64_t ldb,
+                       const float* scales_a, const float* scales_b, const void* bias, void* out,
+                       int64_t ldo, int64_t M, int64_t N, int64_t K, int out_dtype,
+                       void* workspace, int64_t workspace_bytes, void* stream) {
   const char* op = "fp8_scaled_mm";
   JO_REQUIRE(out_dtype == JO_DTYPE_BF16 || out_dtype == JO_DTYPE_F16,
              "out_dtype must be Half or BFloat16");
@@ -1089,9 +1243,38 @@ extern "C" int jo_fp8_scaled_mm(const void* mat_a, int64_t lda, const void* mat_
   JO_REQUIRE((K == 0 || (mat_a && mat_b)) && scales_a && scales_b && out, "%s: null pointer", op);
   JO_REQUIRE(aligned(mat_a, 16) && aligned(mat_b, 16) && aligned(out, 16),
              "%s: operands must be 16-byte aligned", op);
+  JO_REQUIRE(workspace_bytes >= 0 && (workspace_bytes == 0 || (workspace && aligned(workspace, 16))),
+             "%s: workspace must be 16-byte aligned (or 0 bytes)", op);
   GemmArgs g{static_cast<const uint8_t*>(mat_a), static_cast<const uint8_t*>(mat_b), scales_a,
              scales_b, bias, out, lda, ldb, ldo, static_cast<int>(M), static_cast<int>(N),
-             static_cast<int>(K)};
+             static_cast<int>(K), static_cast<float*>(workspace)};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return out_dtype == JO_DTYPE_BF16 ? launch_gemm<BF16>(g, st) : launch_gemm<F16>(g, st);
+  return out_dtype == JO_DTYPE_BF16 ? launch_gemm<BF16>(g, st, workspace_bytes)
+                                    : launch_gemm<F16>(g, st, workspace_bytes);
+}
+}  // namespace
+
+extern "C" int jo_fp8_scaled_mm(const void* mat_a, int64_t lda, const void* mat_b, int64_t ldb,
+                                const float* scales_a, const float* scales_b, const void* bias,
+                                void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                                int out_dtype, void* stream) {
+  return fp8_scaled_mm_impl(mat_a, lda, mat_b, ldb, scales_a, scales_b, bias, out, ldo, M, N, K,
+                            out_dtype, nullptr, 0, stream);
+}
+
+extern "C" int jo_fp8_scaled_mm_ws(const void* mat_a, int64_t lda, const void* mat_b,
+                                   int64_t ldb, const float* scales_a, const float* scales_b,
+                                   const void* bias, void* out, int64_t ldo, int64_t M, int64_t N,
+                                   int64_t K, int out_dtype, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
+  return fp8_scaled_mm_impl(mat_a, lda, mat_b, ldb, scales_a, scales_b, bias, out, ldo, M, N, K,
+                            out_dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t jo_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return 0;
+  GemmArgs g{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, K, K, N,
+             static_cast<int>(M), static_cast<int>(N), static_cast<int>(K)};
+  const GemmPlan p = plan_gemm(g, kSplitCap);
+  return split_bytes(g.M, g.N, p.splits);
 }

@@ -782,11 +782,18 @@ torch::Tensor fp8_scaled_mm(const torch::Tensor& mat_a, const torch::Tensor& mat
               "out must be multiple of 16 bytes for memory alignment");
   if (M == 0 || N == 0) return out;
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(mat_a.device());
-  check_status(jo_fp8_scaled_mm(mat_a.data_ptr(), lda, mat_b.data_ptr(), ldb,
-                                scales_a.data_ptr<float>(), scales_b.data_ptr<float>(),
-                                has_bias ? bias->data_ptr() : nullptr, out.data_ptr(), N, M, N, K,
-                                out_dtype == torch::kBFloat16 ? JO_DTYPE_BF16 : JO_DTYPE_F16,
-                                current_stream(mat_a)),
+  // A split-K workspace when the library would use one (few rows, long K),
+  // from the caching allocator on this stream (so also under graph capture);
+  // it goes back to the cache when this call returns, stream-ordered.
+  const int64_t ws_bytes = jo_fp8_scaled_mm_workspace_bytes(M, N, K);
+  torch::Tensor ws;
+  if (ws_bytes > 0) ws = torch::empty({ws_bytes}, mat_a.options().dtype(torch::kUInt8));
+  check_status(jo_fp8_scaled_mm_ws(mat_a.data_ptr(), lda, mat_b.data_ptr(), ldb,
+                                   scales_a.data_ptr<float>(), scales_b.data_ptr<float>(),
+                                   has_bias ? bias->data_ptr() : nullptr, out.data_ptr(), N, M, N,
+                                   K, out_dtype == torch::kBFloat16 ? JO_DTYPE_BF16 : JO_DTYPE_F16,
+                                   ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
+                                   current_stream(mat_a)),
                "fp8_scaled_mm");
   return out;
 }

@@ -16,7 +16,7 @@ LIB_NAME = "libjoyomni_hip.so"
 
 # The header's JO_ABI_VERSION this binding's SIGNATURES follow; a library
 # reporting another version is refused at load.
-JO_ABI_VERSION = 3
+JO_ABI_VERSION = 4
 
 JO_OK = 0
 JO_ERR_INVALID = 1
@@ -33,10 +33,14 @@ JO_NORM_RMS = 1
 JO_KNOB_QK_SPLIT = 0
 JO_KNOB_KV_SPLIT = 1
 JO_KNOB_GEMM_SHAPE = 2
+JO_KNOB_GEMM_SPLIT = 3
 
 _P = c_void_p
 _I64 = c_int64
 _F = c_float
+
+# Entry points that return something other than an int status.
+RESTYPES = {"jo_fp8_scaled_mm_workspace_bytes": _I64}
 
 # name -> argument types, in header order.
 SIGNATURES: dict[str, list] = {
@@ -71,6 +75,9 @@ SIGNATURES: dict[str, list] = {
         _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _I64,
         c_int, c_int, _F, _P],
     "jo_fp8_scaled_mm": [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, c_int, _P],
+    "jo_fp8_scaled_mm_ws": [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, c_int, _P,
+                            _I64, _P],
+    "jo_fp8_scaled_mm_workspace_bytes": [_I64, _I64, _I64],
     "jo_kv_commit_rope": [
         _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
         _I64, _P, _P, _I64, _I64, c_int, _P],
@@ -110,7 +117,7 @@ def lib() -> ctypes.CDLL:
         fn = getattr(handle, name, None)
         if fn is None:  # reported by the export test; call() raises on use
             continue
-        fn.restype = c_int
+        fn.restype = RESTYPES.get(name, c_int)
         fn.argtypes = argtypes
     _lib = handle
     return _lib

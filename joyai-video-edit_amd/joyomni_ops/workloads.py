@@ -257,7 +257,11 @@ def alloc_outputs(cfg: Config, inputs: dict) -> dict:
         return {"out": torch.empty(d["B"], d["L"], d["H"], d["D"], dtype=torch.bfloat16,
                                    device=dev)}
     if cfg.op == "gemm":
-        return {"out": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev)}
+        # The split-K workspace the library asks for (none at the image
+        # stream's shapes), as the torch op would take it.
+        ws = _abi.lib().jo_fp8_scaled_mm_workspace_bytes(d["M"], d["N"], d["K"])
+        return {"out": torch.empty(d["M"], d["N"], dtype=torch.bfloat16, device=dev),
+                "ws": torch.empty(max(ws, 0), dtype=torch.uint8, device=dev)}
     if cfg.op == "add_ln_quant":
         return {"q": torch.empty(d["M"], d["N"], dtype=torch.float8_e4m3fn, device=dev),
                 "s": torch.empty(d["M"], dtype=torch.float32, device=dev)}
@@ -318,8 +322,10 @@ def launch(cfg: Config, t: dict, stream_handle: int, freqs: torch.Tensor | None 
                   d["eps"], stream_handle)
     elif cfg.op == "gemm":
         M, N, K = d["M"], d["N"], d["K"]
-        _abi.call("jo_fp8_scaled_mm", p(t["a"]), K, p(t["w"]), K, p(t["sa"]), p(t["sb"]),
-                  p(t["bias"]), p(t["out"]), N, M, N, K, _abi.JO_DTYPE_BF16, stream_handle)
+        ws = t["ws"]
+        _abi.call("jo_fp8_scaled_mm_ws", p(t["a"]), K, p(t["w"]), K, p(t["sa"]), p(t["sb"]),
+                  p(t["bias"]), p(t["out"]), N, M, N, K, _abi.JO_DTYPE_BF16,
+                  p(ws) if ws.numel() else None, ws.numel(), stream_handle)
     elif cfg.op == "kv_commit":
         L, T, P, H, D = d["L"], d["T"], d["P"], d["H"], d["D"]
         hd = H * D

@@ -22,7 +22,7 @@ def header_functions() -> dict[str, int]:
     """name -> number of parameters, for every function declared in the header."""
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     out = {}
-    for m in re.finditer(r"\b(?:int|const char\*)\s+(jo_\w+)\s*\(([^)]*)\)\s*;", text):
+    for m in re.finditer(r"\b(?:int|int64_t|const char\*)\s+(jo_\w+)\s*\(([^)]*)\)\s*;", text):
         params = m.group(2).strip()
         out[m.group(1)] = 0 if params in ("", "void") else len(params.split(","))
     return out
@@ -35,7 +35,8 @@ def test_header_declares_all_entry_points():
                  "jo_fused_qk_norm_rope_3d_kvcache", "jo_fused_norm_scale_shift", "jo_rmsnorm",
                  "jo_fused_add_layernorm_scale_shift", "jo_rmsnorm_quant_fp8",
                  "jo_rmsnorm_heads", "jo_norm_scale_shift_quant_fp8", "jo_fp8_scaled_mm",
-                 "jo_kv_commit_rope", "jo_fused_norm_scale_shift_per_sample"):
+                 "jo_kv_commit_rope", "jo_fused_norm_scale_shift_per_sample",
+                 "jo_fp8_scaled_mm_ws", "jo_fp8_scaled_mm_workspace_bytes"):
         assert name in fns, name
 
 
@@ -57,7 +58,7 @@ def test_ctypes_signatures_match_header(abi):
 
 
 def test_abi_version(abi):
-    assert abi.lib().jo_abi_version() == 3
+    assert abi.lib().jo_abi_version() == 4
 
 
 # Launch-size bounds of the entry points (work items of one launch < 2^32).
@@ -180,7 +181,8 @@ def test_validation_errors_without_gpu(abi, name, args, msg):
 def test_launch_override(abi):
     lib = abi.lib()
     accepted = {abi.JO_KNOB_QK_SPLIT: {1, 2, 4, 6, 8}, abi.JO_KNOB_KV_SPLIT: {1, 2},
-                abi.JO_KNOB_GEMM_SHAPE: {0, 1, 2, 3, 4, 5, 6, 7}}
+                abi.JO_KNOB_GEMM_SHAPE: {0, 1, 2, 3, 4, 5, 6, 7},
+                abi.JO_KNOB_GEMM_SPLIT: {1, 2, 4, 8}}
     for knob, ok in accepted.items():
         for v in range(-3, 66):
             want = abi.JO_OK if (v == -1 or v in ok) else abi.JO_ERR_INVALID
@@ -188,8 +190,33 @@ def test_launch_override(abi):
             if want != abi.JO_OK:
                 assert "not one knob" in abi.last_error()
         assert lib.jo_set_launch_override(knob, -1) == abi.JO_OK
-    assert lib.jo_set_launch_override(3, 1) == abi.JO_ERR_INVALID
+    assert lib.jo_set_launch_override(4, 1) == abi.JO_ERR_INVALID
     assert "unknown knob" in abi.last_error()
+
+
+def test_gemm_workspace_bytes(abi):
+    """The split-K workspace the FP8 GEMM asks for (a host computation, the
+    same with or without a GPU: 256 CUs assumed when none is visible): none
+    for the image stream's shapes, S x M x N x 4 bytes for few rows and a long
+    K, and what a forced split asks for (taken only by the small tiles)."""
+    lib = abi.lib()
+    wb = lib.jo_fp8_scaled_mm_workspace_bytes
+    for M, N, K in [(3120, 12288, 4096), (3120, 4096, 16384), (256, 12288, 4096),
+                    (1024, 4096, 16384)]:
+        assert wb(M, N, K) == 0, (M, N, K)
+    assert wb(256, 4096, 16384) == 4 * 256 * 4096 * 4   # 128x128 tiles, K in four
+    assert wb(64, 4096, 16384) == 4 * 64 * 4096 * 4     # 64x64 tiles, K in four
+    assert wb(0, 4096, 4096) == 0 and wb(256, 4096, 0) == 0
+    try:
+        assert lib.jo_set_launch_override(abi.JO_KNOB_GEMM_SHAPE, 6) == abi.JO_OK
+        assert lib.jo_set_launch_override(abi.JO_KNOB_GEMM_SPLIT, 8) == abi.JO_OK
+        assert wb(100, 520, 1024) == 8 * 100 * 520 * 4
+        assert wb(100, 520, 896) == 0          # K % (128 x 8) != 0: no split
+        assert lib.jo_set_launch_override(abi.JO_KNOB_GEMM_SHAPE, 3) == abi.JO_OK
+        assert wb(100, 520, 1024) == 0         # the 224-row tiles never split
+    finally:
+        lib.jo_set_launch_override(abi.JO_KNOB_GEMM_SHAPE, -1)
+        lib.jo_set_launch_override(abi.JO_KNOB_GEMM_SPLIT, -1)
 
 
 def test_launch_override_env_values_are_checked(tmp_path):
@@ -202,11 +229,13 @@ def test_launch_override_env_values_are_checked(tmp_path):
             "lib = _abi.lib()\n"
             "assert lib.jo_set_launch_override(_abi.JO_KNOB_QK_SPLIT, -1) == 0\n"
             "print('loaded')\n" % str(PKG))
-    env = dict(os.environ, JO_QK_SPLIT="3", JO_KV_SPLIT="2", JO_GEMM_SHAPE="7x")
+    env = dict(os.environ, JO_QK_SPLIT="3", JO_KV_SPLIT="2", JO_GEMM_SHAPE="7x",
+               JO_GEMM_SPLIT="3")
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env,
                        timeout=300)
     assert r.returncode == 0 and "loaded" in r.stdout, r.stderr
     assert "ignoring JO_QK_SPLIT=3" in r.stderr and "ignoring JO_GEMM_SHAPE=7x" in r.stderr
+    assert "ignoring JO_GEMM_SPLIT=3" in r.stderr
     assert "JO_KV_SPLIT" not in r.stderr
 
 

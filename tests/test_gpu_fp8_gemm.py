@@ -166,6 +166,57 @@ def test_fp8_scaled_mm_text_stream_shapes(dev, M, N, K):
     assert bad.numel() == 0, f"[{M},{N},{K}]: {bad.shape[0]} outputs off, first {bad[0].tolist()}"
 
 
+@pytest.mark.parametrize("split", [2, 4, 8])
+@pytest.mark.parametrize("M,N,K", [(100, 520, 1024), (257, 264, 2048), (64, 4096, 8192)])
+def test_fp8_scaled_mm_split_k(dev, split, M, N, K):
+    """K split over `split` workgroups per tile (fp32 partials in the op's
+    workspace, added in a fixed order by the second kernel): taken under the
+    forced 128x128 and 64x64 shapes, the others ignore it. Against the exact
+    oracle, and bit-identical on a second call."""
+    import joyomni_ops as jo
+    from joyomni_ops import _abi
+    a, w, sa, sb, bias = operands(M, N, K, M + N + K + split)
+    args = (a.to(dev), w.to(dev).t(), sa.to(dev), sb.to(dev), torch.bfloat16, bias.to(dev))
+    _abi.call("jo_set_launch_override", _abi.JO_KNOB_GEMM_SPLIT, split)
+    try:
+        out = jo.fp8_scaled_mm(*args)
+        again = jo.fp8_scaled_mm(*args)
+        torch.cuda.synchronize()
+    finally:
+        _abi.call("jo_set_launch_override", _abi.JO_KNOB_GEMM_SPLIT, -1)
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    check(out, a, w.t(), sa, sb, bias, f"[{M},{N},{K}] split {split}")
+
+
+def test_fp8_scaled_mm_ws_small_workspace_runs_unsplit(abi, dev, stream_handle):
+    """jo_fp8_scaled_mm_ws with less workspace than the split needs (or none)
+    runs as jo_fp8_scaled_mm: the same bits."""
+    M, N, K = 256, 4096, 16384
+    need = abi.lib().jo_fp8_scaled_mm_workspace_bytes(M, N, K)
+    a, w, sa, sb, bias = operands(M, N, K, 77)
+    ad, wd = a.view(torch.uint8).to(dev), w.view(torch.uint8).to(dev)
+    sad, sbd, bd = sa.to(dev), sb.to(dev), bias.to(dev)
+    outs = []
+    sizes = (0, need - 16, need) if need > 0 else (0, 0, 0)   # forced shapes never split
+    for ws_bytes in sizes:
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        abi.call("jo_fp8_scaled_mm_ws", ad.data_ptr(), K, wd.data_ptr(), K, sad.data_ptr(),
+                 sbd.data_ptr(), bd.data_ptr(), out.data_ptr(), N, M, N, K,
+                 abi.dtype_code(torch.bfloat16), ws.data_ptr() if ws_bytes else None, ws_bytes,
+                 stream_handle)
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+    plain = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    abi.call("jo_fp8_scaled_mm", ad.data_ptr(), K, wd.data_ptr(), K, sad.data_ptr(),
+             sbd.data_ptr(), bd.data_ptr(), plain.data_ptr(), N, M, N, K,
+             abi.dtype_code(torch.bfloat16), stream_handle)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), plain.cpu().view(torch.int16))
+    assert torch.equal(outs[1].view(torch.int16), plain.cpu().view(torch.int16))
+    check(outs[2], a, w.t(), sa, sb, bias, "split with the full workspace")
+
+
 def test_fp8_linear_reference_bench_shape(dev):
     """The reference benchmark's FP8 linear (test_bench.py:160-200): x [4096, 4096]
     bf16 through Fp8Linear's per-token quantization and the GEMM with a
