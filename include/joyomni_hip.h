@@ -406,6 +406,20 @@ int jo_fp8_scaled_mm_ws(const void* mat_a, int64_t lda, const void* mat_b, int64
  * split K (then no workspace is needed). A host-side computation. */
 int64_t jo_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
+/* jo_fp8_scaled_mm_ws without a caller workspace, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): no counterpart in the reference. The split-K partials
+ * (jo_fp8_scaled_mm_workspace_bytes(M, N, K) bytes, the same plan as
+ * jo_fp8_scaled_mm_ws with a workspace that size, so the same bits) go to a
+ * static device array of 32 MiB that each GPU holds until the process ends;
+ * a shape needing more is refused with JO_ERR_INVALID. It calls no
+ * allocator. Every call on a GPU shares that GPU's array: two calls in
+ * flight on one GPU at once (on two streams) race. */
+int jo_fp8_scaled_mm_noalloc(const void* mat_a, int64_t lda, const void* mat_b, int64_t ldb,
+                             const float* scales_a, const float* scales_b, const void* bias,
+                             void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                             int out_dtype, void* stream);
+
 /* ------------------------------------------------------------------------
  * RoPE'd K and copied V into a KV pool, every layer in one launch:
  *   dst_k[l, b, off + n, :] = apply_rotary_emb(src_k[l, b, n, :], cos[b, n], sin[b, n])

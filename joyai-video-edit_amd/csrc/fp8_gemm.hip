@@ -1271,10 +1271,67 @@ extern "C" int jo_fp8_scaled_mm_ws(const void* mat_a, int64_t lda, const void* m
                             out_dtype, workspace, workspace_bytes, stream);
 }
 
+// Allocation-free variant: the split-K partials go to this file-scope device
+// array instead of a caller's workspace. Each GPU the library runs on holds
+// its own copy (kScratchBytes) until the process ends. Host code never uses
+// the array's name as an address (it is a host-side stand-in there): the
+// device address comes from hipGetSymbolAddress, once per device.
+constexpr int64_t kScratchBytes = int64_t{32} << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / 4];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];
+
+// The current device's address of `scratch`, looked up on the first call on
+// that device (with it current) and kept.
+int scratch_address(void** out) {
+  int dev = -1;
+  const hipError_t ge = hipGetDevice(&dev);
+  if (ge != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("fp8_scaled_mm_noalloc: no usable current device (%s)", hipGetErrorString(ge));
+    return JO_ERR_HIP;
+  }
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("fp8_scaled_mm_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                dev, hipGetErrorString(e));
+      return JO_ERR_HIP;
+    }
+    g_scratch[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return JO_OK;
+}
+}  // namespace
+
 extern "C" int64_t jo_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return 0;
   GemmArgs g{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, K, K, N,
              static_cast<int>(M), static_cast<int>(N), static_cast<int>(K)};
   const GemmPlan p = plan_gemm(g, kSplitCap);
   return split_bytes(g.M, g.N, p.splits);
+}
+
+extern "C" int jo_fp8_scaled_mm_noalloc(const void* mat_a, int64_t lda, const void* mat_b,
+                                        int64_t ldb, const float* scales_a,
+                                        const float* scales_b, const void* bias, void* out,
+                                        int64_t ldo, int64_t M, int64_t N, int64_t K,
+                                        int out_dtype, void* stream) {
+  const int64_t need = jo_fp8_scaled_mm_workspace_bytes(M, N, K);
+  JO_REQUIRE(need <= kScratchBytes,
+             "fp8_scaled_mm_noalloc: the split-K partials of [%lld, %lld] x %lld need %lld bytes, "
+             "more than the %lld-byte static scratch (jo_fp8_scaled_mm_ws takes a workspace of "
+             "any size)",
+             static_cast<long long>(M), static_cast<long long>(K), static_cast<long long>(N),
+             static_cast<long long>(need), static_cast<long long>(kScratchBytes));
+  void* ws = nullptr;
+  if (need > 0) {
+    const int st = scratch_address(&ws);
+    if (st != JO_OK) return st;
+  }
+  return fp8_scaled_mm_impl(mat_a, lda, mat_b, ldb, scales_a, scales_b, bias, out, ldo, M, N, K,
+                            out_dtype, ws, need, stream);
 }

@@ -78,6 +78,8 @@ SIGNATURES: dict[str, list] = {
     "jo_fp8_scaled_mm_ws": [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, c_int, _P,
                             _I64, _P],
     "jo_fp8_scaled_mm_workspace_bytes": [_I64, _I64, _I64],
+    "jo_fp8_scaled_mm_noalloc": [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, c_int,
+                                 _P],
     "jo_kv_commit_rope": [
         _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
         _I64, _P, _P, _I64, _I64, c_int, _P],
