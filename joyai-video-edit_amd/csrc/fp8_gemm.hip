@@ -791,7 +791,8 @@ void launch_pair(const GemmArgs& g, hipStream_t stream) {
 // Small-tile kernel, for grids the 8-wave 224/256-row tiles would leave
 // mostly idle (a few hundred rows: the text stream's Fp8Linear calls; 224x256
 // tiles give [256, 4096] 32 tiles for 256 CUs). NW waves on a BM x BN tile
-// (64x64 or 128x128 with four, 128x256 with eight) in a 2 x NW/2 grid of wave
+// (64x64, 64x128, 128x128 or 128x192 with four, 128x256 with eight) in a
+// 2 x NW/2 grid of wave
 // tiles; K advances in 128-byte stages (whole lines, the LDS layout of the
 // 128-byte-stage kernel) through a ring of NST slots that direct loads fill
 // NST-1 stages ahead; one barrier a stage.
@@ -1080,7 +1081,7 @@ int pick_tile_rows(int M, int N) {
 // CU streams from L2 (~45 KB/us per CU for every kernel here), so the cost of
 // a shape is (tiles per CU, rounded up) x (BM + BN) bytes per K byte: the 8-wave
 // 224x256 or 256x256 tiles (pick_tile_rows) unless the small-tile kernel at
-// 128x256, 128x128 or 64x64 streams fewer bytes on the busiest CU, as where
+// 128x256, 128x192, 128x128, 64x128 or 64x64 streams fewer bytes on the busiest CU, as where
 // the large tiles leave most CUs idle (ties go to the smaller tile: two 64x64
 // workgroups share a CU). Measured on MI355X, M = 256: [256, 4096] x 4096
 // 34.2 -> 11.4 us (64x64), [256, 12288] x 4096 42.4 -> 24.3 us (128x128);
@@ -1093,15 +1094,13 @@ int auto_shape(int M, int N) {
   const int bm = pick_tile_rows(M, N);
   int shape = bm == 224 ? 3 : 0;
   int64_t best = cost(bm, 256);
-  if (cost(128, 256) <= best) {
-    best = cost(128, 256);
-    shape = 7;
-  }
-  if (cost(128, 128) <= best) {
-    best = cost(128, 128);
-    shape = 5;
-  }
-  if (cost(64, 64) <= best) shape = 6;
+  // Larger tiles first: a tie goes to the smaller one.
+  const int small[5][3] = {{7, 128, 256}, {9, 128, 192}, {5, 128, 128}, {8, 64, 128}, {6, 64, 64}};
+  for (const auto& t : small)
+    if (cost(t[1], t[2]) <= best) {
+      best = cost(t[1], t[2]);
+      shape = t[0];
+    }
   return shape;
 }
 
@@ -1129,6 +1128,8 @@ void shape_dims(int shape, int M, int N, int& bm, int& bn) {
     case 5: bm = 128; bn = 128; break;
     case 6: bm = 64; bn = 64; break;
     case 7: bm = 128; bn = 256; break;
+    case 8: bm = 64; bn = 128; break;
+    case 9: bm = 128; bn = 192; break;
     default: bm = shape == 3 ? 224 : 256; bn = 256; break;
   }
   (void)M;
@@ -1188,8 +1189,9 @@ int launch_gemm(const GemmArgs& g, hipStream_t stream, int64_t ws_bytes) {
   // 8-wave 256-column tiles measured faster than two 4-wave 128-column
   // workgroups per CU at every deployment shape (3120x12288x4096: 199 -> 185
   // us, 3120x16384x4096: 257 -> 233 us). The JO_KNOB_GEMM_SHAPE override
-  // 0|1|2|3|4|5|6|7 forces 256x256, 256x128, the register-staged kernel,
-  // 224x256, 224x128, or the small-tile kernel at 128x128, 64x64 or 128x256
+  // 0|1|2|3|4|5|6|7|8|9 forces 256x256, 256x128, the register-staged kernel,
+  // 224x256, 224x128, or the small-tile kernel at 128x128, 64x64, 128x256,
+  // 64x128 or 128x192
   // (results are the same up to the fp32 accumulation order inside the
   // matrix cores).
   const GemmPlan plan = plan_gemm(g, ws_bytes);
@@ -1213,6 +1215,10 @@ int launch_gemm(const GemmArgs& g, hipStream_t stream, int64_t ws_bytes) {
     launch_small<OutTag, 64, 64, 4, 4>(g, stream, plan.splits);
   else if (pair_ok && shape == 7)
     launch_small<OutTag, 128, 256, 8, 3>(g, stream);
+  else if (pair_ok && shape == 8)
+    launch_small<OutTag, 64, 128, 4, 4>(g, stream);
+  else if (pair_ok && shape == 9)
+    launch_small<OutTag, 128, 192, 4, 3>(g, stream);
   else
     hipLaunchKernelGGL((fp8_gemm_kernel<OutTag>), grid, dim3(kBlock), 0, stream, g);
   return launch_status("fp8_scaled_mm");

@@ -14,14 +14,14 @@ thread_local char g_last_error[512] = {0};
 constexpr int kKnobs = 4;
 
 // The values each knob accepts besides -1 (the library's own choice):
-// QK waves per token 1, 2, 4, 6, 8; KV rows on 1 or 2 waves; GEMM shapes 0-7;
+// QK waves per token 1, 2, 4, 6, 8; KV rows on 1 or 2 waves; GEMM shapes 0-9;
 // GEMM K splits 1, 2, 4, 8.
 bool knob_value_ok(int knob, int v) {
   if (v == -1) return true;
   switch (knob) {
     case JO_KNOB_QK_SPLIT: return v == 1 || v == 2 || v == 4 || v == 6 || v == 8;
     case JO_KNOB_KV_SPLIT: return v == 1 || v == 2;
-    case JO_KNOB_GEMM_SHAPE: return v >= 0 && v <= 7;
+    case JO_KNOB_GEMM_SHAPE: return v >= 0 && v <= 9;
     case JO_KNOB_GEMM_SPLIT: return v == 1 || v == 2 || v == 4 || v == 8;
     default: return false;
   }

@@ -18,12 +18,13 @@ from oracle import ops
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["auto", "0", "1", "2", "3", "4", "5", "6", "7"], autouse=True)
+@pytest.fixture(params=["auto", "0", "1", "2", "3", "4", "5", "6", "7", "8", "9"],
+                autouse=True)
 def gemm_shape(request):
     """Every kernel variant: the default choice, 256x256 (8 waves), 256x128
     (4 waves), the register-staged kernel (also the K % 64 != 0 path), 224x256
     (8 waves, 4 and 3 row blocks), 224x128 (4 waves), and the small-tile
-    kernel at 128x128 and 64x64 (4 waves) and 128x256 (8 waves)."""
+    kernel at 128x128, 64x64, 64x128 and 128x192 (4 waves) and 128x256 (8 waves)."""
     from joyomni_ops import _abi
     value = -1 if request.param == "auto" else int(request.param)
     _abi.call("jo_set_launch_override", _abi.JO_KNOB_GEMM_SHAPE, value)
