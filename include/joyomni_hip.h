@@ -68,8 +68,9 @@ int jo_abi_version(void);
  *   JO_KNOB_GEMM_SHAPE  FP8 GEMM tile: 0 = 256x256, 1 = 256x128, 2 = the
  *                       register-staged kernel, 3 = 224x256, 4 = 224x128,
  *                       5 = 128x128 and 6 = 64x64 (four waves), 7 = 128x256
- *                       (eight waves), 8 = 64x128 and 9 = 128x192 (four
- *                       waves; 5-9 need K % 128 == 0, else the
+ *                       (eight waves), 8 = 64x128, 9 = 128x192 and 10 =
+ *                       128x96 (four waves), 11 = 64x96 (two waves; 5-11
+ *                       need K % 128 == 0, else the
  *                       register-staged kernel runs) (env JO_GEMM_SHAPE)
  *   JO_KNOB_GEMM_SPLIT  FP8 GEMM K split: 1 (none), 2, 4 or 8 workgroups per
  *                       tile, taken by the 128x128 and 64x64 tiles when

@@ -792,8 +792,9 @@ void launch_pair(const GemmArgs& g, hipStream_t stream) {
 // mostly idle (a few hundred rows: the text stream's Fp8Linear calls; 224x256
 // tiles give [256, 4096] 32 tiles for 256 CUs). NW waves on a BM x BN tile
 // (64x64, 64x128, 128x128 or 128x192 with four, 128x256 with eight) in a
-// 2 x NW/2 grid of wave
-// tiles; K advances in 128-byte stages (whole lines, the LDS layout of the
+// WGM x NW/WGM grid of wave tiles (WGM = 2); the 96-column tiles give each
+// wave 32 x 96 (128x96: four waves down the rows, WGM = 4; 64x96: two waves,
+// WGM = 2, two workgroups to a CU's LDS); K advances in 128-byte stages (whole lines, the LDS layout of the
 // 128-byte-stage kernel) through a ring of NST slots that direct loads fill
 // NST-1 stages ahead; one barrier a stage.
 // Its K loop streams (BM + BN) x 128 bytes a stage for BM x BN x 128 MACs, so
@@ -808,22 +809,23 @@ struct SmallLoads {
   uint32_t off[kPerWave];         // this lane's 16-byte chunk of each slot at K offset 0
 };
 
-template <class OutTag, int BM, int BN, int NW, int NST, bool SPLIT>
+template <class OutTag, int BM, int BN, int NW, int NST, bool SPLIT, int WGM>
 __device__ __forceinline__ void fp8_gemm_small_body(const GemmArgs& g) {
-  constexpr int WROWS = BM / 2, WCOLS = BN / (NW / 2);  // wave tile
+  constexpr int WROWS = BM / WGM, WCOLS = BN / (NW / WGM);  // wave tile
   constexpr int MI = WROWS / 32, J = WCOLS / 32;
   constexpr int kStage = (BM + BN) * kQBK;
   constexpr int kRowBytes = BN * 2 + 16;  // padded LDS row of the staged output tile
   constexpr int kChunksPerRow = BN * 2 / 16;
   using Loads = SmallLoads<BM, BN, NW>;
   constexpr int PER = Loads::kPerWave;
-  static_assert(MI >= 1 && J >= 1 && BM * kRowBytes <= NST * kStage && NST >= 2 && NST <= 5,
+  static_assert(NW % WGM == 0 && WROWS % 32 == 0 && WCOLS % 32 == 0 && MI >= 1 && J >= 1 &&
+                    BM * kRowBytes <= NST * kStage && NST >= 2 && NST <= 5,
                 "tile shape");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * kStage];
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % WGM, wn = wave / WGM;
   int m0, n0;
   xcd_grouped_tile(BM, BN, m0, n0);
 
@@ -989,9 +991,9 @@ __device__ __forceinline__ void fp8_gemm_small_body(const GemmArgs& g) {
   }
 }
 
-template <class OutTag, int BM, int BN, int NW, int NST, bool SPLIT>
+template <class OutTag, int BM, int BN, int NW, int NST, bool SPLIT, int WGM>
 __global__ __launch_bounds__(NW * 64) void fp8_gemm_small_kernel(const GemmArgs g) {
-  fp8_gemm_small_body<OutTag, BM, BN, NW, NST, SPLIT>(g);
+  fp8_gemm_small_body<OutTag, BM, BN, NW, NST, SPLIT, WGM>(g);
 }
 
 // Split K, second pass: out[m, n] = epilogue of the sum over z of the
@@ -1036,15 +1038,15 @@ __global__ __launch_bounds__(kBlock) void fp8_gemm_splitk_reduce(const GemmArgs 
   st16_nt(static_cast<uint16_t*>(g.out) + m * g.ldo + n, pack<OutTag>(o));
 }
 
-template <class OutTag, int BM, int BN, int NW, int NST>
+template <class OutTag, int BM, int BN, int NW, int NST, int WGM = 2>
 void launch_small(const GemmArgs& g, hipStream_t stream, int splits = 1) {
   const dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM, splits);
   if (splits == 1) {
-    hipLaunchKernelGGL((fp8_gemm_small_kernel<OutTag, BM, BN, NW, NST, false>), grid,
+    hipLaunchKernelGGL((fp8_gemm_small_kernel<OutTag, BM, BN, NW, NST, false, WGM>), grid,
                        dim3(NW * 64), 0, stream, g);
     return;
   }
-  hipLaunchKernelGGL((fp8_gemm_small_kernel<OutTag, BM, BN, NW, NST, true>), grid, dim3(NW * 64),
+  hipLaunchKernelGGL((fp8_gemm_small_kernel<OutTag, BM, BN, NW, NST, true, WGM>), grid, dim3(NW * 64),
                      0, stream, g);
   const int64_t chunks = static_cast<int64_t>(g.M) * (g.N / 8);
   hipLaunchKernelGGL((fp8_gemm_splitk_reduce<OutTag>), dim3(static_cast<unsigned>((chunks + kBlock - 1) / kBlock)),
@@ -1081,11 +1083,14 @@ int pick_tile_rows(int M, int N) {
 // CU streams from L2 (~45 KB/us per CU for every kernel here), so the cost of
 // a shape is (tiles per CU, rounded up) x (BM + BN) bytes per K byte: the 8-wave
 // 224x256 or 256x256 tiles (pick_tile_rows) unless the small-tile kernel at
-// 128x256, 128x192, 128x128, 64x128 or 64x64 streams fewer bytes on the busiest CU, as where
-// the large tiles leave most CUs idle (ties go to the smaller tile: two 64x64
-// workgroups share a CU). Measured on MI355X, M = 256: [256, 4096] x 4096
-// 34.2 -> 11.4 us (64x64), [256, 12288] x 4096 42.4 -> 24.3 us (128x128);
-// M = 1024, [1024, 4096] x 16384 155.4 -> 86.4 us (128x128).
+// 128x256, 128x192, 128x128, 128x96, 64x128, 64x96 or 64x64 streams fewer bytes on the
+// busiest CU, as where the large tiles leave most CUs idle (ties go to the
+// smaller tile: two 64x64 workgroups share a CU). The 96-column tiles cut
+// N = 12288 into 128 columns of tiles, so 128 or 256 rows fill the 256 CUs.
+// Measured on MI355X, M = 256: [256, 4096] x 4096 34.2 -> 11.4 us (64x64),
+// [256, 12288] x 4096 42.4 -> 24.3 us (128x128) -> 22.0 us (128x96); M = 128,
+// [128, 12288] x 4096 20.4 us (64x128) -> 17.9 us (64x96); M = 1024,
+// [1024, 4096] x 16384 155.4 -> 86.4 us (128x128).
 int auto_shape(int M, int N) {
   const int64_t cus = cu_count();
   auto cost = [&](int64_t bm, int64_t bn) {
@@ -1095,7 +1100,8 @@ int auto_shape(int M, int N) {
   int shape = bm == 224 ? 3 : 0;
   int64_t best = cost(bm, 256);
   // Larger tiles first: a tie goes to the smaller one.
-  const int small[5][3] = {{7, 128, 256}, {9, 128, 192}, {5, 128, 128}, {8, 64, 128}, {6, 64, 64}};
+  const int small[7][3] = {{7, 128, 256}, {9, 128, 192}, {5, 128, 128}, {10, 128, 96},
+                            {8, 64, 128}, {11, 64, 96}, {6, 64, 64}};
   for (const auto& t : small)
     if (cost(t[1], t[2]) <= best) {
       best = cost(t[1], t[2]);
@@ -1130,6 +1136,8 @@ void shape_dims(int shape, int M, int N, int& bm, int& bn) {
     case 7: bm = 128; bn = 256; break;
     case 8: bm = 64; bn = 128; break;
     case 9: bm = 128; bn = 192; break;
+    case 10: bm = 128; bn = 96; break;
+    case 11: bm = 64; bn = 96; break;
     default: bm = shape == 3 ? 224 : 256; bn = 256; break;
   }
   (void)M;
@@ -1189,9 +1197,9 @@ int launch_gemm(const GemmArgs& g, hipStream_t stream, int64_t ws_bytes) {
   // 8-wave 256-column tiles measured faster than two 4-wave 128-column
   // workgroups per CU at every deployment shape (3120x12288x4096: 199 -> 185
   // us, 3120x16384x4096: 257 -> 233 us). The JO_KNOB_GEMM_SHAPE override
-  // 0|1|2|3|4|5|6|7|8|9 forces 256x256, 256x128, the register-staged kernel,
-  // 224x256, 224x128, or the small-tile kernel at 128x128, 64x64, 128x256,
-  // 64x128 or 128x192
+  // 0|1|2|3|4|5|6|7|8|9|10|11 forces 256x256, 256x128, the register-staged
+  // kernel, 224x256, 224x128, or the small-tile kernel at 128x128, 64x64,
+  // 128x256, 64x128, 128x192, 128x96 or 64x96
   // (results are the same up to the fp32 accumulation order inside the
   // matrix cores).
   const GemmPlan plan = plan_gemm(g, ws_bytes);
@@ -1219,6 +1227,10 @@ int launch_gemm(const GemmArgs& g, hipStream_t stream, int64_t ws_bytes) {
     launch_small<OutTag, 64, 128, 4, 4>(g, stream);
   else if (pair_ok && shape == 9)
     launch_small<OutTag, 128, 192, 4, 3>(g, stream);
+  else if (pair_ok && shape == 10)
+    launch_small<OutTag, 128, 96, 4, 4, 4>(g, stream);
+  else if (pair_ok && shape == 11)
+    launch_small<OutTag, 64, 96, 2, 4, 2>(g, stream);
   else
     hipLaunchKernelGGL((fp8_gemm_kernel<OutTag>), grid, dim3(kBlock), 0, stream, g);
   return launch_status("fp8_scaled_mm");

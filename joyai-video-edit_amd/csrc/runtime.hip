@@ -21,7 +21,7 @@ bool knob_value_ok(int knob, int v) {
   switch (knob) {
     case JO_KNOB_QK_SPLIT: return v == 1 || v == 2 || v == 4 || v == 6 || v == 8;
     case JO_KNOB_KV_SPLIT: return v == 1 || v == 2;
-    case JO_KNOB_GEMM_SHAPE: return v >= 0 && v <= 9;
+    case JO_KNOB_GEMM_SHAPE: return v >= 0 && v <= 11;
     case JO_KNOB_GEMM_SPLIT: return v == 1 || v == 2 || v == 4 || v == 8;
     default: return false;
   }

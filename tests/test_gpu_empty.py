@@ -139,7 +139,7 @@ def test_empty_input(dev, case):
         assert tuple(t.shape) == shape and t.dtype == dtype, (tuple(t.shape), t.dtype)
 
 
-@pytest.mark.parametrize("shape", [-1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9])
+@pytest.mark.parametrize("shape", [-1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11])
 @pytest.mark.parametrize("with_bias", [True, False])
 def test_fp8_scaled_mm_zero_k(dev, shape, with_bias):
     """K == 0: the output is the epilogue of a zero accumulator, the bias (or

@@ -18,13 +18,14 @@ from oracle import ops
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["auto", "0", "1", "2", "3", "4", "5", "6", "7", "8", "9"],
+@pytest.fixture(params=["auto", "0", "1", "2", "3", "4", "5", "6", "7", "8", "9", "10", "11"],
                 autouse=True)
 def gemm_shape(request):
     """Every kernel variant: the default choice, 256x256 (8 waves), 256x128
     (4 waves), the register-staged kernel (also the K % 64 != 0 path), 224x256
     (8 waves, 4 and 3 row blocks), 224x128 (4 waves), and the small-tile
-    kernel at 128x128, 64x64, 64x128 and 128x192 (4 waves) and 128x256 (8 waves)."""
+    kernel at 128x128, 64x64, 64x128, 128x192 and 128x96 (4 waves), 128x256
+    (8 waves) and 64x96 (2 waves)."""
     from joyomni_ops import _abi
     value = -1 if request.param == "auto" else int(request.param)
     _abi.call("jo_set_launch_override", _abi.JO_KNOB_GEMM_SHAPE, value)
@@ -143,12 +144,13 @@ def test_fp8_scaled_mm_deployment_shapes_sampled_rows(dev, N, K):
 _TEXT_ORACLE = {}
 
 
-@pytest.mark.parametrize("M,N,K", [(77, 12288, 4096), (256, 4096, 16384), (512, 16384, 4096),
-                                   (1000, 4096, 4096)])
+@pytest.mark.parametrize("M,N,K", [(77, 12288, 4096), (100, 12288, 4096), (200, 12288, 4096),
+                                   (256, 4096, 16384), (512, 16384, 4096), (1000, 4096, 4096)])
 def test_fp8_scaled_mm_text_stream_shapes(dev, M, N, K):
     """The text stream's Fp8Linear shapes (a few hundred prompt tokens against
     the hidden 4096 / MLP 16384 weights), where the automatic choice takes the
-    small-tile kernel (64x64, 128x128 or, at 512 x 16384, 128x256);
+    small-tile kernel (64x64, 128x128, 64x96 and 128x96 on the qkv projection's
+    12288 columns with a ragged last row of tiles, or, at 512 x 16384, 128x256);
     every output against the exact oracle (computed once per shape, reused
     under every launch shape)."""
     import joyomni_ops as jo
