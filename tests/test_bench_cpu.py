@@ -182,3 +182,25 @@ def test_summary_line_fits_the_driver_tail(bench):
         assert n in back["ops"], n
     assert not any(n.startswith("S_") for n in back["ops"])
     assert back["ops"]["G3"]["frac"] == 0.466 and back["ops"]["G3"]["blt_x"] == 1.21
+
+
+def test_gemm_roofline_bound(bench):
+    """A GEMM line is priced against whichever roofline takes longer: the fp8
+    matrix cores for the image stream's shapes and 4096^3, HBM for the text
+    stream's 256 rows (the weight bytes outlast the flops there); the summary
+    entry carries the fraction of that bound."""
+    from joyomni_ops import workloads as W
+    want = {"G1": "mfma", "G2": "mfma", "G3": "mfma", "G4": "mfma", "T_gemm": "mfma",
+            "G5": "hbm", "G6": "hbm"}
+    for n, bound in want.items():
+        cfg = W.CONFIGS[n]
+        nbytes = W.algorithmic_bytes(cfg)
+        r = {"us_per_call": 50.0, "algorithmic_bytes": nbytes,
+             "frac_of_peak": nbytes / 50e-6 / 8e12}
+        bench.gemm_roofline(r, W.algorithmic_flops(cfg))
+        assert r["bound"] == bound, n
+        assert abs(r["tflops"] - W.algorithmic_flops(cfg) / 50e-6 / 1e12) < 0.1
+        e = bench.compact_entry(n, r)
+        frac = r["frac_of_fp8_peak"] if bound == "mfma" else r["frac_of_peak"]
+        assert e["frac"] == round(frac, 3) and e["tflops"] == round(r["tflops"]), (n, e)
+        assert ("frac_of_peak" in r) == (bound == "hbm")
