@@ -549,27 +549,48 @@ struct PairLoads {
   bool last;                      // the wave owns a slot kPerWave - 1 (always when kEven)
 };
 
-template <class OutTag, int BM, int BN, int NW, int MI>
+// NBS: B stages go through a ring of NBS slots beside A's two, so B loads run
+// NBS - 1 stages ahead and A loads one (NBS = 3 for one-round grids, below).
+template <class OutTag, int BM, int BN, int NW, int MI, int NBS>
 __device__ __forceinline__ void fp8_gemm_pair_tile(const GemmArgs& g, uint8_t* smem,
                                                    const PairLoads<BM, BN, NW>& ld, int wave,
                                                    int wm, int wn, int m0, int n0) {
   using Loads = PairLoads<BM, BN, NW>;
   constexpr int WCOLS = BN / (NW / 2);  // wave tile columns
   constexpr int J = WCOLS / 32;         // n-subtiles of 32 per wave
-  constexpr int kSlot = (BM + BN) * kQBK;
+  // Ring layout. NBS = 2: slot t % 2 holds stage t's A rows then its B rows.
+  // NBS = 3: two A slots, then three B slots.
+  constexpr int kASlot = NBS == 2 ? (BM + BN) * kQBK : BM * kQBK;
+  constexpr int kBSlot = NBS == 2 ? (BM + BN) * kQBK : BN * kQBK;
+  constexpr int kBBase = NBS == 2 ? BM * kQBK : 2 * BM * kQBK;
   constexpr int PER = Loads::kPerWave;
+  constexpr int NB = BN / 8 / NW;  // B loads of a wave a stage: the last NB of its slots
   static_assert(J >= 1 && MI >= 2 && MI <= 4, "tile shape");
-  static_assert(128 * (BN * 2 + 16) <= 2 * kSlot, "epilogue staging fits the slots");
+  static_assert((NBS == 2 || NBS == 3) && (BN / 8) % NW == 0, "B ring");
+  static_assert(128 * (BN * 2 + 16) <= (2 * BM + NBS * BN) * kQBK, "epilogue staging fits the rings");
   const int lane = threadIdx.x % kWave;
   const int stages = g.K / kQBK;
-  // Load i of this wave's share of stage s, and all of them.
-  auto issue_one = [&](int s, int i) {
-    if (Loads::kEven || i + 1 < PER || ld.last)
-      __builtin_amdgcn_global_load_lds(ld.base[i] + (ld.off[i] + s * kQBK), (__attribute__((address_space(3))) void*)(smem + (s & 1) * kSlot + (wave + i * NW) * 1024), 16, 0, 0);
+  // Load i of this wave is A (slot index below BM / 8; a wave's A loads come
+  // first in its slot order) or B; stage t of it goes to ring slot t % 2 or
+  // t % NBS.
+  auto is_a = [&](int i) { return wave + i * NW < BM / 8; };
+  auto issue_one = [&](int t, int i) {
+    if (Loads::kEven || i + 1 < PER || ld.last) {
+      if constexpr (NBS == 2)
+        __builtin_amdgcn_global_load_lds(ld.base[i] + (ld.off[i] + t * kQBK), (__attribute__((address_space(3))) void*)(smem + (t & 1) * kASlot + (wave + i * NW) * 1024), 16, 0, 0);
+      else
+        __builtin_amdgcn_global_load_lds(ld.base[i] + (ld.off[i] + t * kQBK), (__attribute__((address_space(3))) void*)(is_a(i) ? smem + (t & 1) * kASlot + (wave + i * NW) * 1024 : smem + kBBase + (t % NBS) * kBSlot + (wave + i * NW - BM / 8) * 1024), 16, 0, 0);
+    }
   };
-  auto issue = [&](int s) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) issue_one(s, i);
+  // The loads issued in stage s's second half: A of stage s + 2 and B of
+  // stage s + NBS.
+  auto issue_batch_one = [&](int s, int i) {
+    if constexpr (NBS == 2)
+      issue_one(s + 2, i);
+    else if (is_a(i))
+      issue_one(s + 2, i);
+    else if (s + NBS < stages)
+      issue_one(s + NBS, i);
   };
 
   f32x16 acc[MI][J];
@@ -592,14 +613,15 @@ __device__ __forceinline__ void fp8_gemm_pair_tile(const GemmArgs& g, uint8_t* s
     for (int h = 0; h < 2; ++h) {
       const int pos = ((k * 4 + fh * 2 + h) ^ q) << 4;
       offa[k][h] = (wm * 128 + fr) * kQBK + pos;
-      offb[k][h] = BM * kQBK + (wn * WCOLS + fr) * kQBK + pos;
+      offb[k][h] = kBBase + (wn * WCOLS + fr) * kQBK + pos;
     }
   auto read_frags = [&](int s, int k, i32x8 (&af)[MI], i32x8 (&bf)[J]) {
-    const uint8_t* st = smem + (s & 1) * kSlot;
+    const uint8_t* st = smem + (s & 1) * kASlot;
+    const uint8_t* sb = NBS == 2 ? st : smem + (s % NBS) * kBSlot;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(st + offb[k][0] + j * 32 * kQBK);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(st + offb[k][1] + j * 32 * kQBK);
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(sb + offb[k][0] + j * 32 * kQBK);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(sb + offb[k][1] + j * 32 * kQBK);
       bf[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     }
 #pragma unroll
@@ -611,7 +633,7 @@ __device__ __forceinline__ void fp8_gemm_pair_tile(const GemmArgs& g, uint8_t* s
   };
   // Fragment f of half k of stage s: B block f (f < J), else A block f - J.
   auto read_one = [&](int s, int k, int f, i32x8 (&af)[MI], i32x8 (&bf)[J]) {
-    const uint8_t* st = smem + (s & 1) * kSlot;
+    const uint8_t* st = (NBS == 2 || f >= J) ? smem + (s & 1) * kASlot : smem + (s % NBS) * kBSlot;
     const int off = f < J ? offb[k][0] + f * 32 * kQBK : offa[k][0] + (f - J) * 32 * kQBK;
     const int off2 = f < J ? offb[k][1] + f * 32 * kQBK : offa[k][1] + (f - J) * 32 * kQBK;
     const u32x4 lo = *reinterpret_cast<const u32x4*>(st + off);
@@ -622,15 +644,15 @@ __device__ __forceinline__ void fp8_gemm_pair_tile(const GemmArgs& g, uint8_t* s
     else
       af[f - J] = v;
   };
-  // Wait for this wave's LDS reads and for all but `later` stages of its
-  // loads (PER instructions a stage; waves without a slot kPerWave - 1 issue
-  // one fewer).
-  auto wait_own = [&](int later) {
+  // Stage s's wait: this wave's LDS reads, and its loads up to stage s + 1's.
+  // A of s + 1 came with the latest loads; with NBS = 3 only their tail, B of
+  // s + 2, may stay in flight.
+  auto wait_next = [&](int s) {
     JO_WAIT_LDS0();
-    if (Loads::kEven || ld.last)
-      wait_loads<PER>(later);
+    if (NBS == 3 && s + 2 < stages)
+      JO_WAIT_VM(NB);
     else
-      wait_loads<PER - 1>(later);
+      JO_WAIT_VM(0);
   };
   auto bare_barrier = [&]() {
     asm volatile("" ::: "memory");
@@ -661,8 +683,7 @@ __device__ __forceinline__ void fp8_gemm_pair_tile(const GemmArgs& g, uint8_t* s
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
     }
     __builtin_amdgcn_sched_barrier(0);
-    // Stage s+1's loads are this wave's only ones in flight.
-    wait_own(0);
+    wait_next(s);
 #pragma unroll
     for (int qi = 0; qi < KB; ++qi) mfma_q(qi, a1, b1);
     __builtin_amdgcn_sched_barrier(0);
@@ -680,7 +701,7 @@ __device__ __forceinline__ void fp8_gemm_pair_tile(const GemmArgs& g, uint8_t* s
       if constexpr (kMore) {
 #pragma unroll
         for (int u = 0; u < 2; ++u)
-          if (2 * t + u < PER) issue_one(s + 2, 2 * t + u);
+          if (2 * t + u < PER) issue_batch_one(s, 2 * t + u);
       }
       if constexpr (kNext) {
         if (t < NF) read_one(s + 1, 0, t, a0, b0);
@@ -693,16 +714,65 @@ __device__ __forceinline__ void fp8_gemm_pair_tile(const GemmArgs& g, uint8_t* s
     }
     if constexpr (kMore) {
 #pragma unroll
-      for (int i = 2 * NQ; i < PER; ++i) issue_one(s + 2, i);
+      for (int i = 2 * NQ; i < PER; ++i) issue_batch_one(s, i);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
 
   using T = std::true_type;
   using F = std::false_type;
-  issue(0);
-  if (stages > 1) issue(1);
-  wait_own(stages > 1 ? 1 : 0);
+  // Prologue: stage 0, then what the second halves of stages -2 and -1 would
+  // have issued (stage 1; with NBS = 3, A of 1 and B of 1 and 2, B before A
+  // within a stage); stage 0 starts once its own loads are in.
+  auto issue_part = [&](int t, bool a) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (is_a(i) == a) issue_one(t, i);
+  };
+  // In flight after stage 0's loads: NB B loads per later B stage and this
+  // wave's A loads of stage 1 (PER - NB; one fewer for a wave without a last
+  // slot, which is always a B slot since every wave has NB of those).
+  const bool full = Loads::kEven || ld.last;
+  if constexpr (NBS == 2) {
+    auto issue = [&](int t) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) issue_one(t, i);
+    };
+    auto wait_own = [&](int later) {
+      JO_WAIT_LDS0();
+      if (Loads::kEven || ld.last)
+        wait_loads<PER>(later);
+      else
+        wait_loads<PER - 1>(later);
+    };
+    issue(0);
+    if (stages > 1) issue(1);
+    wait_own(stages > 1 ? 1 : 0);
+  } else {
+    issue_part(0, false);
+    issue_part(0, true);
+    if (stages >= 3) {
+      issue_part(1, false);
+      issue_part(1, true);
+      issue_part(2, false);
+      JO_WAIT_LDS0();
+      if (full)
+        JO_WAIT_VM(2 * NB + PER - NB);
+      else
+        JO_WAIT_VM(2 * NB + PER - NB - 1);
+    } else if (stages == 2) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) issue_one(1, i);
+      JO_WAIT_LDS0();
+      if (full)
+        JO_WAIT_VM(PER);
+      else
+        JO_WAIT_VM(PER - 1);
+    } else {
+      JO_WAIT_LDS0();
+      JO_WAIT_VM(0);
+    }
+  }
   bare_barrier();
   read_frags(0, 0, a0, b0);
   int s = 0;
@@ -736,11 +806,11 @@ __device__ __forceinline__ void xcd_grouped_tile(int bm, int bn, int& m0, int& n
   n0 = (w / rows) * bn;
 }
 
-template <class OutTag, int BM, int BN, int NW>
+template <class OutTag, int BM, int BN, int NW, int NBS>
 __device__ __forceinline__ void fp8_gemm_pair_body(const GemmArgs& g) {
   using Loads = PairLoads<BM, BN, NW>;
   static_assert(BM == 256 || BM == 224, "tile rows");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * (BM + BN) * kQBK];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[(2 * BM + NBS * BN) * kQBK];
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -767,23 +837,23 @@ __device__ __forceinline__ void fp8_gemm_pair_body(const GemmArgs& g) {
   }
   ld.last = Loads::kEven || wave + (Loads::kPerWave - 1) * NW < Loads::kSlots;
   if constexpr (BM == 256) {
-    fp8_gemm_pair_tile<OutTag, BM, BN, NW, 4>(g, smem, ld, wave, wm, wn, m0, n0);
+    fp8_gemm_pair_tile<OutTag, BM, BN, NW, 4, NBS>(g, smem, ld, wave, wm, wn, m0, n0);
   } else {
     if (wm == 0)
-      fp8_gemm_pair_tile<OutTag, BM, BN, NW, 4>(g, smem, ld, wave, wm, wn, m0, n0);
+      fp8_gemm_pair_tile<OutTag, BM, BN, NW, 4, NBS>(g, smem, ld, wave, wm, wn, m0, n0);
     else
-      fp8_gemm_pair_tile<OutTag, BM, BN, NW, 3>(g, smem, ld, wave, wm, wn, m0, n0);
+      fp8_gemm_pair_tile<OutTag, BM, BN, NW, 3, NBS>(g, smem, ld, wave, wm, wn, m0, n0);
   }
 }
 
-template <class OutTag, int BM, int BN, int NW>
+template <class OutTag, int BM, int BN, int NW, int NBS>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void fp8_gemm_pair_kernel(const GemmArgs g) {
-  fp8_gemm_pair_body<OutTag, BM, BN, NW>(g);
+  fp8_gemm_pair_body<OutTag, BM, BN, NW, NBS>(g);
 }
 
-template <class OutTag, int BM, int BN, int NW>
+template <class OutTag, int BM, int BN, int NW, int NBS = 2>
 void launch_pair(const GemmArgs& g, hipStream_t stream) {
-  hipLaunchKernelGGL((fp8_gemm_pair_kernel<OutTag, BM, BN, NW>),
+  hipLaunchKernelGGL((fp8_gemm_pair_kernel<OutTag, BM, BN, NW, NBS>),
                      dim3((g.N + BN - 1) / BN, (g.M + BM - 1) / BM), dim3(NW * 64), 0, stream, g);
 }
 
@@ -1067,6 +1137,18 @@ int cu_count() {
   return n;
 }
 
+// One workgroup per CU at most (a single round of tiles). There the 224-row
+// pair kernel runs its B loads two stages ahead (NBS = 3): with no second
+// round to overlap, the lines wait longer (~530 cycles against ~360 on the
+// multi-round shapes), and the extra stage of B lookahead measured
+// 3120x4096x16384 178 -> 168 us and 3120x4096x4096 50.6 -> 48.1 us (three
+// alternating runs, results bit-identical); on the multi-round shapes and
+// the 256-row tiles (4096^3) it was 3-4% slower.
+bool one_round(const GemmArgs& g, int bm, int bn) {
+  const int64_t tiles = static_cast<int64_t>((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
+  return tiles <= cu_count();
+}
+
 // Tile rows for the 8-wave x 256-column kernel: one workgroup per CU, so the
 // time is about (rounds of workgroups over the CUs) x (row blocks per SIMD),
 // 8 for a 256-row tile and 7 for a 224-row one. At M = 3120 (13 tiles of 256,
@@ -1209,6 +1291,8 @@ int launch_gemm(const GemmArgs& g, hipStream_t stream, int64_t ws_bytes) {
     launch_pipe<OutTag, 256, 128, 4, 3>(g, stream);
   else if (pair_ok && shape == 0)
     launch_pair<OutTag, 256, 256, 8>(g, stream);
+  else if (pair_ok && shape == 3 && one_round(g, 224, 256))
+    launch_pair<OutTag, 224, 256, 8, 3>(g, stream);
   else if (pair_ok && shape == 3)
     launch_pair<OutTag, 224, 256, 8>(g, stream);
   else if (pipe_ok && shape == 0)
