@@ -69,7 +69,8 @@ SHAPES = [(1, 8, 16), (17, 8, 16), (256, 256, 128), (300, 264, 208), (257, 520, 
           (3120, 512, 4096), (129, 1024, 16384), (64, 2048, 4096),
           (448, 256, 64), (225, 520, 192),   # one K stage; 224-row tiles exact / one row over
           (2900, 4104, 128),   # 221 tiles, ragged in both directions, over the XCD tile groups
-          (300, 264, 256), (257, 520, 384)]   # two and three 128-byte K stages
+          (300, 264, 256), (257, 520, 384),   # two and three 128-byte K stages
+          (700, 1000, 640)]   # five stages, ragged: a one-round grid's three-slot B ring
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
