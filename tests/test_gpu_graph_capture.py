@@ -131,3 +131,51 @@ def test_graph_captured_on_first_use_with_kstage(dev):
         torch.cuda.synchronize()
         for k in want:
             assert torch.equal(as_bits(got[k]), as_bits(want[k])), f"replay {rep}: {k} differs"
+
+
+@pytest.mark.parametrize("M,N,K,shape", [
+    (700, 1000, 640, 3),     # 224-row pair tiles, one round: B three stages in the ring
+    (3120, 5120, 256, 3),    # 224-row pair tiles, 280 of them (two rounds): two slots
+    (64, 4096, 8192, -1),    # few rows, long K: the split-K partials and their reduction
+])
+def test_fp8_scaled_mm_graph_replays_match_eager(dev, M, N, K, shape):
+    """The FP8 GEMM captured into a graph (its split-K workspace taken from the
+    caching allocator during capture), replayed three times with new operands
+    copied into the captured buffers, each replay bit-identical to the eager
+    call on the same operands."""
+    import joyomni_ops as jo
+    from joyomni_ops import _abi
+
+    def operands(seed):
+        g = torch.Generator().manual_seed(seed)
+        a = (torch.randn(M, K, generator=g) * 2).to(torch.float8_e4m3fn)
+        w = (torch.randn(N, K, generator=g) * 2).to(torch.float8_e4m3fn)
+        sa = torch.rand(M, 1, generator=g) + 0.5
+        sb = torch.rand(1, N, generator=g) + 0.5
+        bias = torch.randn(N, generator=g).to(torch.bfloat16)
+        return [t.to(dev) for t in (a, w, sa, sb, bias)]
+
+    _abi.call("jo_set_launch_override", _abi.JO_KNOB_GEMM_SHAPE, shape)
+    try:
+        static = operands(100)
+        jo.fp8_scaled_mm(static[0], static[1].t(), static[2], static[3], torch.bfloat16, static[4])
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = jo.fp8_scaled_mm(static[0], static[1].t(), static[2], static[3],
+                                   torch.bfloat16, static[4])
+        torch.cuda.synchronize()
+        for rep in range(101, 104):
+            fresh = operands(rep)
+            for s_t, f_t in zip(static, fresh):
+                s_t.copy_(f_t)
+            graph.replay()
+            torch.cuda.synchronize()
+            got = out.clone()
+            want = jo.fp8_scaled_mm(fresh[0], fresh[1].t(), fresh[2], fresh[3], torch.bfloat16,
+                                    fresh[4])
+            torch.cuda.synchronize()
+            assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {rep} differs"
+            assert bool(got.float().abs().sum() > 0)
+    finally:
+        _abi.call("jo_set_launch_override", _abi.JO_KNOB_GEMM_SHAPE, -1)
