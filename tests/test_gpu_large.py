@@ -124,3 +124,66 @@ def test_qk_norm_rope_past_2_31_elements(dev):
                                what=f"{name} past 2^31")
     del q, k
     torch.cuda.empty_cache()
+
+
+def test_add_gate_layernorm_modulate_fp8_past_2_31_elements(big):
+    """N3 (gated residual + LN + AdaLN -> FP8) on [1, M, 3072]: the updated
+    residual bit-exact against the oracle's residual_add, the fp8 bytes and
+    scales bit-exact against the quantization of the unfused pair's y (the
+    same kernel family and summation order), y within 1 bf16 ulp."""
+    from joyomni_ops import dit_ops
+    x, _ = big
+    g = torch.Generator(device=x.device).manual_seed(9)
+    res = torch.randn(1, M, N, generator=g, device=x.device, dtype=torch.bfloat16)
+    gate, shift, scale = (0.2 * torch.randn(1, N, generator=g, device=x.device,
+                                            dtype=torch.bfloat16) for _ in range(3))
+    res0 = res.view(M, N)[ROWS].cpu()
+    res_out, q, s = dit_ops.fused_add_gate_layernorm_modulate_fp8(
+        res, x.view(1, M, N), gate, shift, scale)
+    y = dit_ops.fused_layernorm_modulate(res_out, shift, scale)  # the unfused pair's y
+    torch.cuda.synchronize()
+    xr = x[ROWS].cpu()
+    new_res = ops.residual_add(xr, res0, gate.cpu().reshape(1, N))
+    assert torch.equal(res_out.view(M, N)[ROWS].cpu().view(torch.int16),
+                       new_res.view(torch.int16)), "residual differs"
+    y_rows = y.reshape(M, N)[ROWS].cpu()
+    q_ref, s_ref = ops.per_token_quant_fp8(y_rows)
+    assert torch.equal(fp8_rows(q), q_ref), "fp8 bytes differ from quant(unfused y)"
+    assert torch.equal(s[ROWS].cpu().reshape(-1), s_ref), "scales differ"
+    ref = ops.norm_scale_shift_f32(new_res, None, None, scale.cpu().reshape(1, N),
+                                   shift.cpu().reshape(1, N), 0, 1e-6)
+    assert_within_ulp(y_rows, ref, torch.bfloat16, ref.abs().amax(dim=-1, keepdim=True),
+                      what="N3 y past 2^31")
+    del res, res_out, q, s, y
+
+
+def test_fp8_scaled_mm_output_past_2_31_elements(dev):
+    """An FP8 GEMM whose [131584, 16384] bf16 output (4.3 GB) crosses element
+    2^31 (multi-round 224x256 tiles): rows on either side of it against the
+    exact oracle, to the GEMM tests' bar."""
+    import joyomni_ops as jo
+    Mg, Ng, Kg = (1 << 31) // 16384 + 512, 16384, 256
+    edge = (1 << 31) // Ng
+    rows = [0, edge - 1, edge, Mg - 1]
+    g = torch.Generator(device=dev).manual_seed(5)
+    a = (torch.randn(Mg, Kg, generator=g, device=dev) * 2).to(torch.float8_e4m3fn)
+    w = (torch.randn(Ng, Kg, generator=g, device=dev) * 2).to(torch.float8_e4m3fn)
+    sa = torch.rand(Mg, 1, generator=g, device=dev) * 0.02 + 1e-3
+    sb = torch.rand(1, Ng, generator=g, device=dev) * 0.02 + 1e-3
+    bias = torch.randn(Ng, generator=g, device=dev).to(torch.bfloat16)
+    out = jo.fp8_scaled_mm(a, w.t(), sa, sb, torch.bfloat16, bias)
+    torch.cuda.synchronize()
+    assert out.numel() > (1 << 31)
+    ar = a.view(torch.uint8)[rows].cpu().view(torch.float8_e4m3fn)
+    _, acc, mag = ops.fp8_scaled_mm(ar, w.cpu().t(), sa[rows].cpu(), sb.cpu(), torch.bfloat16,
+                                    bias.cpu())
+    ref = acc * sa[rows].cpu().double().reshape(-1, 1) * sb.cpu().double().reshape(1, -1) \
+        + bias.cpu().double().reshape(1, -1)
+    # one bf16 ulp of the exact value (2^(floor(log2|ref|) - 7)) plus the fp32
+    # summation slack of the matrix cores, as in the GEMM's own tests
+    ulp = 2.0 ** (torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -14))) - 7)
+    err = (out[rows].cpu().double() - ref).abs()
+    bad = err > ulp + mag * 2.0 ** -13
+    assert not bool(bad.any()), f"{int(bad.sum())} outputs off"
+    del a, w, out
+    torch.cuda.empty_cache()
